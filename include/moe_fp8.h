@@ -1,0 +1,188 @@
+/*
+ * moe_fp8.h - C ABI of the MI355X (gfx950) FP8-blockwise fused-MoE layer.
+ *
+ * Every entry point takes plain device pointers and sizes, enqueues its work
+ * on the given HIP stream (a hipStream_t passed as void*, NULL = the default
+ * stream) and returns immediately: MOE_OK (0) or a negative status whose
+ * message moe_last_error() returns (thread-local). No entry point allocates
+ * or frees device memory; callers pass outputs and a workspace sized by the
+ * matching *_workspace_bytes function. Functions are re-entrant; calls on
+ * different streams may run concurrently as long as they do not share a
+ * workspace.
+ *
+ * Tensor layouts (row-major, C order):
+ *   x            [T, H]      bf16 hidden states
+ *   router_w     [E, H]      bf16 router weight (the HF / reference parameter,
+ *                            whose transpose the reference passes as [H, E])
+ *   w13          [E, 2I, H]  e4m3fn codes, gate rows [0, I) then up rows [I, 2I)
+ *   w13_scale    [E, 2I/128, H/128]  fp32 block scale (checkpoint weight_scale_inv)
+ *   w2           [E, H, I]   e4m3fn codes
+ *   w2_scale     [E, H/128, I/128]   fp32 block scale
+ *   shared-expert tensors: the same per expert, n_shared experts of intermediate I
+ *
+ * The reference interface each function replaces is cited beside it
+ * (paths inside jinhuang12/vllm-neuron).
+ */
+#ifndef MOE_FP8_H
+#define MOE_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_FP8_ABI_VERSION 1
+
+/* status codes */
+#define MOE_OK 0
+#define MOE_ERR_ARG (-1)         /* bad argument / shape (reference: ValueError)              */
+#define MOE_ERR_UNSUPPORTED (-2) /* valid but unsupported config (reference: NotImplementedError) */
+#define MOE_ERR_HIP (-3)         /* HIP runtime / launch failure (reference: RuntimeError)    */
+
+/* router computation orders (router.py:19-69 RouterComputationOrder, plus grouped) */
+#define MOE_ORDER_TOPK_ACT 0 /* linear -> topk -> act on the k values     (router.py:384-441) */
+#define MOE_ORDER_ACT_TOPK 1 /* linear -> act on all E -> topk (-> renorm) (router.py:444-504) */
+#define MOE_ORDER_GROUPED 2  /* DeepSeek-V3 grouped top-k with selection-only correction bias */
+
+/* router activation (RouterActFnType) */
+#define MOE_SCORING_SOFTMAX 0
+#define MOE_SCORING_SIGMOID 1
+
+int moe_abi_version(void);
+const char* moe_last_error(void);
+
+/* ---- router ------------------------------------------------------------- */
+
+/* logits[T,E] = x[T,H] . router_w[E,H]^T (+ bias[E]); bf16 operands, fp32
+ * accumulation. Replaces the F.linear of router.py:419-424 (and the disabled
+ * nkilib router_topk call, router.py:774-795). H % 64 == 0. */
+size_t moe_router_logits_workspace_bytes(int T, int H, int E);
+int moe_router_logits(const void* x_bf16, const void* router_w_bf16, const float* bias, int T,
+                      int H, int E, float* logits, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Top-k selection + activation (+ renorm, * routed_scale) from fp32 logits.
+ * ids/weights [T,K] in descending key order (ties -> lower expert index);
+ * affinities [T,E] (optional, NULL to skip) is the dense scatter the reference
+ * returns (router.py:437-441). corr_bias [E] (optional) is used by
+ * MOE_ORDER_GROUPED for selection only. renorm != 0 divides by
+ * (sum_k w + renorm_eps). E <= 1024, K <= 64.
+ * Replaces router.py:384-566 and moe_block_tkg.py:165-205. */
+int moe_router_topk(const float* logits, const float* corr_bias, int T, int E, int K, int order,
+                    int scoring, int n_group, int topk_group, int renorm, float renorm_eps,
+                    float routed_scale, int32_t* ids, float* weights, float* affinities,
+                    void* stream);
+
+/* ---- blockwise (align-by-expert) mapping -------------------------------- */
+
+/* N = min(ceil((T*min(K,E) - (E-1)) / B) + E - 1, T*min(K,E))  (moe_blockwise.py:376-382) */
+int moe_num_blocks(int T, int K, int E, int B);
+size_t moe_mapping_workspace_bytes(int T, int E);
+
+/* Builds the reference mapping (moe_blockwise.py:25-157, torch flow :325-437):
+ * token_position_to_id [N*B] (token id or -1), block_to_expert [N],
+ * conditions [N], plus expert_counts [E].
+ * Input is either ids [T,K] (each row distinct experts, -1 = unused slot) or
+ * affinities [T,E] (selected where != 0). With ids, inv_pos [T,K] (optional)
+ * receives the slot of (t, ids[t,k]). With affinities, affinities_masked
+ * [T*E] (optional) receives affinities * padding_mask (padding_mask [T] bytes,
+ * optional, nonzero = real token; moe_blockwise.py:480-498).
+ * Out-of-range ids or more routed pairs than N*B holds are dropped and counted
+ * in the workspace status word (moe_mapping_status). */
+int moe_blockwise_mapping(const int32_t* ids, const float* affinities, const uint8_t* padding_mask,
+                          int T, int K, int E, int B, int N, int32_t* token_position_to_id,
+                          int32_t* block_to_expert, int32_t* conditions, int32_t* expert_counts,
+                          int32_t* inv_pos, float* affinities_masked, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Synchronizes `stream` and returns, in *dropped, the number of routed pairs
+ * the last moe_blockwise_mapping on this workspace had to drop (0 = valid). */
+int moe_mapping_status(const void* workspace, void* stream, int* dropped);
+
+/* inv[T,E] = slot of (t, e) in token_position_to_id, -1 if (t, e) is not
+ * routed. Used when a caller hands moe_cte a mapping built elsewhere
+ * (moe_cte.py:35-94 receives only token_position_to_id / block_to_expert). */
+int moe_invert_mapping(const int32_t* token_position_to_id, const int32_t* block_to_expert, int N,
+                       int B, int T, int E, int32_t* inv, void* stream);
+
+/* ---- fp8 activation quantization --------------------------------------- */
+
+/* Per row, per 128 columns: s = max(amax, 1e-10) / 448, q = RNE_e4m3fn(clamp(x/s, +-448)).
+ * No reference counterpart on a CPU path (closest: the MX activation quantizer
+ * of rmsnorm_router_topk_tkg.py:288-343). cols % 128 == 0. */
+int moe_act_quant_1x128(const void* x_bf16, int rows, int cols, uint8_t* q, float* scales,
+                        void* stream);
+
+/* ---- expert row tiles ---------------------------------------------------- */
+
+/* A tile is {expert, first slot, rows, 0} (int32 x4): at most `mt` consecutive
+ * slots of one block of token_position_to_id; shared experts j < n_shared get
+ * tiles over slots [N*B + j*T, N*B + (j+1)*T) with expert id E + j. */
+int moe_max_tiles(int T, int K, int E, int N, int B, int n_shared, int mt);
+int moe_build_tiles(const int32_t* token_position_to_id, const int32_t* block_to_expert, int N,
+                    int B, int T, int E, int n_shared, int mt, int32_t* tiles, int max_tiles,
+                    int32_t* num_tiles, void* stream);
+
+/* ---- expert GEMMs (fp8 MFMA, 128x128 block scales in the accumulator) ---- */
+
+/* hq[slot, :I] / hs[slot, :I/128] = quant_1x128(SiLU(x W_g^T) * (x W_u^T)) for every
+ * slot of every tile, x rows gathered by token_position_to_id (shared slots map
+ * to token slot - N*B - j*T). hq/hs have N*B + n_shared*T rows.
+ * Replaces the gate_up half of nkilib moe_cte (moe_cte.py:356-421) and of
+ * _torch_moe_impl (moe_cte.py:557-575), SiLU activation. mt in {16,32,64,128}. */
+int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
+                       const uint8_t* w13, const float* w13_scale, const uint8_t* w13_shared,
+                       const float* w13_shared_scale, int n_shared,
+                       const int32_t* token_position_to_id, int NB, const int32_t* tiles,
+                       const int32_t* num_tiles, int max_tiles, int mt, uint8_t* hq, float* hs,
+                       void* stream);
+
+/* y[slot, :H] = bf16(hq[slot] W_d^T) per tile slot (unweighted).
+ * Replaces the down projection of moe_cte (moe_cte.py:585-588). */
+int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int E,
+                    const uint8_t* w2, const float* w2_scale, const uint8_t* w2_shared,
+                    const float* w2_shared_scale, int n_shared, int NB, const int32_t* tiles,
+                    const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
+                    void* stream);
+
+/* ---- weighted unpermute-combine ----------------------------------------- */
+
+/* out[t] = bf16( sum_{s<S, inv[t,s]>=0} w[t,s] * y[inv[t,s]]  +  sum_{j<n_shared} y[NB + j*T + t] ),
+ * fp32 accumulation in s order then j order. POST_SCALE accumulate of
+ * moe_cte.py:603-606 and the scatter-add combine of topk_reduce.py:144-159. */
+int moe_combine(const void* y_bf16, const int32_t* inv, const float* w, int S, int T, int H, int NB,
+                int n_shared, void* out_bf16, void* stream);
+
+/* ---- whole layer --------------------------------------------------------- */
+
+/* router -> top-k -> mapping -> act quant -> gate_up -> down -> combine.
+ * ids/weights/logits outputs are optional (NULL to skip). The layer forward of
+ * the reference MoE block (GptOssExperts.forward, model_bf16.py:1221-1232 ->
+ * forward_prefill :1347-1484 / forward_decode :1309-1345; fused decode
+ * moe_block_tkg.py:306-591) with DeepSeek-style fp8-blockwise experts. */
+size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, int n_shared, int B);
+int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E, int K, int n_shared,
+                      const void* router_w_bf16, const float* router_bias,
+                      const float* corr_bias, int order, int scoring, int n_group,
+                      int topk_group, int renorm, float renorm_eps, float routed_scale,
+                      const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
+                      const float* w2_scale, const uint8_t* w13_shared,
+                      const float* w13_shared_scale, const uint8_t* w2_shared,
+                      const float* w2_shared_scale, int B, void* out_bf16, int32_t* ids_out,
+                      float* weights_out, float* logits_out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* ---- diagnostics ----------------------------------------------------------- */
+
+/* c[16,16] = decode(a[16,128]) . decode(b[16,128])^T through one fp8 MFMA with
+ * the operand/accumulator lane mapping the expert GEMMs use. No reference
+ * counterpart: it pins the gfx950 fp8 MFMA data layout for the tests. */
+int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_FP8_H */

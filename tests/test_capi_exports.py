@@ -1,0 +1,77 @@
+"""The C-ABI library loads and exports every function include/moe_fp8.h declares;
+host-side validation errors map onto the reference's exception types. No GPU needed:
+argument checks run before any HIP call."""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "moe_fp8.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(moe_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_and_binding_agree():
+    from vllm_neuron_amd import _lib
+    names = header_functions()
+    assert len(names) >= 15
+    assert sorted(_lib.PROTOTYPES) == names
+
+
+def test_library_exports_every_declared_symbol():
+    from vllm_neuron_amd import _lib
+    lib = _lib.load()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    assert lib.moe_abi_version() == 1
+
+
+def test_block_formula_and_sizes_match_oracle():
+    from oracle.blockwise import num_blocks
+    from vllm_neuron_amd import _lib
+    lib = _lib.load()
+    for T, K, E, B in [(64, 2, 8, 256), (64, 8, 256, 256), (8192, 8, 256, 256), (1, 8, 384, 256),
+                       (16384, 8, 384, 256), (4096, 8, 160, 256), (5, 1, 6, 1), (3, 4, 2, 7)]:
+        assert lib.moe_num_blocks(T, K, E, B) == num_blocks(T, K, E, B)
+    assert lib.moe_mapping_workspace_bytes(64, 256) > 0
+    assert lib.moe_layer_workspace_bytes(64, 7168, 2048, 256, 8, 1, 256) > 0
+    assert lib.moe_max_tiles(64, 8, 256, 257, 256, 1, 16) >= 64 * 8 // 16
+
+
+def test_argument_errors_raise_reference_exception_types():
+    from vllm_neuron_amd import _lib
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    # E above the selector's capacity -> ValueError (router.py:632-678 raises ValueError)
+    rc = lib.moe_router_topk(p, None, 4, 2048, 2, 0, 0, 1, 1, 0, 0.0, 1.0, p, p, None, None)
+    assert rc == _lib.MOE_ERR_ARG
+    with pytest.raises(ValueError, match="E must be"):
+        _lib.check(rc)
+    # unsupported expert count in the mapping -> NotImplementedError
+    rc = lib.moe_blockwise_mapping(p, None, None, 4, 2, 4096, 256, lib.moe_num_blocks(4, 2, 4096, 256),
+                                   p, p, p, p, None, None, p, 1 << 20, None)
+    assert rc == _lib.MOE_ERR_UNSUPPORTED
+    with pytest.raises(NotImplementedError):
+        _lib.check(rc)
+    # wrong N -> ValueError with the formula value in the message
+    rc = lib.moe_blockwise_mapping(p, None, None, 64, 8, 256, 256, 7, p, p, p, p, None, None, p,
+                                   1 << 20, None)
+    assert rc == _lib.MOE_ERR_ARG and b"257" in lib.moe_last_error()
+    rc = lib.moe_expert_gate_up(p, p, 4, 100, 256, 4, p, p, None, None, 0, p, 0, p, p, 1, 16, p, p, None)
+    assert rc == _lib.MOE_ERR_ARG and b"multiples of 128" in lib.moe_last_error()
+    rc = lib.moe_layer_forward(p, 4, 7168, 2048, 256, 8, 1, p, None, None, 2, 1, 8, 4, 1, 1e-20,
+                               2.5, p, p, p, p, p, p, p, p, 256, p, None, None, None, p, 1, None)
+    assert rc == _lib.MOE_ERR_ARG and b"workspace too small" in lib.moe_last_error()
+
+
+def test_ops_reject_cpu_tensors():
+    import torch
+    from vllm_neuron_amd import ops
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        ops.act_quant(torch.zeros(4, 128, dtype=torch.bfloat16))

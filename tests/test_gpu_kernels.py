@@ -1,0 +1,187 @@
+"""GPU parity of the individual kernels against the oracle (bit-exact for integer,
+index and fp8-code work; tolerances stated where the result is floating point)."""
+import numpy as np
+import pytest
+import torch
+
+from _util import np_f32, np_u8, say
+from oracle import router as R
+from oracle.blockwise import build_blockwise_mapping, mapping_from_ids
+from oracle.fp8 import e4m3fn_decode, quant_act_1x128
+from vllm_neuron_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def test_mfma_fp8_fragment_layout(cuda):
+    """Integer-valued operands: every partial sum is exact, so any lane-layout error
+    (row/column/K mapping, output placement) shows as an exact mismatch."""
+    say("mfma fragment layout")
+    from oracle.fp8 import e4m3fn_encode
+    rng = np.random.default_rng(0)
+    ai = rng.integers(-8, 9, (16, 128)).astype(np.float32)
+    bi = rng.integers(-8, 9, (16, 128)).astype(np.float32)
+    ta = torch.from_numpy(e4m3fn_encode(ai)).view(torch.float8_e4m3fn).to(cuda)
+    tb = torch.from_numpy(e4m3fn_encode(bi)).view(torch.float8_e4m3fn).to(cuda)
+    c = ops.selftest_mfma(ta, tb).cpu().numpy()
+    assert np.array_equal(c, ai @ bi.T)
+
+
+def test_mfma_fp8_wide_range_accumulation(cuda):
+    """Full-range random codes: products are exact, but the MFMA's inner sum is not an
+    exact fp32 sum; it stays within 1e-3 of the largest |product| sum (measured ~1e-4)."""
+    say("mfma wide range")
+    rng = np.random.default_rng(1)
+    finite = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    a = rng.choice(finite, (16, 128)).astype(np.uint8)
+    b = rng.choice(finite, (16, 128)).astype(np.uint8)
+    ta = torch.from_numpy(a).view(torch.float8_e4m3fn).to(cuda)
+    tb = torch.from_numpy(b).view(torch.float8_e4m3fn).to(cuda)
+    c = ops.selftest_mfma(ta, tb).cpu().numpy()
+    da, db = e4m3fn_decode(a).astype(np.float64), e4m3fn_decode(b).astype(np.float64)
+    ref = da @ db.T
+    scale = np.abs(da) @ np.abs(db).T
+    err = np.abs(c - ref) / scale
+    say("mfma wide-range max error / sum|products|", float(err.max()))
+    assert err.max() < 1e-3
+
+
+@pytest.mark.parametrize("R_,C", [(64, 1024), (3, 7168), (1, 128), (257, 5120), (8192, 7168)])
+def test_act_quant_bit_exact(cuda, R_, C):
+    say("act_quant", R_, C)
+    g = torch.Generator().manual_seed(R_ * 7 + C)
+    x = torch.randn(R_, C, generator=g)
+    if R_ > 2:
+        x[0, :128] = 0.0
+        x[1, :256] *= 1e-30          # bf16 subnormal / tiny range
+        x[2, 128:256] *= 1e4
+    xb = x.to(torch.bfloat16)
+    q, s = ops.act_quant(xb.to(cuda))
+    torch.cuda.synchronize()
+    oq, os_ = quant_act_1x128(xb.float().numpy())
+    assert np.array_equal(np_u8(q), oq)
+    assert np.array_equal(np_f32(s), os_)
+
+
+@pytest.mark.parametrize("T,H,E", [(64, 1024, 8), (64, 7168, 256), (300, 5120, 160), (1, 7168, 384)])
+def test_router_logits_close(cuda, T, H, E):
+    say("router_logits", T, H, E)
+    g = torch.Generator().manual_seed(T + H + E)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(E, generator=g) * 0.1
+    lg = ops.router_logits(x.to(cuda), w.to(cuda), bias.to(cuda)).cpu().numpy()
+    ref = R.router_logits(x.float().numpy(), w.float().numpy(), bias.numpy())
+    # bf16 products are exact in fp32; only the fp32 summation order differs
+    assert np.allclose(lg, ref, rtol=1e-5, atol=2e-5)
+
+
+ROUTER_CASES = [
+    # name, E, K, order, scoring, n_group, topk_group, renorm, eps, scale, bias
+    ("softmax_topk_act_c0", 8, 2, 0, 0, 1, 1, False, 0.0, 1.0, False),
+    ("sigmoid_topk_act", 64, 4, 0, 1, 1, 1, False, 0.0, 1.0, False),
+    ("softmax_act_topk_renorm", 128, 6, 1, 0, 1, 1, True, 0.0, 1.0, False),
+    ("sigmoid_act_topk_norm_eps", 256, 8, 1, 1, 1, 1, True, 1e-20, 1.0, False),
+    ("dsv3_grouped", 256, 8, 2, 1, 8, 4, True, 1e-20, 2.5, True),
+    ("kimi_grouped_1group", 384, 8, 2, 1, 1, 1, True, 1e-20, 2.827, True),
+    ("glm_160", 160, 8, 2, 1, 1, 1, True, 1e-20, 2.5, True),
+    ("grouped_softmax", 64, 6, 2, 0, 8, 3, False, 0.0, 1.0, True),
+    ("grouped_1expert_groups", 16, 3, 2, 1, 16, 5, True, 1e-20, 1.0, False),
+]
+
+
+@pytest.mark.parametrize("case", ROUTER_CASES, ids=[c[0] for c in ROUTER_CASES])
+@pytest.mark.parametrize("T", [1, 77, 2048])
+def test_router_topk_bit_exact(cuda, case, T):
+    name, E, K, order, scoring, ng, tg, renorm, eps, scale, use_bias = case
+    say("router_topk", name, T)
+    rng = np.random.default_rng(E * 1000 + T)
+    lg = rng.normal(0, 1.5, (T, E)).astype(np.float32)
+    lg[: T // 4] = np.round(lg[: T // 4] * 2) / 2         # exact ties in a quarter of the rows
+    bias = rng.normal(0, 0.01, E).astype(np.float32) if use_bias else None
+    ids, w, aff = ops.router_topk(torch.from_numpy(lg).to(cuda), K, order, scoring, ng, tg,
+                                  None if bias is None else torch.from_numpy(bias).to(cuda),
+                                  renorm, eps, scale, dense=True)
+    sc = R.SOFTMAX if scoring == 0 else R.SIGMOID
+    if order == 0:
+        oi, ow = R.route_topk_act(lg, K, sc, renorm, eps, scale)
+    elif order == 1:
+        oi, ow = R.route_act_topk_renorm(lg, K, sc, renorm, eps, scale)
+    else:
+        oi, ow = R.route_grouped(lg, bias, K, ng, tg, sc, renorm, eps, scale)
+    assert np.array_equal(ids.cpu().numpy(), oi)
+    assert np.array_equal(w.cpu().numpy(), ow)
+    assert np.array_equal(aff.cpu().numpy(), R.scatter_dense(oi, ow, E))
+
+
+MAP_CASES = [(1, 8, 256, 256), (7, 2, 8, 4), (64, 2, 8, 256), (64, 8, 256, 256), (300, 8, 160, 16),
+             (4096, 8, 160, 256), (8192, 8, 256, 256), (1000, 6, 384, 64), (513, 1, 5, 1)]
+
+
+@pytest.mark.parametrize("T,K,E,B", MAP_CASES)
+def test_mapping_from_ids_bit_exact(cuda, T, K, E, B):
+    say("mapping ids", T, K, E, B)
+    rng = np.random.default_rng(T + K + E + B)
+    p = rng.zipf(1.5, E).astype(np.float64)
+    p[rng.permutation(E)[: E // 10]] = 0                   # ~10% empty experts, skewed rest
+    p = p / p.sum()
+    ids = np.stack([rng.choice(E, K, replace=False, p=p) if (p > 0).sum() >= K else
+                    rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+    m = ops.blockwise_mapping(ids=torch.from_numpy(ids).to(cuda), n_experts=E, block_size=B, check=True)
+    tpid, b2e, cond, counts, inv = mapping_from_ids(ids, E, B)
+    assert np.array_equal(m["token_position_to_id"].cpu().numpy(), tpid)
+    assert np.array_equal(m["block_to_expert"].cpu().numpy(), b2e)
+    assert np.array_equal(m["conditions"].cpu().numpy(), cond)
+    assert np.array_equal(m["expert_counts"].cpu().numpy(), counts)
+    assert np.array_equal(m["inv_pos"].cpu().numpy(), inv)
+
+
+@pytest.mark.parametrize("T,K,E,B", [(64, 2, 8, 256), (300, 8, 160, 16), (2048, 8, 256, 256)])
+def test_mapping_from_affinities_bit_exact(cuda, T, K, E, B):
+    say("mapping affinities", T, K, E, B)
+    rng = np.random.default_rng(T * 3 + E)
+    lg = rng.normal(0, 1, (T, E)).astype(np.float32)
+    ids, w = R.route_topk_act(lg, K, R.SOFTMAX)
+    aff = R.scatter_dense(ids, w, E)
+    pm = np.arange(T) < (T - T // 5)
+    m = ops.blockwise_mapping(affinities=torch.from_numpy(aff).to(cuda), top_k=K, block_size=B,
+                              padding_mask=torch.from_numpy(pm).to(cuda), check=True)
+    am, tpid, b2e, cond = build_blockwise_mapping(aff, E, K, B, padding_mask=pm)
+    assert np.array_equal(m["affinities_masked"].cpu().numpy(), am)
+    assert np.array_equal(m["token_position_to_id"].cpu().numpy(), tpid)
+    assert np.array_equal(m["block_to_expert"].cpu().numpy(), b2e)
+    assert np.array_equal(m["conditions"].cpu().numpy(), cond)
+
+
+def test_mapping_overflow_is_reported(cuda):
+    say("mapping overflow")
+    T, K, E, B = 16, 1, 4, 4
+    aff = np.ones((T, E), np.float32)                     # 4 nonzeros per row but top_k = 1
+    with pytest.raises(IndexError):
+        ops.blockwise_mapping(affinities=torch.from_numpy(aff).to(cuda), top_k=K, block_size=B, check=True)
+
+
+@pytest.mark.parametrize("mt", [16, 32, 64, 128])
+def test_tiles_cover_every_slot_once(cuda, mt):
+    say("tiles", mt)
+    rng = np.random.default_rng(mt)
+    T, K, E, B = 700, 4, 24, 64
+    ids = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+    m = ops.blockwise_mapping(ids=torch.from_numpy(ids).to(cuda), n_experts=E, block_size=B)
+    tiles, num, max_tiles = ops.build_tiles(m["token_position_to_id"], m["block_to_expert"], B, T, K, E, 1, mt)
+    n = int(num.item())
+    tl = tiles[:n].cpu().numpy()
+    tpid = m["token_position_to_id"].cpu().numpy()
+    b2e = m["block_to_expert"].cpu().numpy()
+    NB = tpid.size
+    seen = np.zeros(NB + T, np.int32)
+    for e, s0, rows, _ in tl:
+        assert 1 <= rows <= mt
+        for s in range(s0, s0 + rows):
+            seen[s] += 1
+            if e < E:
+                assert b2e[s // B] == e and s // B == s0 // B
+            else:
+                assert s >= NB
+    assert np.all(seen[:NB][tpid >= 0] == 1) and np.all(seen[NB:] == 1)
+    assert n <= max_tiles

@@ -1,0 +1,166 @@
+// C-ABI glue: error strings, version, and the whole-layer forward that chains
+// the kernels on one stream with a caller-provided workspace.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+static thread_local char g_err[1024] = {0};
+
+void set_error(const char* fn, const char* fmt, ...) {
+  int n = snprintf(g_err, sizeof(g_err), "%s: ", fn);
+  if (n < 0 || n >= (int)sizeof(g_err)) return;
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err + n, sizeof(g_err) - n, fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+// Rows per expert tile: the average routed rows per expert, rounded up to the
+// next supported MFMA tile height.
+static int choose_mt(int T, int K, int E) {
+  long avg = ((long)T * std::min(K, E) + E - 1) / E;
+  if (avg <= 16) return 16;
+  if (avg <= 32) return 32;
+  if (avg <= 64) return 64;
+  return 128;
+}
+
+struct LayerWs {
+  float* logits;
+  void* router_ws;
+  size_t router_ws_bytes;
+  int32_t* ids;
+  float* weights;
+  int32_t* tpid;
+  int32_t* b2e;
+  int32_t* cond;
+  int32_t* counts;
+  int32_t* inv;
+  void* map_ws;
+  size_t map_ws_bytes;
+  uint8_t* xq;
+  float* xs;
+  int32_t* tiles;
+  int32_t* num_tiles;
+  uint8_t* hq;
+  float* hs;
+  uint16_t* y;
+  size_t bytes;
+};
+
+static inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Carves the workspace (base may be null to size it).
+static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, int B) {
+  LayerWs w{};
+  const int N = moe_num_blocks(T, K, E, B);
+  const long NB = (long)N * B;
+  const long P = NB + (long)n_sh * T;
+  const int mt = choose_mt(T, K, E);
+  const int max_tiles = moe_max_tiles(T, K, E, N, B, n_sh, mt);
+  size_t off = 0;
+  auto take = [&](size_t bytes) -> char* {
+    char* p = base ? base + off : nullptr;
+    off += al(bytes);
+    return p;
+  };
+  w.logits = (float*)take((size_t)T * E * 4);
+  w.router_ws_bytes = moe_router_logits_workspace_bytes(T, H, E);
+  w.router_ws = take(w.router_ws_bytes);
+  w.ids = (int32_t*)take((size_t)T * K * 4);
+  w.weights = (float*)take((size_t)T * K * 4);
+  w.tpid = (int32_t*)take((size_t)NB * 4);
+  w.b2e = (int32_t*)take((size_t)N * 4);
+  w.cond = (int32_t*)take((size_t)N * 4);
+  w.counts = (int32_t*)take((size_t)E * 4);
+  w.inv = (int32_t*)take((size_t)T * K * 4);
+  w.map_ws_bytes = moe_mapping_workspace_bytes(T, E);
+  w.map_ws = take(w.map_ws_bytes);
+  w.xq = (uint8_t*)take((size_t)T * H);
+  w.xs = (float*)take((size_t)T * (H / 128) * 4);
+  w.tiles = (int32_t*)take((size_t)max_tiles * 16);
+  w.num_tiles = (int32_t*)take(16);
+  w.hq = (uint8_t*)take((size_t)P * I);
+  w.hs = (float*)take((size_t)P * (I / 128) * 4);
+  w.y = (uint16_t*)take((size_t)P * H * 2);
+  w.bytes = off;
+  return w;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_abi_version(void) { return MOE_FP8_ABI_VERSION; }
+
+extern "C" const char* moe_last_error(void) { return g_err; }
+
+extern "C" size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, int n_shared, int B) {
+  if (T <= 0 || H <= 0 || I <= 0 || E <= 0 || K <= 0 || n_shared < 0 || B <= 0) return 0;
+  return carve(nullptr, T, H, I, E, K, n_shared, B).bytes;
+}
+
+extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E, int K,
+                                 int n_shared, const void* router_w_bf16,
+                                 const float* router_bias, const float* corr_bias, int order,
+                                 int scoring, int n_group, int topk_group, int renorm,
+                                 float renorm_eps, float routed_scale, const uint8_t* w13,
+                                 const float* w13_scale, const uint8_t* w2, const float* w2_scale,
+                                 const uint8_t* w13_shared, const float* w13_shared_scale,
+                                 const uint8_t* w2_shared, const float* w2_shared_scale, int B,
+                                 void* out_bf16, int32_t* ids_out, float* weights_out,
+                                 float* logits_out, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  MOE_API_BEGIN("moe_layer_forward");
+  MOE_CHECK_ARG(x_bf16 && router_w_bf16 && w13 && w13_scale && w2 && w2_scale && out_bf16 && workspace,
+                "null pointer argument");
+  MOE_CHECK_ARG(T > 0 && E > 0 && K > 0 && K <= E && B > 0 && n_shared >= 0,
+                "bad sizes T=%d E=%d K=%d B=%d", T, E, K, B);
+  MOE_CHECK_ARG(H % 256 == 0 && I % 128 == 0, "H must be a multiple of 256 and I of 128");
+  const size_t need = moe_layer_workspace_bytes(T, H, I, E, K, n_shared, B);
+  MOE_CHECK_ARG(workspace_bytes >= need, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  MOE_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
+  LayerWs w = carve((char*)workspace, T, H, I, E, K, n_shared, B);
+  const int N = moe_num_blocks(T, K, E, B);
+  const long NB = (long)N * B;
+  MOE_CHECK_SUPPORTED(NB + (long)n_shared * T < (1L << 31), "too many slots");
+  const int mt = choose_mt(T, K, E);
+  const int max_tiles = moe_max_tiles(T, K, E, N, B, n_shared, mt);
+  float* logits = logits_out ? logits_out : w.logits;
+  int32_t* ids = ids_out ? ids_out : w.ids;
+  float* wts = weights_out ? weights_out : w.weights;
+
+  char saved[1024];
+  int rc;
+#define MOE_STEP(call)                                         \
+  rc = (call);                                                 \
+  if (rc != MOE_OK) {                                          \
+    snprintf(saved, sizeof(saved), "%s", moe_last_error());    \
+    moe::set_error(_moe_fn, "%s", saved);                      \
+    return rc;                                                 \
+  }
+  MOE_STEP(moe_router_logits(x_bf16, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+                             w.router_ws_bytes, stream));
+  MOE_STEP(moe_router_topk(logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
+                           renorm_eps, routed_scale, ids, wts, nullptr, stream));
+  MOE_STEP(moe_blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond,
+                                 w.counts, w.inv, nullptr, w.map_ws, w.map_ws_bytes, stream));
+  MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
+  MOE_STEP(moe_build_tiles(w.tpid, w.b2e, N, B, T, E, n_shared, mt, w.tiles, max_tiles,
+                           w.num_tiles, stream));
+  MOE_STEP(moe_expert_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
+                              w13_shared_scale, n_shared, w.tpid, (int)NB, w.tiles, w.num_tiles,
+                              max_tiles, mt, w.hq, w.hs, stream));
+  MOE_STEP(moe_expert_down(w.hq, w.hs, T, H, I, E, w2, w2_scale, w2_shared, w2_shared_scale,
+                           n_shared, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y, stream));
+  MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)NB, n_shared, out_bf16, stream));
+#undef MOE_STEP
+  return MOE_OK;
+}

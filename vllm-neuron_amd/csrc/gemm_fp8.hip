@@ -1,0 +1,395 @@
+// FP8-blockwise grouped expert GEMMs for gfx950 (OCP e4m3fn MFMA).
+//
+//   gate_up: h = quant_1x128( SiLU(x W_g^T) * (x W_u^T) )   per routed slot
+//   down   : y = bf16( h W_d^T )                              per routed slot
+//
+// Reference: the blockwise expert MLP of nkilib moe_cte called at
+// vllm_neuron/functional/moe/moe_cte.py:356-421, whose CPU fallback
+// _torch_moe_impl (moe_cte.py:465-612) defines the math: gate/up projections
+// (:557-559), SiLU(gate) * up (:574-575), down projection (:585-588). The fp8
+// 128x128 block-scale dequantization is DeepSeek-V3's checkpoint format.
+//
+// Work decomposition: a work item is (row tile, N tile). A row tile holds up
+// to MT consecutive slots of one expert (moe_build_tiles). Each workgroup
+// (4 waves) owns 256 weight rows: for gate_up, 128 gate rows and the matching
+// 128 up rows (so one workgroup sees a whole 128-column quantization group of
+// h); for down, 256 output columns. Wave w owns four 16-row MFMA column tiles.
+//
+// K loop: one v_mfma_f32_16x16x128_f8f6f4 per 128-wide K block (exactly one
+// scale block), accumulated in fp32 as acc += mfma(a, b) * (s_a[row] * s_w).
+// Activation rows are gathered into LDS (double buffered); weight fragments
+// stream from HBM straight into registers with a PD-deep prefetch ring, as
+// each weight byte is used by exactly one lane.
+//
+// Operand lane layout: lane l supplies row l%16 and the 32 bytes
+// [(l/16)*16, +16) and [64 + (l/16)*16, +16) of the K block. A and B use the
+// same mapping, so the hardware's K order inside the block does not matter.
+// Accumulator layout: lane l, register i holds D[4*(l/16) + i][l%16].
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+struct GemmArgs {
+  const uint8_t* a;   // xq [T, H] (gate_up) or hq [rows, I] (down)
+  const float* as;    // activation scales [rows, K/128]
+  const uint8_t* w;   // routed weights
+  const float* ws;    // routed weight scales
+  const uint8_t* wsh;  // shared-expert weights
+  const float* wssh;   // shared-expert weight scales
+  const int32_t* tpid;
+  const int4* tiles;
+  const int32_t* num_tiles;
+  uint8_t* hq;
+  float* hs;
+  uint16_t* y;
+  int T, H, I, E, nsh;
+  long NB;
+};
+
+__device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b) {
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+  // format codes 0/0 = e4m3 x e4m3; zero scale operands select the unscaled instruction
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ v8i load_frag_global(const uint8_t* p) {
+  int4 lo = *(const int4*)p;
+  int4 hi = *(const int4*)(p + 64);
+  return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+}
+
+__device__ __forceinline__ v8i load_frag_lds(const uint8_t* p) {
+  int4 lo = *(const int4*)p;
+  int4 hi = *(const int4*)(p + 64);
+  return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+}
+
+template <int MT, int KIND, int PD>
+__global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
+  constexpr int MS = MT / 16;
+  constexpr int ACH = MT * 8;                 // 16-byte chunks per A tile per K block
+  constexpr int APT = (ACH + 255) / 256;      // chunks per thread
+  constexpr int LDA = 128 + 16;               // padded LDS row (bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t sA[2][MT * LDA];
+  __shared__ __attribute__((aligned(16))) float sAs[2][MT];
+  __shared__ long sSrc[MT];
+  __shared__ float sRed[4][MT];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int Kdim = (KIND == 0) ? p.H : p.I;
+  const int KB = Kdim / MOE_GROUP;
+  const int NT = (KIND == 0) ? p.I / 128 : p.H / 256;
+  const int total = p.num_tiles[0] * NT;
+
+  for (int wi = blockIdx.x; wi < total; wi += gridDim.x) {
+    const int tile = wi / NT, nt = wi - tile * NT;
+    const int4 td = p.tiles[tile];
+    const int e = td.x, nrows = td.z;
+    const long slot0 = td.y;
+    if (e < 0 || e >= p.E + p.nsh) continue;  // workgroup-uniform: malformed tile
+    const bool is_sh = e >= p.E;
+    const int ej = is_sh ? e - p.E : e;
+
+    if (tid < MT) {
+      long src = -1;
+      if (tid < nrows) {
+        const long slot = slot0 + tid;
+        if (KIND == 0) {
+          src = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
+          if (src >= p.T) src = -1;  // token ids outside [0, T) are treated as padding
+        } else {
+          src = slot;
+        }
+      }
+      sSrc[tid] = src;
+    }
+    __syncthreads();
+
+    // activation chunk sources
+    const uint8_t* aptr[APT];
+    int aoff[APT];
+#pragma unroll
+    for (int c = 0; c < APT; ++c) {
+      const int chunk = tid + 256 * c;
+      aptr[c] = nullptr;
+      aoff[c] = -1;
+      if (chunk < ACH) {
+        const int row = chunk >> 3, col = (chunk & 7) * 16;
+        aoff[c] = row * LDA + col;
+        const long src = sSrc[row];
+        if (src >= 0) aptr[c] = p.a + (size_t)src * Kdim + col;
+      }
+    }
+    const float* asp = nullptr;
+    if (tid < MT && sSrc[tid] >= 0) asp = p.as + (size_t)sSrc[tid] * KB;
+
+    // weight fragments and scale rows
+    const uint8_t* wb;
+    const float* wsb;
+    if (KIND == 0) {
+      wb = (is_sh ? p.wsh : p.w) + (size_t)ej * 2 * p.I * p.H;
+      wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (2 * p.I / 128) * KB;
+    } else {
+      wb = (is_sh ? p.wsh : p.w) + (size_t)ej * p.H * p.I;
+      wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (p.H / 128) * KB;
+    }
+    const uint8_t* bp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int row;
+      if (KIND == 0)
+        row = (j < 2) ? nt * 128 + wave * 32 + j * 16 + r16
+                      : p.I + nt * 128 + wave * 32 + (j - 2) * 16 + r16;
+      else
+        row = nt * 256 + wave * 64 + j * 16 + r16;
+      bp[j] = wb + (size_t)row * Kdim + g * 16;
+    }
+    const float* sw0 = (KIND == 0) ? wsb + (size_t)nt * KB : wsb + (size_t)(nt * 2 + (wave >> 1)) * KB;
+    const float* sw1 = (KIND == 0) ? wsb + (size_t)(p.I / 128 + nt) * KB : sw0;
+
+    v8i bq[PD][4];
+    int4 aq[PD][APT];
+    float asq[PD];
+    float swq[PD][2];
+
+    auto load_stage = [&](int slot, int kb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bq[slot][j] = load_frag_global(bp[j] + (size_t)kb * MOE_GROUP);
+#pragma unroll
+      for (int c = 0; c < APT; ++c)
+        aq[slot][c] = aptr[c] ? *(const int4*)(aptr[c] + (size_t)kb * MOE_GROUP) : make_int4(0, 0, 0, 0);
+      asq[slot] = asp ? asp[kb] : 0.f;
+      swq[slot][0] = sw0[kb];
+      swq[slot][1] = sw1[kb];
+    };
+    auto store_A = [&](int buf, int slot) {
+#pragma unroll
+      for (int c = 0; c < APT; ++c)
+        if (aoff[c] >= 0) *(int4*)&sA[buf][aoff[c]] = aq[slot][c];
+      if (tid < MT) sAs[buf][tid] = asq[slot];
+    };
+
+    v4f acc[MS][4];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[ms][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int s = 0; s < PD - 1; ++s)
+      if (s < KB) load_stage(s, s);
+    store_A(0, 0);
+    __syncthreads();
+
+    for (int kb0 = 0; kb0 < KB; kb0 += PD) {
+#pragma unroll
+      for (int s = 0; s < PD; ++s) {
+        const int kb = kb0 + s;
+        if (kb < KB) {
+          if (kb + PD - 1 < KB) load_stage((s + PD - 1) % PD, kb + PD - 1);
+          const int buf = kb & 1;
+#pragma unroll
+          for (int ms = 0; ms < MS; ++ms) {
+            const v8i a = load_frag_lds(&sA[buf][(ms * 16 + r16) * LDA + g * 16]);
+            const v4f sa = *(const v4f*)&sAs[buf][ms * 16 + 4 * g];
+            const v4f c0 = sa * swq[s][0];
+            const v4f c1 = sa * swq[s][1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const v4f part = mfma_fp8(a, bq[s][j]);
+              acc[ms][j] += part * ((KIND == 0 && j >= 2) ? c1 : c0);
+            }
+          }
+          if (kb + 1 < KB) store_A((kb + 1) & 1, (s + 1) % PD);
+          __syncthreads();
+        }
+      }
+    }
+
+    if (KIND == 0) {
+      // h = SiLU(gate) * up, written over the gate accumulators.
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float m = 0.f;
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const float gt = acc[ms][jj][i], up = acc[ms][jj + 2][i];
+            const float h = gt / (1.0f + __expf(-gt)) * up;
+            acc[ms][jj][i] = h;
+            m = fmaxf(m, fabsf(h));
+          }
+          m = group16_max_f32(m);
+          if (r16 == 0) sRed[wave][ms * 16 + 4 * g + i] = m;
+        }
+      }
+      __syncthreads();
+      const int GI = p.I / MOE_GROUP;
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = ms * 16 + 4 * g + i;
+          const float amax = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), fmaxf(sRed[2][row], sRed[3][row]));
+          const float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
+          if (sSrc[row] >= 0) {
+            const long slot = slot0 + row;
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+              const int col = nt * 128 + wave * 32 + jj * 16 + r16;
+              const float yv = fminf(fmaxf(acc[ms][jj][i] / sc, -448.0f), 448.0f);
+              p.hq[(size_t)slot * p.I + col] = (uint8_t)f32_to_e4m3fn(yv);
+            }
+            if (wave == 0 && r16 == 0) p.hs[(size_t)slot * GI + nt] = sc;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = ms * 16 + 4 * g + i;
+          if (row < nrows) {
+            const long slot = slot0 + row;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int col = nt * 256 + wave * 64 + j * 16 + r16;
+              p.y[(size_t)slot * p.H + col] = f32_to_bf16_bits(acc[ms][j][i]);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Single-wave check of the fragment mapping above: c[16,16] = a[16,128] . b[16,128]^T.
+__global__ void selftest_mfma_kernel(const uint8_t* a, const uint8_t* b, float* c) {
+  const int lane = threadIdx.x, g = lane >> 4, r16 = lane & 15;
+  const v8i fa = load_frag_global(a + r16 * 128 + g * 16);
+  const v8i fb = load_frag_global(b + r16 * 128 + g * 16);
+  const v4f d = mfma_fp8(fa, fb);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[(4 * g + i) * 16 + r16] = d[i];
+}
+
+template <int KIND>
+static int launch_gemm(const GemmArgs& a, int max_tiles, int mt, hipStream_t st) {
+  const int NT = (KIND == 0) ? a.I / 128 : a.H / 256;
+  const long items = (long)max_tiles * NT;
+  const int grid = (int)std::max(1L, std::min(items, 4096L));
+  switch (mt) {
+    case 16:
+      hipLaunchKernelGGL((expert_gemm_kernel<16, KIND, 3>), dim3(grid), dim3(256), 0, st, a);
+      break;
+    case 32:
+      hipLaunchKernelGGL((expert_gemm_kernel<32, KIND, 3>), dim3(grid), dim3(256), 0, st, a);
+      break;
+    case 64:
+      hipLaunchKernelGGL((expert_gemm_kernel<64, KIND, 2>), dim3(grid), dim3(256), 0, st, a);
+      break;
+    case 128:
+      hipLaunchKernelGGL((expert_gemm_kernel<128, KIND, 2>), dim3(grid), dim3(256), 0, st, a);
+      break;
+    default:
+      return MOE_ERR_ARG;
+  }
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+#define MOE_CHECK_ALIGN16(ptr) \
+  MOE_CHECK_ARG(((uintptr_t)(ptr)&15) == 0, "%s must be 16-byte aligned", #ptr)
+
+extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
+                                  const uint8_t* w13, const float* w13_scale,
+                                  const uint8_t* w13_shared, const float* w13_shared_scale,
+                                  int n_shared, const int32_t* token_position_to_id, int NB,
+                                  const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                                  int mt, uint8_t* hq, float* hs, void* stream) {
+  MOE_API_BEGIN("moe_expert_gate_up");
+  MOE_CHECK_ARG(xq && xs && w13 && w13_scale && token_position_to_id && tiles && num_tiles && hq && hs,
+                "null pointer argument");
+  MOE_CHECK_ARG(T > 0 && E > 0 && NB >= 0 && max_tiles > 0, "bad sizes");
+  MOE_CHECK_ARG(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0,
+                "H and I must be positive multiples of 128 (H=%d I=%d)", H, I);
+  MOE_CHECK_ARG(n_shared == 0 || (w13_shared && w13_shared_scale), "shared weights missing");
+  MOE_CHECK_ARG(mt == 16 || mt == 32 || mt == 64 || mt == 128, "mt must be 16/32/64/128");
+  MOE_CHECK_ALIGN16(xq);
+  MOE_CHECK_ALIGN16(w13);
+  MOE_CHECK_ARG(n_shared == 0 || ((uintptr_t)w13_shared & 15) == 0, "w13_shared misaligned");
+  GemmArgs a{};
+  a.a = xq;
+  a.as = xs;
+  a.w = w13;
+  a.ws = w13_scale;
+  a.wsh = w13_shared;
+  a.wssh = w13_shared_scale;
+  a.tpid = token_position_to_id;
+  a.tiles = (const int4*)tiles;
+  a.num_tiles = num_tiles;
+  a.hq = hq;
+  a.hs = hs;
+  a.T = T;
+  a.H = H;
+  a.I = I;
+  a.E = E;
+  a.nsh = n_shared;
+  a.NB = NB;
+  if (launch_gemm<0>(a, max_tiles, mt, (hipStream_t)stream) != MOE_OK)
+    MOE_CHECK_ARG(false, "bad mt %d", mt);
+  MOE_API_END();
+}
+
+extern "C" int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int E,
+                               const uint8_t* w2, const float* w2_scale, const uint8_t* w2_shared,
+                               const float* w2_shared_scale, int n_shared, int NB,
+                               const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                               int mt, void* y_bf16, void* stream) {
+  MOE_API_BEGIN("moe_expert_down");
+  MOE_CHECK_ARG(hq && hs && w2 && w2_scale && tiles && num_tiles && y_bf16, "null pointer argument");
+  MOE_CHECK_ARG(T > 0 && E > 0 && NB >= 0 && max_tiles > 0, "bad sizes");
+  MOE_CHECK_ARG(H > 0 && H % 256 == 0 && I > 0 && I % 128 == 0,
+                "H must be a multiple of 256 and I of 128 (H=%d I=%d)", H, I);
+  MOE_CHECK_ARG(n_shared == 0 || (w2_shared && w2_shared_scale), "shared weights missing");
+  MOE_CHECK_ARG(mt == 16 || mt == 32 || mt == 64 || mt == 128, "mt must be 16/32/64/128");
+  MOE_CHECK_ALIGN16(hq);
+  MOE_CHECK_ALIGN16(w2);
+  MOE_CHECK_ARG(n_shared == 0 || ((uintptr_t)w2_shared & 15) == 0, "w2_shared misaligned");
+  GemmArgs a{};
+  a.a = hq;
+  a.as = hs;
+  a.w = w2;
+  a.ws = w2_scale;
+  a.wsh = w2_shared;
+  a.wssh = w2_shared_scale;
+  a.tiles = (const int4*)tiles;
+  a.num_tiles = num_tiles;
+  a.y = (uint16_t*)y_bf16;
+  a.T = T;
+  a.H = H;
+  a.I = I;
+  a.E = E;
+  a.nsh = n_shared;
+  a.NB = NB;
+  if (launch_gemm<1>(a, max_tiles, mt, (hipStream_t)stream) != MOE_OK)
+    MOE_CHECK_ARG(false, "bad mt %d", mt);
+  MOE_API_END();
+}
+
+extern "C" int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, void* stream) {
+  MOE_API_BEGIN("moe_selftest_mfma_fp8");
+  MOE_CHECK_ARG(a && b && c, "null pointer argument");
+  MOE_CHECK_ALIGN16(a);
+  MOE_CHECK_ALIGN16(b);
+  hipLaunchKernelGGL(selftest_mfma_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, a, b, c);
+  MOE_API_END();
+}

@@ -1,0 +1,95 @@
+// Device helpers shared by the FP8-blockwise MoE kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+#define MOE_WAVE 64
+#define MOE_GROUP 128  // quantization group along K (weights 128x128, activations 1x128)
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// OCP float8 e4m3fn encode, round-to-nearest-even. The caller clamps the input
+// to [-448, 448] first (max finite e4m3fn), so no NaN/overflow path is needed.
+// Normal range: keep the fp32 exponent, round the 23-bit mantissa to 3 bits;
+// a mantissa carry propagates into the exponent field by the integer add.
+// Subnormal range (|x| < 2^-6): code = rint(|x| * 2^9), 0..8 (8 == min normal).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  uint32_t code;
+  if (a < 0x3c800000u) {                       // |x| < 2^-6
+    code = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  } else {
+    uint32_t exp = (a >> 23) - 120u;           // (e - 127) + 7
+    uint32_t mant = a & 0x7fffffu;
+    uint32_t lsb = (mant >> 20) & 1u;
+    uint32_t m3 = (mant + 0x7ffffu + lsb) >> 20;  // 0..8
+    code = (exp << 3) + m3;
+  }
+  return code | sign;
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic fp32 exp / sigmoid built from individually rounded IEEE ops
+// (no contraction), so the host oracle reproduces them bit for bit:
+// Cody-Waite reduction with C1 = 355/512 (exact), degree-7 Taylor (Horner),
+// scale by 2^n. Argument clamped to [-80, 80] (no subnormal intermediates).
+// ---------------------------------------------------------------------------
+__device__ __attribute__((noinline)) float det_exp_f32(float x) {
+#pragma clang fp contract(off)
+  x = fminf(fmaxf(x, -80.0f), 80.0f);
+  float n = __builtin_rintf(x * 0x1.715476p+0f);          // log2(e)
+  float r = (x - n * 0x1.63p-1f) - n * -0x1.bd0106p-13f;  // ln2 = C1 + C2, C1 = 355/512
+  float p = 0x1.a01a02p-13f;                               // 1/5040
+  p = p * r + 0x1.6c16c2p-10f;                             // 1/720
+  p = p * r + 0x1.111112p-7f;                              // 1/120
+  p = p * r + 0x1.555556p-5f;                              // 1/24
+  p = p * r + 0x1.555556p-3f;                              // 1/6
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  return __builtin_ldexpf(p, (int)n);
+}
+
+__device__ __forceinline__ float det_sigmoid_f32(float x) {
+#pragma clang fp contract(off)
+  float e = det_exp_f32(-x);
+  return 1.0f / (1.0f + e);
+}
+
+// ---------------------------------------------------------------------------
+// Wave reductions (wave64).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MOE_WAVE));
+  return v;
+}
+
+// Reduction across the 16 lanes that share lane/16 (one MFMA output row group).
+__device__ __forceinline__ float group16_max_f32(float v) {
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MOE_WAVE));
+  return v;
+}

@@ -1,0 +1,119 @@
+// 1x128 fp8 activation quantization and the weighted unpermute-combine.
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+// One wave per (row, 128-column group): lane l holds columns 2l, 2l+1.
+// s = max(amax, 1e-10) / 448 and q = RNE_e4m3fn(clamp(x / s, +-448)), both IEEE
+// fp32 divisions, so codes and scales match the oracle bit for bit.
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int rows,
+                                                        int cols, uint8_t* __restrict__ q,
+                                                        float* __restrict__ s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = cols / MOE_GROUP;
+  const long total = (long)rows * G;
+  for (long gi = (long)blockIdx.x * 4 + wave; gi < total; gi += (long)gridDim.x * 4) {
+    const long r = gi / G;
+    const int g = (int)(gi - r * G);
+    const size_t off = (size_t)r * cols + (size_t)g * MOE_GROUP + 2 * lane;
+    uint32_t pair = *(const uint32_t*)(x + off);
+    float v0 = bf16_bits_to_f32((uint16_t)(pair & 0xffffu));
+    float v1 = bf16_bits_to_f32((uint16_t)(pair >> 16));
+    float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
+    float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
+    float y0 = fminf(fmaxf(v0 / sc, -448.0f), 448.0f);
+    float y1 = fminf(fmaxf(v1 / sc, -448.0f), 448.0f);
+    uint32_t c = f32_to_e4m3fn(y0) | (f32_to_e4m3fn(y1) << 8);
+    *(uint16_t*)(q + off) = (uint16_t)c;
+    if (lane == 0) s[r * G + g] = sc;
+  }
+}
+
+// out[t] = sum_s w[t,s] * y[inv[t,s]] (inv >= 0) + sum_j y[NB + j*T + t], fp32 accumulation,
+// one workgroup per token, 8 bf16 (16 B) per thread per step.
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
+                                                      const int32_t* __restrict__ inv,
+                                                      const float* __restrict__ w, int S, int T,
+                                                      int H, long NB, int n_shared,
+                                                      uint16_t* __restrict__ out) {
+  __shared__ long s_row[1024 + 16];
+  __shared__ float s_w[1024 + 16];
+  __shared__ int s_n;
+  const int t = blockIdx.x;
+  if (threadIdx.x == 0) {
+    int n = 0;
+    for (int s = 0; s < S; ++s) {
+      int p = inv[(size_t)t * S + s];
+      if (p >= 0) {
+        s_row[n] = p;
+        s_w[n] = (w != nullptr) ? w[(size_t)t * S + s] : 1.f;
+        ++n;
+      }
+    }
+    for (int j = 0; j < n_shared; ++j) {
+      s_row[n] = NB + (long)j * T + t;
+      s_w[n] = 1.f;
+      ++n;
+    }
+    s_n = n;
+  }
+  __syncthreads();
+  const int n = s_n;
+  for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    for (int r = 0; r < n; ++r) {
+      const float wt = s_w[r];
+      int4 v = *(const int4*)(y + (size_t)s_row[r] * H + c * 8);
+      const uint32_t u[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += wt * bf16_bits_to_f32((uint16_t)(u[i] & 0xffffu));
+        acc[2 * i + 1] += wt * bf16_bits_to_f32((uint16_t)(u[i] >> 16));
+      }
+    }
+    int4 o;
+    o.x = (int)(f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16));
+    o.y = (int)(f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16));
+    o.z = (int)(f32_to_bf16_bits(acc[4]) | ((uint32_t)f32_to_bf16_bits(acc[5]) << 16));
+    o.w = (int)(f32_to_bf16_bits(acc[6]) | ((uint32_t)f32_to_bf16_bits(acc[7]) << 16));
+    *(int4*)(out + (size_t)t * H + c * 8) = o;
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_act_quant_1x128(const void* x_bf16, int rows, int cols, uint8_t* q,
+                                   float* scales, void* stream) {
+  MOE_API_BEGIN("moe_act_quant_1x128");
+  MOE_CHECK_ARG(x_bf16 && q && scales, "null pointer argument");
+  MOE_CHECK_ARG(rows >= 0 && cols > 0 && cols % MOE_GROUP == 0,
+                "cols must be a positive multiple of 128, got %d", cols);
+  MOE_CHECK_ARG(((uintptr_t)x_bf16 & 3) == 0 && ((uintptr_t)q & 1) == 0, "misaligned x or q");
+  if (rows == 0) return MOE_OK;
+  long groups = (long)rows * (cols / MOE_GROUP);
+  int grid = (int)std::min<long>((groups + 3) / 4, 8192);
+  hipLaunchKernelGGL(act_quant_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, rows, cols, q, scales);
+  MOE_API_END();
+}
+
+extern "C" int moe_combine(const void* y_bf16, const int32_t* inv, const float* w, int S, int T,
+                           int H, int NB, int n_shared, void* out_bf16, void* stream) {
+  MOE_API_BEGIN("moe_combine");
+  MOE_CHECK_ARG(y_bf16 && out_bf16 && (inv || S == 0), "null pointer argument");
+  MOE_CHECK_ARG(T >= 0 && H > 0 && H % 8 == 0 && S >= 0 && S <= 1024 && n_shared >= 0 &&
+                    n_shared <= 16 && NB >= 0,
+                "bad sizes T=%d H=%d S=%d n_shared=%d", T, H, S, n_shared);
+  MOE_CHECK_ARG(((uintptr_t)y_bf16 & 15) == 0 && ((uintptr_t)out_bf16 & 15) == 0,
+                "y and out must be 16-byte aligned");
+  if (T == 0) return MOE_OK;
+  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)y_bf16, inv, w, S, T, H, (long)NB, n_shared,
+                     (uint16_t*)out_bf16);
+  MOE_API_END();
+}

@@ -1,0 +1,379 @@
+// Router kernels for gfx950: logits GEMM (bf16 MFMA, fp32 accumulate) and the
+// per-token top-k selector (one wave per token, wave shuffles for the argmax).
+//
+// Reference behaviour: vllm_neuron/functional/moe/router.py:384-566 (torch
+// fallback orders), moe_block_tkg.py:153-205 (router_pre_norm / norm_topk_prob),
+// plus DeepSeek-V3 grouped sigmoid routing with a selection-only correction bias.
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+// ---------------------------------------------------------------------------
+// logits[t, e] = sum_h x[t, h] * w[e, h]   (bf16 operands, fp32 accumulation)
+//
+// Workgroup tile: 64 tokens x 64 experts, 4 waves; wave w owns experts
+// [16w, 16w + 16) for all 64 tokens (4 MFMA row tiles). K advances 64 per step
+// (two v_mfma_f32_16x16x32_bf16). The x tile goes through LDS (shared by the
+// four waves); each wave streams its 16 router rows straight into registers.
+// Operand lane layout: lane l holds row l%16 and the 8 K-values
+// [s*32 + (l/16)*8, +8) of sub-step s; A and B use the same mapping, so the
+// MFMA forms the full 32-long dot product per sub-step.
+// blockIdx.z splits K; with more than one split the kernel writes fp32
+// partials [ksplit, T, E] that router_logits_reduce sums in split order.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void router_logits_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const float* __restrict__ bias, int T, int H, int E, int kchunk,
+    float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint16_t sx[64][64 + 8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+  const int k_begin = blockIdx.z * kchunk;
+  const int k_end = min(H, k_begin + kchunk);
+  const int g = lane >> 4, r16 = lane & 15;
+
+  int erow = e0 + wave * 16 + r16;
+  const bool erow_ok = erow < E;
+  if (!erow_ok) erow = E - 1;
+  const uint16_t* wrow = w + (size_t)erow * H;
+
+  v4f acc[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) acc[m] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  // x tile load: 64 rows x 64 bf16 = 512 chunks of 16 B, 2 per thread.
+  for (int k0 = k_begin; k0 < k_end; k0 += 64) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      int idx = threadIdx.x + c * 256;
+      int row = idx >> 3, col = (idx & 7) * 8;
+      int4 v = {0, 0, 0, 0};
+      if (t0 + row < T) v = *(const int4*)(x + (size_t)(t0 + row) * H + k0 + col);
+      *(int4*)&sx[row][col] = v;
+    }
+    v8bf b[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) b[s] = *(const v8bf*)(wrow + k0 + s * 32 + g * 8);
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        v8bf a = *(const v8bf*)&sx[m * 16 + r16][s * 32 + g * 8];
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[s], acc[m], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // C layout: lane l, register i -> row 4*(l/16)+i of the 16-row tile, column l%16.
+  if (!erow_ok) return;
+  const int e = e0 + wave * 16 + r16;
+  float bv = (bias != nullptr && gridDim.z == 1) ? bias[e] : 0.f;
+  float* o = out + (size_t)blockIdx.z * T * E;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      int t = t0 + m * 16 + g * 4 + i;
+      if (t < T) o[(size_t)t * E + e] = acc[m][i] + bv;
+    }
+  }
+}
+
+__global__ void router_logits_reduce(const float* __restrict__ part, const float* __restrict__ bias,
+                                     int T, int E, int ksplit, float* __restrict__ out) {
+  size_t n = (size_t)T * E;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int k = 0; k < ksplit; ++k) s += part[(size_t)k * n + i];
+    if (bias != nullptr) s += bias[i % E];
+    out[i] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Top-k selector: one wave per token.
+//
+// Key used for selection:
+//   ORDER_TOPK_ACT : the raw logit                                (router.py:411-427)
+//   ORDER_ACT_TOPK : softmax -> the raw logit (softmax is strictly increasing),
+//                    sigmoid -> sigmoid(logit)                    (router.py:473-494)
+//   ORDER_GROUPED  : act(logit) + correction_bias, restricted to the topk_group
+//                    groups with the largest sum-of-top-2 keys    (DeepSeek-V3)
+// Ties select the lower expert (group) index; ids come out in descending key.
+// Weights: ORDER_TOPK_ACT applies the activation to the K selected logits
+// (softmax over the K values, or sigmoid); the other orders gather act(logit).
+// Optional renorm w / (sum_k w + eps), sums taken k = 0..K-1; then * scale.
+// Softmax over all experts sums e = 0..E-1 sequentially (matches the oracle).
+// ---------------------------------------------------------------------------
+constexpr int kTopkMaxE = 1024;
+constexpr int kTopkMaxP = kTopkMaxE / 64;
+
+struct KeyIdx {
+  float v;
+  int i;
+};
+
+__device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
+  return v > v2 || (v == v2 && i < i2);
+}
+
+__device__ __forceinline__ KeyIdx wave_argmax(float v, int i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float v2 = __shfl_xor(v, o, 64);
+    int i2 = __shfl_xor(i, o, 64);
+    if (better(v2, i2, v, i)) {
+      v = v2;
+      i = i2;
+    }
+  }
+  return {v, i};
+}
+
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const float* __restrict__ logits, const float* __restrict__ corr_bias, int T, int E, int K,
+    int order, int scoring, int n_group, int topk_group, int renorm, float eps, float scale,
+    int32_t* __restrict__ ids, float* __restrict__ weights, float* __restrict__ aff) {
+  __shared__ float s_act[4][kTopkMaxE];
+  __shared__ float s_key[4][kTopkMaxE];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;  // wave-uniform; no workgroup barrier below
+  const float* row = logits + (size_t)t * E;
+  const int P = (E + 63) / 64;
+  const float NEG_INF = -__builtin_inff();
+  const bool need_act = order != MOE_ORDER_TOPK_ACT;
+
+  float lg[kTopkMaxP];
+#pragma unroll
+  for (int j = 0; j < kTopkMaxP; ++j) {
+    int e = lane + 64 * j;
+    lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
+  }
+
+  if (need_act) {
+    if (scoring == MOE_SCORING_SIGMOID) {
+#pragma unroll
+      for (int j = 0; j < kTopkMaxP; ++j) {
+        int e = lane + 64 * j;
+        if (j < P && e < E) s_act[wave][e] = det_sigmoid_f32(lg[j]);
+      }
+    } else {
+      float m = NEG_INF;
+#pragma unroll
+      for (int j = 0; j < kTopkMaxP; ++j) m = fmaxf(m, lg[j]);
+      m = wave_max_f32(m);
+#pragma unroll
+      for (int j = 0; j < kTopkMaxP; ++j) {
+        int e = lane + 64 * j;
+        if (j < P && e < E) s_act[wave][e] = det_exp_f32(lg[j] - m);
+      }
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      float sum = 0.f;
+      for (int e = 0; e < E; ++e) sum += s_act[wave][e];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < kTopkMaxP; ++j) {
+        int e = lane + 64 * j;
+        if (j < P && e < E) s_act[wave][e] = s_act[wave][e] / sum;
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+
+  // Selection keys (kept in registers, mirrored in LDS for the group scan).
+  float key[kTopkMaxP];
+  bool valid[kTopkMaxP];
+#pragma unroll
+  for (int j = 0; j < kTopkMaxP; ++j) {
+    int e = lane + 64 * j;
+    valid[j] = (j < P && e < E);
+    float kv = NEG_INF;
+    if (valid[j]) {
+      if (order == MOE_ORDER_TOPK_ACT || (order == MOE_ORDER_ACT_TOPK && scoring == MOE_SCORING_SOFTMAX)) {
+        kv = lg[j];
+      } else if (order == MOE_ORDER_ACT_TOPK) {
+        kv = s_act[wave][e];
+      } else {
+        kv = s_act[wave][e] + (corr_bias != nullptr ? corr_bias[e] : 0.f);
+      }
+      s_key[wave][e] = kv;
+    }
+    key[j] = kv;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+
+  if (order == MOE_ORDER_GROUPED && n_group > 1 && topk_group < n_group) {
+    const int gs = E / n_group;
+    float gscore = NEG_INF;
+    int gidx = 0x7fffffff;
+    if (lane < n_group) {
+      float t1 = NEG_INF, t2 = NEG_INF;
+      for (int q = 0; q < gs; ++q) {
+        float v = s_key[wave][lane * gs + q];
+        if (v > t1) {
+          t2 = t1;
+          t1 = v;
+        } else if (v > t2) {
+          t2 = v;
+        }
+      }
+      gscore = (gs == 1) ? t1 : t1 + t2;
+      gidx = lane;
+    }
+    uint64_t keep = 0;
+    for (int q = 0; q < topk_group; ++q) {
+      KeyIdx b = wave_argmax(gscore, gidx);
+      if (b.i < n_group) keep |= 1ull << b.i;
+      if (lane == b.i) {
+        gscore = NEG_INF;
+        gidx = 0x7fffffff;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kTopkMaxP; ++j) {
+      int e = lane + 64 * j;
+      if (valid[j] && !((keep >> (e / gs)) & 1ull)) valid[j] = false;
+    }
+  }
+
+  // K rounds of wave argmax; lane k keeps the k-th winner.
+  int my_id = -1;
+  float my_key = 0.f;
+  int taken[kTopkMaxP];
+#pragma unroll
+  for (int j = 0; j < kTopkMaxP; ++j) taken[j] = -1;
+  for (int k = 0; k < K; ++k) {
+    float bv = NEG_INF;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < kTopkMaxP; ++j) {
+      int e = lane + 64 * j;
+      if (valid[j] && taken[j] < 0 && better(key[j], e, bv, bi)) {
+        bv = key[j];
+        bi = e;
+      }
+    }
+    KeyIdx b = wave_argmax(bv, bi);
+#pragma unroll
+    for (int j = 0; j < kTopkMaxP; ++j)
+      if (lane + 64 * j == b.i) taken[j] = k;
+    if (lane == k) {
+      my_id = (b.i < E) ? b.i : -1;  // no valid candidate left (NaN keys): id -1
+      my_key = b.v;
+    }
+  }
+
+  // Weights for the K selections (lane k holds selection k).
+  float wv = 0.f;
+  if (order == MOE_ORDER_TOPK_ACT) {
+    if (scoring == MOE_SCORING_SOFTMAX) {
+      float m0 = __shfl(my_key, 0, 64);
+      float ex = (lane < K) ? det_exp_f32(my_key - m0) : 0.f;
+      float sum = 0.f;
+      for (int k = 0; k < K; ++k) sum += __shfl(ex, k, 64);
+      wv = ex / sum;
+    } else {
+      wv = (lane < K) ? det_sigmoid_f32(my_key) : 0.f;
+    }
+  } else {
+    wv = (lane < K && my_id >= 0) ? s_act[wave][my_id] : 0.f;
+  }
+  if (renorm) {
+    float sum = 0.f;
+    for (int k = 0; k < K; ++k) sum += __shfl(wv, k, 64);
+    float den = sum + eps;
+    wv = wv / den;
+  }
+  wv = wv * scale;
+
+  if (lane < K) {
+    ids[(size_t)t * K + lane] = my_id;
+    weights[(size_t)t * K + lane] = wv;
+  }
+  if (aff != nullptr) {
+#pragma unroll
+    for (int j = 0; j < kTopkMaxP; ++j) {
+      int e = lane + 64 * j;
+      int k = taken[j];
+      float v = __shfl(wv, k < 0 ? 0 : k, 64);  // all lanes take part in the shuffle
+      if (j < P && e < E) aff[(size_t)t * E + e] = (k >= 0) ? v : 0.f;
+    }
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_router_logits(const void* x_bf16, const void* w_bf16, const float* bias, int T,
+                                 int H, int E, float* logits, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  MOE_API_BEGIN("moe_router_logits");
+  MOE_CHECK_ARG(x_bf16 && w_bf16 && logits, "null pointer argument");
+  MOE_CHECK_ARG(T >= 0 && H > 0 && E > 0, "bad sizes T=%d H=%d E=%d", T, H, E);
+  MOE_CHECK_ARG(H % 64 == 0, "H must be a multiple of 64, got %d", H);
+  MOE_CHECK_ARG(((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)w_bf16 & 15) == 0,
+                "x and w must be 16-byte aligned");
+  if (T == 0) return MOE_OK;
+  hipStream_t st = (hipStream_t)stream;
+  int ks = router_logits_splits(T, H, E);
+  int kchunk = ((H / 64 + ks - 1) / ks) * 64;
+  ks = (H + kchunk - 1) / kchunk;
+  dim3 grid((T + 63) / 64, (E + 63) / 64, ks);
+  if (ks == 1) {
+    hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, st, (const uint16_t*)x_bf16,
+                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, logits);
+  } else {
+    size_t need = (size_t)ks * T * E * sizeof(float);
+    MOE_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                  "workspace too small: need %zu bytes", need);
+    float* part = (float*)workspace;
+    hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, st, (const uint16_t*)x_bf16,
+                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, part);
+    size_t n = (size_t)T * E;
+    int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(router_logits_reduce, dim3(blocks), dim3(256), 0, st, part, bias, T, E, ks,
+                       logits);
+  }
+  MOE_API_END();
+}
+
+extern "C" size_t moe_router_logits_workspace_bytes(int T, int H, int E) {
+  if (T <= 0 || H <= 0 || E <= 0 || H % 64) return 0;
+  int ks = router_logits_splits(T, H, E);
+  int kchunk = ((H / 64 + ks - 1) / ks) * 64;
+  ks = (H + kchunk - 1) / kchunk;
+  return ks > 1 ? (size_t)ks * T * E * sizeof(float) : 0;
+}
+
+extern "C" int moe_router_topk(const float* logits, const float* corr_bias, int T, int E, int K,
+                               int order, int scoring, int n_group, int topk_group, int renorm,
+                               float renorm_eps, float routed_scale, int32_t* ids, float* weights,
+                               float* affinities, void* stream) {
+  MOE_API_BEGIN("moe_router_topk");
+  MOE_CHECK_ARG(logits && ids && weights, "null pointer argument");
+  MOE_CHECK_ARG(T >= 0 && E > 0 && E <= kTopkMaxE, "E must be in [1, %d], got %d", kTopkMaxE, E);
+  MOE_CHECK_ARG(K >= 1 && K <= E && K <= 64, "top_k must be in [1, min(E, 64)], got %d", K);
+  MOE_CHECK_ARG(order >= MOE_ORDER_TOPK_ACT && order <= MOE_ORDER_GROUPED, "bad order %d", order);
+  MOE_CHECK_ARG(scoring == MOE_SCORING_SOFTMAX || scoring == MOE_SCORING_SIGMOID,
+                "bad scoring %d", scoring);
+  if (order == MOE_ORDER_GROUPED) {
+    MOE_CHECK_ARG(n_group >= 1 && n_group <= 64 && E % n_group == 0,
+                  "n_group must divide E and be <= 64 (E=%d, n_group=%d)", E, n_group);
+    MOE_CHECK_ARG(topk_group >= 1 && topk_group <= n_group, "bad topk_group %d", topk_group);
+    MOE_CHECK_ARG((long)topk_group * (E / n_group) >= K,
+                  "topk_group * group size must be >= top_k");
+  }
+  if (T == 0) return MOE_OK;
+  hipLaunchKernelGGL(router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
+                     renorm_eps, routed_scale, ids, weights, affinities);
+  MOE_API_END();
+}

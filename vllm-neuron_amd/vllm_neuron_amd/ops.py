@@ -1,0 +1,249 @@
+"""Typed torch wrappers over the C ABI (one per entry point of include/moe_fp8.h).
+
+Each wrapper checks device, dtype and shape, allocates its outputs with torch
+(device memory only; the kernels never allocate), and enqueues the HIP kernel
+on the current torch stream. CPU tensors are rejected: there is no CPU path.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import ptr
+
+ORDER_TOPK_ACT, ORDER_ACT_TOPK, ORDER_GROUPED = 0, 1, 2
+SCORING = {"softmax": 0, "sigmoid": 1}
+FP8 = torch.float8_e4m3fn
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("vllm_neuron_amd kernels need GPU tensors (no CPU fallback)")
+
+
+def _need(t, dtype, shape=None, name="tensor"):
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _u8(t):
+    return t.view(torch.uint8) if t.dtype == FP8 else t
+
+
+def num_blocks(T, K, E, B):
+    return _lib.load().moe_num_blocks(T, K, E, B)
+
+
+def choose_mt(T, K, E):
+    avg = -(-T * min(K, E) // E)
+    for mt in (16, 32, 64):
+        if avg <= mt:
+            return mt
+    return 128
+
+
+# ---------------------------------------------------------------- router
+
+def router_logits(x, router_w, bias=None):
+    """x [T,H] bf16, router_w [E,H] bf16, bias [E] fp32 -> logits [T,E] fp32."""
+    _need_cuda(x, router_w, bias)
+    T, H = x.shape
+    E = router_w.shape[0]
+    _need(x, torch.bfloat16, (T, H), "hidden_states")
+    _need(router_w, torch.bfloat16, (E, H), "router weight [E, H]")
+    if bias is not None:
+        _need(bias, torch.float32, (E,), "router_bias")
+    out = torch.empty(T, E, device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    wsb = lib.moe_router_logits_workspace_bytes(T, H, E)
+    ws = torch.empty(max(wsb, 1), device=x.device, dtype=torch.uint8)
+    _lib.call("moe_router_logits", ptr(x), ptr(router_w), ptr(bias), T, H, E, ptr(out), ptr(ws),
+              wsb, _stream())
+    return out
+
+
+def router_topk(logits, top_k, order, scoring, n_group=1, topk_group=1, corr_bias=None,
+                renorm=False, eps=0.0, scale=1.0, dense=False):
+    """logits [T,E] fp32 -> ids [T,K] int32, weights [T,K] fp32 (+ affinities [T,E] if dense)."""
+    _need_cuda(logits, corr_bias)
+    T, E = logits.shape
+    _need(logits, torch.float32, (T, E), "logits")
+    if corr_bias is not None:
+        _need(corr_bias, torch.float32, (E,), "correction bias")
+    ids = torch.empty(T, top_k, device=logits.device, dtype=torch.int32)
+    w = torch.empty(T, top_k, device=logits.device, dtype=torch.float32)
+    aff = torch.empty(T, E, device=logits.device, dtype=torch.float32) if dense else None
+    _lib.call("moe_router_topk", ptr(logits), ptr(corr_bias), T, E, top_k, order,
+              SCORING[scoring] if isinstance(scoring, str) else int(scoring), n_group, topk_group,
+              int(bool(renorm)), float(eps), float(scale), ptr(ids), ptr(w), ptr(aff), _stream())
+    return (ids, w, aff) if dense else (ids, w)
+
+
+# ---------------------------------------------------------------- mapping
+
+def blockwise_mapping(ids=None, affinities=None, n_experts=None, top_k=None, block_size=256,
+                      padding_mask=None, check=False):
+    """Reference blockwise mapping from ids [T,K] or affinities [T,E]; returns a dict with
+    token_position_to_id [N*B], block_to_expert [N], conditions [N], expert_counts [E] and
+    inv_pos [T,K] (ids) or affinities_masked [T*E, 1] (affinities)."""
+    src = ids if ids is not None else affinities
+    if (ids is None) == (affinities is None):
+        raise ValueError("give exactly one of ids / affinities")
+    _need_cuda(src, padding_mask)
+    dev = src.device
+    if ids is not None:
+        T, K = ids.shape
+        E = int(n_experts)
+        _need(ids, torch.int32, (T, K), "ids")
+    else:
+        T, E = affinities.shape
+        K = int(top_k)
+        _need(affinities, torch.float32, (T, E), "expert_affinities")
+    B = int(block_size)
+    N = num_blocks(T, K, E, B)
+    lib = _lib.load()
+    out = {
+        "token_position_to_id": torch.empty(N * B, device=dev, dtype=torch.int32),
+        "block_to_expert": torch.empty(N, device=dev, dtype=torch.int32),
+        "conditions": torch.empty(N, device=dev, dtype=torch.int32),
+        "expert_counts": torch.empty(E, device=dev, dtype=torch.int32),
+        "num_blocks": N,
+    }
+    inv = torch.empty(T, K, device=dev, dtype=torch.int32) if ids is not None else None
+    aff_m = torch.empty(T * E, 1, device=dev, dtype=torch.float32) if affinities is not None else None
+    pm = None
+    if padding_mask is not None:
+        if tuple(padding_mask.shape) != (T,):
+            raise ValueError(f"padding_mask must be [T], got {tuple(padding_mask.shape)}")
+        pm = padding_mask.to(torch.uint8).contiguous()
+    wsb = lib.moe_mapping_workspace_bytes(T, E)
+    ws = torch.empty(wsb, device=dev, dtype=torch.uint8)
+    _lib.call("moe_blockwise_mapping", ptr(ids), ptr(affinities), ptr(pm), T, K, E, B, N,
+              ptr(out["token_position_to_id"]), ptr(out["block_to_expert"]),
+              ptr(out["conditions"]), ptr(out["expert_counts"]), ptr(inv), ptr(aff_m), ptr(ws),
+              wsb, _stream())
+    if check:
+        dropped = ctypes.c_int(0)
+        _lib.call("moe_mapping_status", ptr(ws), _stream(), ctypes.byref(dropped))
+        if dropped.value:
+            raise IndexError(f"{dropped.value} routed (token, expert) pairs do not fit the "
+                             f"N*B = {N * B} mapping (or expert ids out of range)")
+    if inv is not None:
+        out["inv_pos"] = inv
+    if aff_m is not None:
+        out["affinities_masked"] = aff_m
+    return out
+
+
+def invert_mapping(tpid, b2e, B, T, E):
+    _need_cuda(tpid, b2e)
+    N = b2e.numel()
+    inv = torch.empty(T, E, device=tpid.device, dtype=torch.int32)
+    _lib.call("moe_invert_mapping", ptr(tpid), ptr(b2e), N, B, T, E, ptr(inv), _stream())
+    return inv
+
+
+# ---------------------------------------------------------------- quant / GEMM / combine
+
+def act_quant(x):
+    """x [R,C] bf16 -> (codes [R,C] e4m3fn, scales [R, C/128] fp32)."""
+    _need_cuda(x)
+    R, C = x.shape
+    _need(x, torch.bfloat16, (R, C), "activations")
+    q = torch.empty(R, C, device=x.device, dtype=FP8)
+    s = torch.empty(R, C // 128, device=x.device, dtype=torch.float32)
+    _lib.call("moe_act_quant_1x128", ptr(x), R, C, ptr(q), ptr(s), _stream())
+    return q, s
+
+
+def build_tiles(tpid, b2e, B, T, K, E, n_shared, mt):
+    N = b2e.numel()
+    lib = _lib.load()
+    max_tiles = lib.moe_max_tiles(T, K, E, N, B, n_shared, mt)
+    tiles = torch.empty(max_tiles, 4, device=tpid.device, dtype=torch.int32)
+    num = torch.empty(1, device=tpid.device, dtype=torch.int32)
+    _lib.call("moe_build_tiles", ptr(tpid), ptr(b2e), N, B, T, E, n_shared, mt, ptr(tiles),
+              max_tiles, ptr(num), _stream())
+    return tiles, num, max_tiles
+
+
+def expert_gate_up(xq, xs, w, tpid, NB, tiles, num_tiles, max_tiles, mt):
+    T, H = xq.shape
+    E, I2, _ = w.w13.shape
+    I = I2 // 2
+    S = w.n_shared
+    P = NB + S * T
+    hq = torch.empty(P, I, device=xq.device, dtype=FP8)
+    hs = torch.empty(P, I // 128, device=xq.device, dtype=torch.float32)
+    _lib.call("moe_expert_gate_up", ptr(_u8(xq)), ptr(xs), T, H, I, E, ptr(_u8(w.w13)),
+              ptr(w.w13_scale), ptr(_u8(w.shared_w13)) if S else None,
+              ptr(w.shared_w13_scale) if S else None, S, ptr(tpid), NB, ptr(tiles),
+              ptr(num_tiles), max_tiles, mt, ptr(_u8(hq)), ptr(hs), _stream())
+    return hq, hs
+
+
+def expert_down(hq, hs, w, T, NB, tiles, num_tiles, max_tiles, mt):
+    E, H, I = w.w2.shape
+    S = w.n_shared
+    y = torch.empty(hq.shape[0], H, device=hq.device, dtype=torch.bfloat16)
+    _lib.call("moe_expert_down", ptr(_u8(hq)), ptr(hs), T, H, I, E, ptr(_u8(w.w2)),
+              ptr(w.w2_scale), ptr(_u8(w.shared_w2)) if S else None,
+              ptr(w.shared_w2_scale) if S else None, S, NB, ptr(tiles), ptr(num_tiles),
+              max_tiles, mt, ptr(y), _stream())
+    return y
+
+
+def combine(y, inv, wts, T, H, NB, n_shared):
+    """out[t] = sum_s wts[t,s] * y[inv[t,s]] + shared rows; inv/wts [T,S] (wts None -> 1)."""
+    S = 0 if inv is None else inv.shape[1]
+    out = torch.empty(T, H, device=y.device, dtype=torch.bfloat16)
+    _lib.call("moe_combine", ptr(y), ptr(inv), ptr(wts), S, T, H, NB, n_shared, ptr(out),
+              _stream())
+    return out
+
+
+def selftest_mfma(a, b):
+    """a, b [16,128] e4m3fn -> c [16,16] fp32 through one fp8 MFMA."""
+    _need_cuda(a, b)
+    c = torch.empty(16, 16, device=a.device, dtype=torch.float32)
+    _lib.call("moe_selftest_mfma_fp8", ptr(_u8(a.contiguous())), ptr(_u8(b.contiguous())), ptr(c),
+              _stream())
+    return c
+
+
+# ---------------------------------------------------------------- whole layer
+
+def layer_forward(x, w, cfg, return_routing=False):
+    """Whole layer on the HIP path: returns out [T,H] bf16 (+ ids, weights, logits)."""
+    _need_cuda(x, w.w13)
+    T, H = x.shape
+    _need(x, torch.bfloat16, (T, H), "hidden_states")
+    E, I = w.n_experts, w.intermediate
+    K, S, B = cfg.top_k, w.n_shared, cfg.block_size
+    lib = _lib.load()
+    wsb = lib.moe_layer_workspace_bytes(T, H, I, E, K, S, B)
+    ws = torch.empty(wsb, device=x.device, dtype=torch.uint8)
+    out = torch.empty(T, H, device=x.device, dtype=torch.bfloat16)
+    ids = torch.empty(T, K, device=x.device, dtype=torch.int32) if return_routing else None
+    wts = torch.empty(T, K, device=x.device, dtype=torch.float32) if return_routing else None
+    lg = torch.empty(T, E, device=x.device, dtype=torch.float32) if return_routing else None
+    order = ORDER_GROUPED if cfg.grouped else ORDER_TOPK_ACT
+    _lib.call("moe_layer_forward", ptr(x), T, H, I, E, K, S, ptr(w.router_w), ptr(w.router_bias),
+              ptr(w.corr_bias), order, SCORING[cfg.scoring], cfg.n_group, cfg.topk_group,
+              int(cfg.renorm), 1e-20, float(cfg.routed_scaling), ptr(_u8(w.w13)),
+              ptr(w.w13_scale), ptr(_u8(w.w2)), ptr(w.w2_scale),
+              ptr(_u8(w.shared_w13)) if S else None, ptr(w.shared_w13_scale) if S else None,
+              ptr(_u8(w.shared_w2)) if S else None, ptr(w.shared_w2_scale) if S else None, B,
+              ptr(out), ptr(ids), ptr(wts), ptr(lg), ptr(ws), wsb, _stream())
+    if return_routing:
+        return out, ids, wts, lg
+    return out
