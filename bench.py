@@ -50,6 +50,7 @@ def run_phase_b(x, w, cfg, steps, torch, ops):
     T = x.shape[0]
     E, K, B, S = cfg.n_experts, cfg.top_k, cfg.block_size, w.n_shared
     mt = ops.choose_mt(T, K, E)
+    block = ops.use_block_kernels(T, K, E)
     st = torch.cuda.current_stream()
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     ids = None
@@ -60,12 +61,22 @@ def run_phase_b(x, w, cfg, steps, torch, ops):
         m = ops.blockwise_mapping(ids=ids, n_experts=E, block_size=B)
         xq, xs = ops.act_quant(x)
         NB = m["token_position_to_id"].numel()
-        tiles, num, mx = ops.build_tiles(m["token_position_to_id"], m["block_to_expert"], B, T, K, E, S, mt)
+        tpid = m["token_position_to_id"]
+        if block:
+            tiles, num, mx = ops.build_block_tiles(tpid, m["block_to_expert"], B, T, K, E, S)
+        else:
+            tiles, num, mx = ops.build_tiles(tpid, m["block_to_expert"], B, T, K, E, S, mt)
         ev[i][0].record(st)
-        hq, hs = ops.expert_gate_up(xq, xs, w, m["token_position_to_id"], NB, tiles, num, mx, mt)
+        if block:
+            hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mx)
+        else:
+            hq, hs = ops.expert_gate_up(xq, xs, w, tpid, NB, tiles, num, mx, mt)
         ev[i][1].record(st)
         ev[i][2].record(st)
-        y = ops.expert_down(hq, hs, w, T, NB, tiles, num, mx, mt)
+        if block:
+            y = ops.expert_down_block(hq, hs, w, T, NB, tiles, num, mx)
+        else:
+            y = ops.expert_down(hq, hs, w, T, NB, tiles, num, mx, mt)
         ev[i][3].record(st)
         ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, S)
     torch.cuda.synchronize()

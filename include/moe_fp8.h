@@ -147,6 +147,34 @@ int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int
                     const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
                     void* stream);
 
+/* Prefill-sized variants ("block" kernels): one workgroup computes 256 slots
+ * of one expert x 256 weight rows with 32x32x64 fp8 MFMA tiles, both operands
+ * staged through LDS. Their tile list holds up to 256 consecutive slots of one
+ * expert per tile: `tiles` is max_tiles * 24 bytes (int32x4 tiles followed by
+ * int32x2 {first tile, tile count} of each tile's expert), built by
+ * moe_build_block_tiles with a scratch workspace of
+ * moe_block_tiles_workspace_bytes(N, max_tiles). Same outputs as
+ * moe_expert_gate_up / moe_expert_down (same replaced reference interface,
+ * moe_cte.py:356-421 and :557-588); the layer uses them when the average
+ * expert receives more than 64 rows. */
+int moe_max_block_tiles(int T, int K, int E, int N, int B, int n_shared);
+size_t moe_block_tiles_workspace_bytes(int N, int max_tiles);
+int moe_build_block_tiles(const int32_t* token_position_to_id, const int32_t* block_to_expert,
+                          int N, int B, int T, int E, int n_shared, int32_t* tiles, int max_tiles,
+                          int32_t* num_tiles, void* workspace, size_t workspace_bytes,
+                          void* stream);
+int moe_expert_gate_up_block(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
+                             const uint8_t* w13, const float* w13_scale,
+                             const uint8_t* w13_shared, const float* w13_shared_scale,
+                             int n_shared, const int32_t* token_position_to_id, int NB,
+                             const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                             uint8_t* hq, float* hs, void* stream);
+int moe_expert_down_block(const uint8_t* hq, const float* hs, int T, int H, int I, int E,
+                          const uint8_t* w2, const float* w2_scale, const uint8_t* w2_shared,
+                          const float* w2_shared_scale, int n_shared, int NB,
+                          const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                          void* y_bf16, void* stream);
+
 /* ---- weighted unpermute-combine ----------------------------------------- */
 
 /* out[t] = bf16( sum_{s<S, inv[t,s]>=0} w[t,s] * y[inv[t,s]]  +  sum_{j<n_shared} y[NB + j*T + t] ),
@@ -176,10 +204,12 @@ int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E, int K, int
 
 /* ---- diagnostics ----------------------------------------------------------- */
 
-/* c[16,16] = decode(a[16,128]) . decode(b[16,128])^T through one fp8 MFMA with
- * the operand/accumulator lane mapping the expert GEMMs use. No reference
+/* shape 0: c[16,16] = decode(a[16,128]) . decode(b[16,128])^T through one
+ * v_mfma_f32_16x16x128_f8f6f4; shape 1: c[32,32] = decode(a[32,128]) .
+ * decode(b[32,128])^T through two v_mfma_f32_32x32x64_f8f6f4; each with the
+ * operand/accumulator lane mapping the expert GEMMs use. No reference
  * counterpart: it pins the gfx950 fp8 MFMA data layout for the tests. */
-int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, void* stream);
+int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, int shape, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,17 +13,18 @@ from vllm_neuron_amd import ops
 pytestmark = pytest.mark.gpu
 
 
-def test_mfma_fp8_fragment_layout(cuda):
+@pytest.mark.parametrize("shape,n", [(0, 16), (1, 32)])
+def test_mfma_fp8_fragment_layout(cuda, shape, n):
     """Integer-valued operands: every partial sum is exact, so any lane-layout error
     (row/column/K mapping, output placement) shows as an exact mismatch."""
-    say("mfma fragment layout")
+    say("mfma fragment layout", shape)
     from oracle.fp8 import e4m3fn_encode
-    rng = np.random.default_rng(0)
-    ai = rng.integers(-8, 9, (16, 128)).astype(np.float32)
-    bi = rng.integers(-8, 9, (16, 128)).astype(np.float32)
+    rng = np.random.default_rng(shape)
+    ai = rng.integers(-8, 9, (n, 128)).astype(np.float32)
+    bi = rng.integers(-8, 9, (n, 128)).astype(np.float32)
     ta = torch.from_numpy(e4m3fn_encode(ai)).view(torch.float8_e4m3fn).to(cuda)
     tb = torch.from_numpy(e4m3fn_encode(bi)).view(torch.float8_e4m3fn).to(cuda)
-    c = ops.selftest_mfma(ta, tb).cpu().numpy()
+    c = ops.selftest_mfma(ta, tb, shape).cpu().numpy()
     assert np.array_equal(c, ai @ bi.T)
 
 
@@ -185,3 +186,35 @@ def test_tiles_cover_every_slot_once(cuda, mt):
                 assert s >= NB
     assert np.all(seen[:NB][tpid >= 0] == 1) and np.all(seen[NB:] == 1)
     assert n <= max_tiles
+
+
+@pytest.mark.parametrize("T,K,E,B,S", [(700, 4, 24, 64, 1), (4096, 8, 40, 256, 1), (300, 2, 3, 16, 0),
+                                       (9000, 8, 256, 256, 1)])
+def test_block_tiles_cover_every_slot_once(cuda, T, K, E, B, S):
+    """Block tiles: <= 256 consecutive slots of one expert; every routed slot in exactly one
+    tile; the segment records let every (tile, column tile) item be recovered."""
+    say("block tiles", T, K, E, B)
+    rng = np.random.default_rng(T + E)
+    p = rng.zipf(1.3, E).astype(np.float64)
+    p[: max(1, E // 10)] = 0
+    p /= p.sum()
+    ids = np.stack([rng.choice(E, K, replace=False, p=p) for _ in range(T)]).astype(np.int32)
+    m = ops.blockwise_mapping(ids=torch.from_numpy(ids).to(cuda), n_experts=E, block_size=B)
+    tiles, num, mx = ops.build_block_tiles(m["token_position_to_id"], m["block_to_expert"], B, T, K, E, S)
+    n = int(num.item())
+    raw = tiles.cpu().numpy()
+    tl = raw[: 4 * mx].reshape(mx, 4)[:n]
+    sg = raw[4 * mx:].reshape(mx, 2)[:n]
+    tpid = m["token_position_to_id"].cpu().numpy()
+    b2e = m["block_to_expert"].cpu().numpy()
+    NB = tpid.size
+    seen = np.zeros(NB + S * T, np.int32)
+    for t, (e, s0, rows, _) in enumerate(tl):
+        assert 1 <= rows <= 256
+        first, cnt = sg[t]
+        assert first <= t < first + cnt and np.all(tl[first:first + cnt, 0] == e)
+        seen[s0:s0 + rows] += 1
+        if e < E:
+            assert np.all(b2e[np.arange(s0, s0 + rows) // B] == e)
+    assert np.all(seen[:NB][tpid >= 0] == 1) and np.all(seen[NB:] == 1)
+    assert np.all(seen[:NB][tpid < 0] <= 1)

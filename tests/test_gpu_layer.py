@@ -149,3 +149,27 @@ def test_layer_dsv3_full_size(cuda, T, idx, tokens):
     _check_layer(cfg, w, x, tokens=tokens, tag=f"dsv3 T={T}")
     del w
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("T,E,K,S", [(2048, 8, 2, 0), (3000, 16, 4, 1), (700, 4, 2, 1)])
+def test_layer_block_kernels(cuda, T, E, K, S):
+    """Prefill-sized path (> 64 rows per expert): block kernels against the oracle,
+    including partial 256-row tiles, and agreement with the row-tile kernels."""
+    cfg = MoEConfig(1024, 512, E, K, n_shared=S, scoring="sigmoid", grouped=True, n_group=1,
+                    topk_group=1, renorm=True, routed_scaling=1.0)
+    say("layer block kernels", T, E, K, S)
+    assert ops.use_block_kernels(T, K, E)
+    w = synthetic.make_weights(cfg, 21 + E, device=cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, 21 + E).to(cuda)
+    out = _check_layer(cfg, w, x, tag=f"block T={T} E={E}")
+    # the same routing through the row-tile kernels (different MFMA shape and order)
+    lg = ops.router_logits(x, w.router_w, w.router_bias)
+    ids, wts = ops.router_topk(lg, K, ops.ORDER_GROUPED, "sigmoid", 1, 1, w.corr_bias, True, 1e-20, 1.0)
+    m = ops.blockwise_mapping(ids=ids, n_experts=E, block_size=256)
+    xq, xs = ops.act_quant(x)
+    NB = m["token_position_to_id"].numel()
+    tiles, num, mx = ops.build_tiles(m["token_position_to_id"], m["block_to_expert"], 256, T, K, E, S, 128)
+    hq, hs = ops.expert_gate_up(xq, xs, w, m["token_position_to_id"], NB, tiles, num, mx, 128)
+    y = ops.expert_down(hq, hs, w, T, NB, tiles, num, mx, 128)
+    alt = ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, S)
+    assert rel_l2(np_f32(out), np_f32(alt)) < 5e-3

@@ -51,8 +51,17 @@ struct LayerWs {
   uint8_t* hq;
   float* hs;
   uint16_t* y;
+  int32_t* btiles;
+  int32_t* bnum;
+  void* btiles_ws;
+  size_t btiles_ws_bytes;
   size_t bytes;
 };
+
+// The prefill-sized ("block") kernels take over above 64 rows per expert.
+static bool use_block(int T, int K, int E) {
+  return ((long)T * std::min(K, E) + E - 1) / E > 64;
+}
 
 static inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -89,6 +98,13 @@ static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, in
   w.hq = (uint8_t*)take((size_t)P * I);
   w.hs = (float*)take((size_t)P * (I / 128) * 4);
   w.y = (uint16_t*)take((size_t)P * H * 2);
+  if (use_block(T, K, E)) {
+    const int mbt = moe_max_block_tiles(T, K, E, N, B, n_sh);
+    w.btiles = (int32_t*)take((size_t)mbt * 24);
+    w.bnum = (int32_t*)take(16);
+    w.btiles_ws_bytes = moe_block_tiles_workspace_bytes(N, mbt);
+    w.btiles_ws = take(w.btiles_ws_bytes);
+  }
   w.bytes = off;
   return w;
 }
@@ -153,13 +169,26 @@ extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E,
   MOE_STEP(moe_blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond,
                                  w.counts, w.inv, nullptr, w.map_ws, w.map_ws_bytes, stream));
   MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
-  MOE_STEP(moe_build_tiles(w.tpid, w.b2e, N, B, T, E, n_shared, mt, w.tiles, max_tiles,
-                           w.num_tiles, stream));
-  MOE_STEP(moe_expert_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
-                              w13_shared_scale, n_shared, w.tpid, (int)NB, w.tiles, w.num_tiles,
-                              max_tiles, mt, w.hq, w.hs, stream));
-  MOE_STEP(moe_expert_down(w.hq, w.hs, T, H, I, E, w2, w2_scale, w2_shared, w2_shared_scale,
-                           n_shared, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y, stream));
+  if (use_block(T, K, E)) {
+    const int mbt = moe_max_block_tiles(T, K, E, N, B, n_shared);
+    MOE_STEP(moe_build_block_tiles(w.tpid, w.b2e, N, B, T, E, n_shared, w.btiles, mbt, w.bnum,
+                                   w.btiles_ws, w.btiles_ws_bytes, stream));
+    MOE_STEP(moe_expert_gate_up_block(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
+                                      w13_shared_scale, n_shared, w.tpid, (int)NB, w.btiles,
+                                      w.bnum, mbt, w.hq, w.hs, stream));
+    MOE_STEP(moe_expert_down_block(w.hq, w.hs, T, H, I, E, w2, w2_scale, w2_shared,
+                                   w2_shared_scale, n_shared, (int)NB, w.btiles, w.bnum, mbt,
+                                   w.y, stream));
+  } else {
+    MOE_STEP(moe_build_tiles(w.tpid, w.b2e, N, B, T, E, n_shared, mt, w.tiles, max_tiles,
+                             w.num_tiles, stream));
+    MOE_STEP(moe_expert_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
+                                w13_shared_scale, n_shared, w.tpid, (int)NB, w.tiles,
+                                w.num_tiles, max_tiles, mt, w.hq, w.hs, stream));
+    MOE_STEP(moe_expert_down(w.hq, w.hs, T, H, I, E, w2, w2_scale, w2_shared, w2_shared_scale,
+                             n_shared, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y,
+                             stream));
+  }
   MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)NB, n_shared, out_bf16, stream));
 #undef MOE_STEP
   return MOE_OK;

@@ -268,14 +268,35 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
   }
 }
 
-// Single-wave check of the fragment mapping above: c[16,16] = a[16,128] . b[16,128]^T.
-__global__ void selftest_mfma_kernel(const uint8_t* a, const uint8_t* b, float* c) {
-  const int lane = threadIdx.x, g = lane >> 4, r16 = lane & 15;
-  const v8i fa = load_frag_global(a + r16 * 128 + g * 16);
-  const v8i fb = load_frag_global(b + r16 * 128 + g * 16);
-  const v4f d = mfma_fp8(fa, fb);
+// Single-wave checks of the fragment mappings:
+//   16x16: c[16,16] = a[16,128] . b[16,128]^T with the mapping above;
+//   32x32: c[32,32] = a[32,128] . b[32,128]^T with the block-kernel mapping
+//          (lane l: row l%32, bytes [h*64 + (l/32)*32, +32) for MFMA h).
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+
+__global__ void selftest_mfma_kernel(const uint8_t* a, const uint8_t* b, float* c, int shape) {
+  const int lane = threadIdx.x;
+  if (shape == 0) {
+    const int g = lane >> 4, r16 = lane & 15;
+    const v8i fa = load_frag_global(a + r16 * 128 + g * 16);
+    const v8i fb = load_frag_global(b + r16 * 128 + g * 16);
+    const v4f d = mfma_fp8(fa, fb);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) c[(4 * g + i) * 16 + r16] = d[i];
+    for (int i = 0; i < 4; ++i) c[(4 * g + i) * 16 + r16] = d[i];
+  } else {
+    const int g2 = lane >> 5, l32 = lane & 31;
+    v16f_t d = {};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int4* pa = (const int4*)(a + l32 * 128 + h * 64 + g2 * 32);
+      const int4* pb = (const int4*)(b + l32 * 128 + h * 64 + g2 * 32);
+      const v8i fa = (v8i){pa[0].x, pa[0].y, pa[0].z, pa[0].w, pa[1].x, pa[1].y, pa[1].z, pa[1].w};
+      const v8i fb = (v8i){pb[0].x, pb[0].y, pb[0].z, pb[0].w, pb[1].x, pb[1].y, pb[1].z, pb[1].w};
+      d = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa, fb, d, 0, 0, 0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) c[(8 * (r >> 2) + 4 * g2 + (r & 3)) * 32 + l32] = d[r];
+  }
 }
 
 template <int KIND>
@@ -385,11 +406,14 @@ extern "C" int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H,
   MOE_API_END();
 }
 
-extern "C" int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, void* stream) {
+extern "C" int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, int shape,
+                                     void* stream) {
   MOE_API_BEGIN("moe_selftest_mfma_fp8");
   MOE_CHECK_ARG(a && b && c, "null pointer argument");
+  MOE_CHECK_ARG(shape == 0 || shape == 1, "shape must be 0 (16x16x128) or 1 (32x32x64)");
   MOE_CHECK_ALIGN16(a);
   MOE_CHECK_ALIGN16(b);
-  hipLaunchKernelGGL(selftest_mfma_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, a, b, c);
+  hipLaunchKernelGGL(selftest_mfma_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, a, b, c,
+                     shape);
   MOE_API_END();
 }

@@ -44,7 +44,14 @@ PROTOTYPES = {
     "moe_layer_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "moe_layer_forward": (_i, [_p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _i, _i, _i, _i, _f, _f,
                                _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p, _p, _sz, _p]),
-    "moe_selftest_mfma_fp8": (_i, [_p, _p, _p, _p]),
+    "moe_max_block_tiles": (_i, [_i, _i, _i, _i, _i, _i]),
+    "moe_block_tiles_workspace_bytes": (_sz, [_i, _i]),
+    "moe_build_block_tiles": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _i, _p, _p, _sz, _p]),
+    "moe_expert_gate_up_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _p, _p,
+                                      _i, _p, _p, _p]),
+    "moe_expert_down_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _p,
+                                   _p]),
+    "moe_selftest_mfma_fp8": (_i, [_p, _p, _p, _i, _p]),
 }
 
 _lock = threading.Lock()

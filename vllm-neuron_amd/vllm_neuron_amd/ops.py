@@ -43,6 +43,11 @@ def num_blocks(T, K, E, B):
     return _lib.load().moe_num_blocks(T, K, E, B)
 
 
+def use_block_kernels(T, K, E):
+    """The layer switches to the prefill-sized kernels above 64 rows per expert."""
+    return -(-T * min(K, E) // E) > 64
+
+
 def choose_mt(T, K, E):
     avg = -(-T * min(K, E) // E)
     for mt in (16, 32, 64):
@@ -211,12 +216,53 @@ def combine(y, inv, wts, T, H, NB, n_shared):
     return out
 
 
-def selftest_mfma(a, b):
-    """a, b [16,128] e4m3fn -> c [16,16] fp32 through one fp8 MFMA."""
+def build_block_tiles(tpid, b2e, B, T, K, E, n_shared):
+    """Tile list of the prefill-sized kernels (up to 256 slots of one expert per tile)."""
+    N = b2e.numel()
+    lib = _lib.load()
+    max_tiles = lib.moe_max_block_tiles(T, K, E, N, B, n_shared)
+    tiles = torch.empty(max_tiles * 6, device=tpid.device, dtype=torch.int32)
+    num = torch.empty(1, device=tpid.device, dtype=torch.int32)
+    wsb = lib.moe_block_tiles_workspace_bytes(N, max_tiles)
+    ws = torch.empty(wsb, device=tpid.device, dtype=torch.uint8)
+    _lib.call("moe_build_block_tiles", ptr(tpid), ptr(b2e), N, B, T, E, n_shared, ptr(tiles),
+              max_tiles, ptr(num), ptr(ws), wsb, _stream())
+    return tiles, num, max_tiles
+
+
+def expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num_tiles, max_tiles):
+    T, H = xq.shape
+    E, I2, _ = w.w13.shape
+    I = I2 // 2
+    S = w.n_shared
+    hq = torch.empty(NB + S * T, I, device=xq.device, dtype=FP8)
+    hs = torch.empty(NB + S * T, I // 128, device=xq.device, dtype=torch.float32)
+    _lib.call("moe_expert_gate_up_block", ptr(_u8(xq)), ptr(xs), T, H, I, E, ptr(_u8(w.w13)),
+              ptr(w.w13_scale), ptr(_u8(w.shared_w13)) if S else None,
+              ptr(w.shared_w13_scale) if S else None, S, ptr(tpid), NB, ptr(tiles),
+              ptr(num_tiles), max_tiles, ptr(_u8(hq)), ptr(hs), _stream())
+    return hq, hs
+
+
+def expert_down_block(hq, hs, w, T, NB, tiles, num_tiles, max_tiles):
+    E, H, I = w.w2.shape
+    S = w.n_shared
+    y = torch.empty(hq.shape[0], H, device=hq.device, dtype=torch.bfloat16)
+    _lib.call("moe_expert_down_block", ptr(_u8(hq)), ptr(hs), T, H, I, E, ptr(_u8(w.w2)),
+              ptr(w.w2_scale), ptr(_u8(w.shared_w2)) if S else None,
+              ptr(w.shared_w2_scale) if S else None, S, NB, ptr(tiles), ptr(num_tiles),
+              max_tiles, ptr(y), _stream())
+    return y
+
+
+def selftest_mfma(a, b, shape=0):
+    """shape 0: a, b [16,128] -> c [16,16] (one 16x16x128 fp8 MFMA);
+    shape 1: a, b [32,128] -> c [32,32] (two 32x32x64 fp8 MFMAs)."""
     _need_cuda(a, b)
-    c = torch.empty(16, 16, device=a.device, dtype=torch.float32)
+    n = 16 if shape == 0 else 32
+    c = torch.empty(n, n, device=a.device, dtype=torch.float32)
     _lib.call("moe_selftest_mfma_fp8", ptr(_u8(a.contiguous())), ptr(_u8(b.contiguous())), ptr(c),
-              _stream())
+              shape, _stream())
     return c
 
 
