@@ -4,28 +4,29 @@
 // block-scaled fp8 weights), organised for experts that receive hundreds of
 // rows, where the layer becomes MFMA-bound:
 //
-//  * one workgroup (8 waves) computes a 256-row x 256-column tile: the rows are
-//    up to 256 consecutive slots of one expert, the columns 256 weight rows
+//  * one workgroup (8 waves) computes a 128-row x 256-column tile: the rows are
+//    up to 128 consecutive slots of one expert, the columns 256 weight rows
 //    (gate_up: 128 gate rows + the matching 128 up rows; down: 256 outputs);
-//  * both operands are staged through LDS, two stages of 128 K each, loaded with
-//    global_load_lds_dwordx4 (no register staging); 16-byte chunks are XOR-
-//    swizzled by row so the 32-lane fragment reads hit distinct banks;
-//  * wave w owns rows [32 w, +32) and all 256 columns as 8
-//    v_mfma_f32_32x32x64_f8f6f4 tiles; per 128-K scale block two MFMAs form the
-//    raw product, then acc += part * (s_a[row] * s_w) promotes it in fp32 (the
-//    combined scale per row and column half is precomputed into LDS);
-//  * for gate_up a wave holds the gate and the up columns of the same 128 h
-//    columns, so SiLU(g) * u, the row amax of the 1x128 quantization group and
-//    the requantization are wave-local;
+//  * both operands are staged through LDS in three stages of 128 K each (two K
+//    blocks of lookahead), loaded with global_load_lds_dwordx4 (no register
+//    staging); 16-byte chunks are XOR-swizzled by row pairs so 16-lane fragment
+//    reads hit distinct banks of the 64-bank LDS;
+//  * wave (wm, wn) owns rows [32 wm, +32) and 128 columns as 2 x 8 tiles of
+//    v_mfma_f32_16x16x128_f8f6f4: one MFMA per tile covers a whole 128-K scale
+//    block, so the 16 products of a K block are independent and issue back to
+//    back; acc += part * (s_a[row] * s_w) promotes each in fp32 (the combined
+//    scale per row and column half is precomputed into LDS);
+//  * for gate_up wave column half wn holds gate and up columns [64 wn, +64) of
+//    the tile's 128 h columns, so SiLU(g) * u is wave-local and only the row
+//    amax of the 1x128 quantization group is combined across the two halves;
 //  * work items (row tile, column tile) are enumerated expert by expert, column
 //    tile by column tile, and mapped so that one XCD runs the items of one
 //    expert together: the row tiles of an expert share each weight tile through
 //    the XCD's L2, and the column tiles share the activation rows.
 //
-// Fragment lane layout (32x32x64): lane l supplies row l%32 and the 32 bytes
-// [h*64 + (l/32)*32, +32) of the 128-wide K block for MFMA h in {0, 1}; A and B
-// use the same mapping. Accumulator: lane l, register r holds
-// D[8*(r/4) + 4*(l/32) + r%4][l%32].
+// Fragment lane layout (16x16x128): lane l supplies row l%16 and the bytes
+// [(l/16)*16, +16) and [64 + (l/16)*16, +16) of the 128-wide K block, the same
+// mapping for A and B. Accumulator: lane l, register i holds D[4*(l/16) + i][l%16].
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -33,12 +34,12 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 namespace moe {
 
-constexpr int kBM = 256, kBN = 256, kBK = 128;
+constexpr int kBM = 128, kBN = 256, kBK = 128;
 constexpr int kBlkThreads = 512;
-constexpr int kStageA = kBM * kBK;                     // 32 KB
-constexpr int kStageB = kBN * kBK;                     // 32 KB
-constexpr int kStageBytes = kStageA + kStageB + 2 * kBM * 4;  // + s_a * s_w per row, per column half
-constexpr int kBlkLds = 2 * kStageBytes;               // 132 KB
+constexpr int kStages = 3;
+constexpr int kStageA = kBM * kBK;  // 16 KB
+constexpr int kStageB = kBN * kBK;  // 32 KB
+constexpr int kDmaPerWave = (kStageA + kStageB) / 1024 / 8;  // 6 x 1 KB regions per wave
 
 struct BlkArgs {
   const uint8_t* a;
@@ -58,8 +59,9 @@ struct BlkArgs {
   long NB;
 };
 
-__device__ __forceinline__ v16f mfma32_fp8(const v8i& a, const v8i& b, const v16f& c) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+__device__ __forceinline__ v4f mfma16_fp8(const v8i& a, const v8i& b) {
+  const v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -68,26 +70,49 @@ __device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds_wave_base
   __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
 }
 
-__device__ __forceinline__ void wait_vm0() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt[3:0] | [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-// Logical 16-byte chunk c of row r lives at chunk c ^ (r & 7).
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ (row & 7); }
+// Workgroup barrier that waits only for this wave's LDS operations (lgkmcnt),
+// leaving the look-ahead direct-to-LDS loads in flight; __syncthreads() would
+// also drain vmcnt. LDS-DMA data is covered by the explicit vmcnt waits.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt untouched
+  __builtin_amdgcn_s_barrier();
+}
 
-__device__ __forceinline__ v8i lds_frag32(const uint8_t* base, int row, int c0) {
+// Logical 16-byte chunk c of row r lives at chunk c ^ ((r >> 1) & 7): any 16
+// consecutive rows read at one logical chunk touch 16 distinct 16-byte bank
+// groups of the 64-bank LDS (two 128-byte rows span the banks once).
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+// 16x16x128 operand fragment of `row`: logical chunks g and g + 4 (g = lane / 16).
+__device__ __forceinline__ v8i lds_frag16(const uint8_t* base, int row, int g) {
   const uint8_t* rp = base + row * kBK;
-  int4 lo = *(const int4*)(rp + swz(row, c0) * 16);
-  int4 hi = *(const int4*)(rp + swz(row, c0 + 1) * 16);
+  int4 lo = *(const int4*)(rp + swz(row, g) * 16);
+  int4 hi = *(const int4*)(rp + swz(row, g + 4) * 16);
   return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
 template <int KIND>
 __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kBlkLds];
+  // Pipeline stages as distinct objects, so the compiler can tell that fragment
+  // reads of one stage do not alias the direct-to-LDS loads in flight into another.
+  __shared__ __attribute__((aligned(16))) uint8_t sT0[kStageA + kStageB];  // A tile, then B tile
+  __shared__ __attribute__((aligned(16))) uint8_t sT1[kStageA + kStageB];
+  __shared__ __attribute__((aligned(16))) uint8_t sT2[kStageA + kStageB];
+  __shared__ __attribute__((aligned(16))) float sS0[2 * kBM];
+  __shared__ __attribute__((aligned(16))) float sS1[2 * kBM];
+  __shared__ __attribute__((aligned(16))) float sS2[2 * kBM];
   __shared__ int sSrc[kBM];
+  __shared__ float sRed[2][kBM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
   const int Kdim = (KIND == 0) ? p.H : p.I;
   const int KB = Kdim / kBK;
   const int NT = (KIND == 0) ? p.I / 128 : p.H / kBN;
@@ -96,9 +121,9 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   // contiguous item range [x * per, (x + 1) * per).
   const int count = p.num_tiles[0] * NT;
   const int per = (count + 7) / 8;
-  const int j = blockIdx.x >> 3;
-  if (j >= per) return;
-  const int L = (blockIdx.x & 7) * per + j;
+  const int jx = blockIdx.x >> 3;
+  if (jx >= per) return;
+  const int L = (blockIdx.x & 7) * per + jx;
   if (L >= count) return;
   const int2 sg = p.seg[L / NT];
   const int r0 = L - NT * sg.x;
@@ -117,8 +142,8 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     if (r < nrows) {
       const long slot = slot0 + r;
       if (KIND == 0) {
-        long s = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
-        src = (s >= 0 && s < p.T) ? (int)s : -1;
+        long sv = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
+        src = (sv >= 0 && sv < p.T) ? (int)sv : -1;
       } else {
         src = (int)slot;
       }
@@ -127,8 +152,6 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   }
   __syncthreads();
 
-  // Loader assignment: wave w fills the 1 KB regions 4w..4w+3 of each operand
-  // (8 rows per region); lane l writes region byte l*16 = row l/8, stored chunk l%8.
   const uint8_t* wb;
   const float* wsb;
   if (KIND == 0) {
@@ -138,147 +161,215 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     wb = (is_sh ? p.wsh : p.w) + (size_t)ej * p.H * p.I;
     wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (p.H / 128) * KB;
   }
-  uint32_t oa[4], ob[4];
+  // Loader: 48 regions of 1 KB (A: 16, B: 32), 6 per wave: A regions 2w, 2w+1 and
+  // B regions 4w..4w+3. Lane l writes region byte l*16 = row l/8, stored chunk l%8.
+  uint32_t off[kDmaPerWave];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 32 * wave + 8 * i + (lane >> 3);
-    const int c = swz(row, lane & 7);
-    const int src = sSrc[row];
-    oa[i] = (uint32_t)((src >= 0 ? src : 0) * Kdim + c * 16);
-    int wrow;
-    if (KIND == 0)
-      wrow = (row < 128) ? nt * 128 + row : p.I + nt * 128 + (row - 128);
-    else
-      wrow = nt * kBN + row;
-    ob[i] = (uint32_t)(wrow * Kdim + c * 16);
+  for (int i = 0; i < kDmaPerWave; ++i) {
+    if (i < 2) {
+      const int row = 8 * (2 * wave + i) + (lane >> 3);
+      const int src = sSrc[row];
+      off[i] = (uint32_t)((src >= 0 ? src : 0) * Kdim + swz(row, lane & 7) * 16);
+    } else {
+      const int row = 8 * (4 * wave + i - 2) + (lane >> 3);
+      int wrow;
+      if (KIND == 0)
+        wrow = (row < 128) ? nt * 128 + row : p.I + nt * 128 + (row - 128);
+      else
+        wrow = nt * kBN + row;
+      off[i] = (uint32_t)(wrow * Kdim + swz(row, lane & 7) * 16);
+    }
   }
-  // Threads 0..255 own one row's activation scale; threads 256..511 duplicate it
-  // for the second column half. Each writes s_a[row] * s_w[half] per stage.
-  const int srow = tid & (kBM - 1), shalf = tid >> 8;
-  const float* asp = (sSrc[srow] >= 0) ? p.as + (size_t)sSrc[srow] * KB : nullptr;
-  const float* swr;  // weight-scale row of column half `shalf`
+  const uint8_t* abase = p.a;
+  // Scale writers: threads 0..255 own (row tid % 128, column half tid / 128) and
+  // store s_a[row] * s_w[half] for each stage.
+  const int srow = tid & (kBM - 1), shalf = (tid >> 7) & 1;
+  const bool swriter = tid < 2 * kBM;
+  const float amask = (swriter && sSrc[srow] >= 0) ? 1.f : 0.f;
+  const float* asp = p.as + (size_t)(sSrc[srow] >= 0 ? sSrc[srow] : 0) * KB;
+  const float* swr;
   if (KIND == 0)
     swr = wsb + (size_t)(shalf == 0 ? nt : p.I / 128 + nt) * KB;
   else
     swr = wsb + (size_t)(nt * 2 + shalf) * KB;
-  const uint8_t* abase = p.a;
 
-  auto issue = [&](int stage, int kb) {
-    uint8_t* sa = smem + stage * kStageBytes;
+  auto issue = [&](uint8_t* sa, int kb) {
     uint8_t* sb = sa + kStageA;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      load_lds16(abase + oa[i] + (size_t)kb * kBK, sa + (4 * wave + i) * 1024);
-      load_lds16(wb + ob[i] + (size_t)kb * kBK, sb + (4 * wave + i) * 1024);
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      if (i < 2)
+        load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (2 * wave + i) * 1024);
+      else
+        load_lds16(wb + off[i] + (size_t)kb * kBK, sb + (4 * wave + i - 2) * 1024);
     }
   };
-  auto scale_of = [&](int kb) -> float { return asp ? asp[kb] * swr[kb] : 0.f; };
-  auto put_scale = [&](int stage, float v) {
-    ((float*)(smem + stage * kStageBytes + kStageA + kStageB))[shalf * kBM + srow] = v;
-  };
 
-  v16f acc[8];
+  // Accumulators: 2 row tiles (16 rows) x 8 column tiles (16 columns), v_mfma 16x16x128.
+  v4f acc[2][8];
 #pragma unroll
-  for (int n = 0; n < 8; ++n)
+  for (int m = 0; m < 2; ++m)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[n][r] = 0.f;
+    for (int n = 0; n < 8; ++n) acc[m][n] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  const bool active = 32 * wave < nrows;  // this wave's 32-row tile holds rows
-  const int g2 = lane >> 5, l32 = lane & 31;
-  const int arow = 32 * wave + l32;
-
-  issue(0, 0);
-  float asn = scale_of(0);
-  wait_vm0();
-  put_scale(0, asn);
-  __syncthreads();
-
-  for (int kb = 0; kb < KB; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < KB) {
-      issue(cur ^ 1, kb + 1);
-      asn = scale_of(kb + 1);
-    }
-    if (active) {
-      const uint8_t* sa = smem + cur * kStageBytes;
-      const uint8_t* sb = sa + kStageA;
-      const float* ssc = (const float*)(sb + kStageB);
-      const v8i a0 = lds_frag32(sa, arow, 2 * g2);
-      const v8i a1 = lds_frag32(sa, arow, 4 + 2 * g2);
+  const bool active = 32 * wm < nrows;  // this wave's 32 rows hold at least one row
+  const int g = lane >> 4, l16 = lane & 15;
+  // B rows of this wave's eight 16-column tiles. gate_up: tiles 0-3 gate columns
+  // [64 wn, +64), tiles 4-7 the matching up columns; down: columns [128 wn, +128).
+  int brow[8];
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        v16f cs;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const v4f s4 = *(const v4f*)&ssc[hh * kBM + 32 * wave + 8 * q + 4 * g2];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) cs[4 * q + i] = s4[i];
-        }
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const int brow = 128 * hh + 32 * n + l32;
-          const v8i b0 = lds_frag32(sb, brow, 2 * g2);
-          const v8i b1 = lds_frag32(sb, brow, 4 + 2 * g2);
-          v16f part = mfma32_fp8(a0, b0, (v16f){});
-          part = mfma32_fp8(a1, b1, part);
-          acc[4 * hh + n] += part * cs;
-        }
-      }
-    }
-    if (kb + 1 < KB) {
-      wait_vm0();
-      put_scale(cur ^ 1, asn);
-    }
-    __syncthreads();
+  for (int n = 0; n < 8; ++n) {
+    if (KIND == 0)
+      brow[n] = (n < 4) ? 64 * wn + 16 * n + l16 : 128 + 64 * wn + 16 * (n - 4) + l16;
+    else
+      brow[n] = 128 * wn + 16 * n + l16;
   }
 
-  if (!active) return;
-  if (KIND == 0) {
-    const int GI = p.I / 128;
-    float amax[16];
+  auto compute = [&](const uint8_t* sa, const float* ssc) {
+    const uint8_t* sb = sa + kStageA;
+    v8i a[2];
+    v4f cs[2][2];  // [row tile][column half]
 #pragma unroll
-    for (int r = 0; r < 16; ++r) amax[r] = 0.f;
-#pragma unroll
-    for (int n = 0; n < 4; ++n)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float g = acc[n][r], u = acc[n + 4][r];
-        const float h = g / (1.0f + __expf(-g)) * u;
-        acc[n][r] = h;
-        amax[r] = fmaxf(amax[r], fabsf(h));
-      }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float m = amax[r];
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      amax[r] = m;
+    for (int m = 0; m < 2; ++m) {
+      a[m] = lds_frag16(sa, 32 * wm + 16 * m + l16, g);
+      const int r4 = 32 * wm + 16 * m + 4 * g;
+      cs[m][0] = *(const v4f*)&ssc[((KIND == 0) ? 0 : wn) * kBM + r4];
+      cs[m][1] = (KIND == 0) ? *(const v4f*)&ssc[kBM + r4] : cs[m][0];
     }
+    // Two batches of four column tiles. The fragments of batch 1 are requested
+    // before the MFMAs of batch 0 issue, and each batch's eight MFMAs are
+    // independent, so the MFMA pipe is fed back to back while earlier results
+    // get their fp32 promotion. Both row tiles are always computed (branch-free;
+    // a partial last tile wastes at most 16 rows).
+    v8i b0[4], b1[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 32 * wave + 8 * (r >> 2) + 4 * g2 + (r & 3);
-      if (row < nrows && sSrc[row] >= 0) {
-        const long slot = slot0 + row;
-        const float sc = fmaxf(amax[r], 0x1.b7cdfep-34f) / 448.0f;
+    for (int j = 0; j < 4; ++j) b0[j] = lds_frag16(sb, brow[j], g);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b1[j] = lds_frag16(sb, brow[4 + j], g);
+#pragma unroll
+    for (int bt = 0; bt < 2; ++bt) {
+      v4f part[2][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v8i& b = bt == 0 ? b0[j] : b1[j];
+        part[0][j] = mfma16_fp8(a[0], b);
+        part[1][j] = mfma16_fp8(a[1], b);
+      }
+      const int hf = (KIND == 0) ? bt : 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[0][4 * bt + j] += part[0][j] * cs[0][hf];
+        acc[1][4 * bt + j] += part[1][j] * cs[1][hf];
+      }
+    }
+    // Schedule: all LDS fragment reads, the first 8 MFMAs, then each remaining
+    // MFMA followed by the 4 promotion FMAs of an earlier product.
+    __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);   // MFMA
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_group_barrier(0x002, 40, 0);   // VALU
+  };
+
+  // Raw scales ride a 3-slot register ring indexed by the unrolled step position
+  // (no loop-carried copies, which would wait on the loads in flight).
+  float ra[3] = {0.f, 0.f, 0.f}, rw[3] = {0.f, 0.f, 0.f};
+  issue(sT0, 0);
+  if (KB > 1) issue(sT1, 1);
+  ra[0] = asp[0];
+  rw[0] = swr[0];
+  ra[1] = asp[min(1, KB - 1)];
+  rw[1] = swr[min(1, KB - 1)];
+  wait_vm<0>();
+  if (swriter) sS0[shalf * kBM + srow] = ra[0] * rw[0] * amask;
+  __syncthreads();
+
+  // pos = kb % 3; na_: stage of block kb + 2; n1s: scale slot of block kb + 1
+  auto step = [&](int kb, int pos, const uint8_t* ca, const float* cs_, uint8_t* na_,
+                  float* n1s) {
+    // Every step issues the same 8 vector-memory ops (past the last block it
+    // re-reads block KB - 1 into a stage that is not read again), so the
+    // in-order vmcnt wait below is exact on every path.
+    const int kn = min(kb + 2, KB - 1);
+    ra[(pos + 2) % 3] = asp[kn];
+    rw[(pos + 2) % 3] = swr[kn];
+    issue(na_, kn);
+    __builtin_amdgcn_sched_barrier(0);
+    if (active) compute(ca, cs_);
+    __builtin_amdgcn_sched_barrier(0);
+    // Issue order per step: 2 scale loads, then 6 tile loads. Block kb + 1's tile
+    // loads (previous step) are followed by this step's 8 ops.
+    wait_vm<2 + kDmaPerWave>();
+    if (kb + 1 < KB && swriter) n1s[shalf * kBM + srow] = ra[(pos + 1) % 3] * rw[(pos + 1) % 3] * amask;
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int kb = 0; kb < KB; kb += 3) {
+    step(kb, 0, sT0, sS0, sT2, sS1);
+    if (kb + 1 < KB) step(kb + 1, 1, sT1, sS1, sT0, sS2);
+    if (kb + 2 < KB) step(kb + 2, 2, sT2, sS2, sT1, sS0);
+  }
+  __syncthreads();
+
+  // Accumulator layout (16x16): lane l, register i holds D[4*(l/16) + i][l%16].
+  if (KIND == 0) {
+    // h = SiLU(gate) * up for this wave's 64 h columns; the row amax of the 1x128
+    // group combines the two column-half waves through LDS.
+    const int GI = p.I / 128;
+    float amax[2][4];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float mx = 0.f;
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          const float yv = fminf(fmaxf(acc[n][r] / sc, -448.0f), 448.0f);
-          p.hq[(size_t)slot * p.I + nt * 128 + 32 * n + l32] = (uint8_t)f32_to_e4m3fn(yv);
+          const float gt = acc[m][n][i], up = acc[m][n + 4][i];
+          const float h = gt / (1.0f + __expf(-gt)) * up;
+          acc[m][n][i] = h;
+          mx = fmaxf(mx, fabsf(h));
         }
-        if (l32 == 0) p.hs[(size_t)slot * GI + nt] = sc;
-      }
-    }
-  } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 32 * wave + 8 * (r >> 2) + 4 * g2 + (r & 3);
-      if (row < nrows) {
-        const long slot = slot0 + row;
-#pragma unroll
-        for (int n = 0; n < 8; ++n)
-          p.y[(size_t)slot * p.H + nt * kBN + 32 * n + l32] = f32_to_bf16_bits(acc[n][r]);
+        for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        amax[m][i] = mx;
+        if (l16 == 0) sRed[wn][32 * wm + 16 * m + 4 * g + i] = mx;
       }
+    __syncthreads();
+    if (active) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 32 * wm + 16 * m + 4 * g + i;
+          if (row < nrows && sSrc[row] >= 0) {
+            const long slot = slot0 + row;
+            const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+              const float yv = fminf(fmaxf(acc[m][n][i] / sc, -448.0f), 448.0f);
+              p.hq[(size_t)slot * p.I + nt * 128 + 64 * wn + 16 * n + l16] = (uint8_t)f32_to_e4m3fn(yv);
+            }
+            if (wn == 0 && l16 == 0) p.hs[(size_t)slot * GI + nt] = sc;
+          }
+        }
     }
+    (void)amax;
+  } else if (active) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 32 * wm + 16 * m + 4 * g + i;
+        if (row < nrows) {
+          const long slot = slot0 + row;
+#pragma unroll
+          for (int n = 0; n < 8; ++n)
+            p.y[(size_t)slot * p.H + nt * kBN + 128 * wn + 16 * n + l16] = f32_to_bf16_bits(acc[m][n][i]);
+        }
+      }
   }
 }
 
