@@ -39,6 +39,27 @@ def expert_bytes(H, I, part):
     return H * I + 4 * (H // 128) * (I // 128)
 
 
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "expert_gemm_dsv3_hbm_traffic_pmc.md")
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed counter
+    summary (rocprofv3 FETCH_SIZE and WRITE_SIZE passes, each scaled by its
+    calibration factor against a plain copy kernel); None when absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if not line.startswith("traffic:"):
+                    continue
+                kv = dict(t.split("=", 1) for t in line.split()[1:])
+                if kv.get("kernel") == kernel and kv.get("workload") == workload:
+                    return int((float(kv["fetch_kib"]) * float(kv["fetch_factor"])
+                                + float(kv["write_kib"]) * float(kv["write_factor"])) * 1024)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None
+
+
 def layer_counts(ids, E):
     import torch
     counts = torch.bincount(ids.reshape(-1).long(), minlength=E)
@@ -183,7 +204,8 @@ def main():
                    "active_experts": active, "parallelism": "none (1 GPU, all experts resident)"},
         "roofline": {"bound": "hbm", "kernel": "expert_gemm_kernel gate_up (decode)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("expert_gemm_kernel<16,0,3>", "decode64"),
                      "alg_bytes_per_launch": gu_bytes, "avg_launch_ms": round(gu_ms, 4)},
         "layer": {"alg_bytes": layer_bytes, "alg_flops": layer_flops,
                   "hbm_GBs": round(layer_bytes / sec / 1e9, 1),

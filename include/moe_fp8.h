@@ -63,6 +63,24 @@ int moe_router_logits(const void* x_bf16, const void* router_w_bf16, const float
                       int H, int E, float* logits, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* The same product with fp32 hidden states (router_w fp32 if w_is_f32, else
+ * bf16; [E,H]); fp32 v_mfma_f32_16x16x4f32, fp32 accumulation. For router()
+ * when its operands are not bf16-exact: router.py:236 casts hidden_states to
+ * the fp32 computation dtype before the optional RMSNorm (router.py:409-410),
+ * so F.linear (router.py:418-424) sees fp32 operands. Workspace size as
+ * moe_router_logits_workspace_bytes. H % 64 == 0. */
+int moe_router_logits_f32(const float* x, const void* router_w, int w_is_f32, const float* bias,
+                          int T, int H, int E, float* logits, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* RMSNorm over rows of x [T,H] (bf16, or fp32 if x_is_f32):
+ * y = (x * 1/sqrt(mean(x[:hidden_actual]^2) + eps)) * gamma for columns <
+ * hidden_actual, 0 beyond; fp32 math, out bf16 (or fp32 if out_is_f32).
+ * gamma fp32 [H]. Replaces _torch_rms_norm (router.py:681-688) and the
+ * RMSNorm step of moe_block_tkg (moe_block_tkg.py:135-151). */
+int moe_rms_norm(const void* x, int x_is_f32, const float* gamma, int T, int H, int hidden_actual,
+                 float eps, void* out, int out_is_f32, void* stream);
+
 /* Top-k selection + activation (+ renorm, * routed_scale) from fp32 logits.
  * ids/weights [T,K] in descending key order (ties -> lower expert index);
  * affinities [T,E] (optional, NULL to skip) is the dense scatter the reference

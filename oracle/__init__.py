@@ -31,6 +31,12 @@ Parity status per function (what pins it):
 * moe.*                          float64 brute force on tiny shapes, dense == sparse form,
                                  linearity, permutation invariance
 * moe.topk_reduce                docstring example of topk_reduce.py:70-82 (KAT)
+* router.rms_norm_padded         constant rows (closed form), scale invariance at eps 0,
+                                 equals rms_norm at hidden_actual = H, zero padding
+* router.route_topk_scatter_act  same ids as a full sort; softmax weights equal the float64
+                                 softmax of the selected logits; sigmoid rows 0 off the top-k
+* moe.moe_block_tkg_fp8          NO_SCALE over all experts equals the dense all-expert form
+                                 (moe_dense_reference, unit affinities); token permutation
 
 The nkilib device kernels the reference calls (router_topk,
 find_nonzero_indices, indexed_flatten, moe_cte, moe_block_tkg) are absent

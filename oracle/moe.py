@@ -12,6 +12,10 @@
                           (moe_block_tkg.py:314-316, kernel-only in the reference) added
                           with weight 1.
 * topk_reduce          <- _cpu_topk_reduce, vllm_neuron/functional/moe/topk_reduce.py:144-159.
+* moe_block_tkg_fp8    <- _torch_moe_block_tkg_impl, vllm_neuron/functional/moe/moe_block_tkg.py:57-303
+                          (RMSNorm -> fp32 router -> pre/post-norm selection -> experts on
+                          the normalized input, NO_SCALE or POST_SCALE), composed from the
+                          functions above and the router oracle.
 """
 import numpy as np
 
@@ -104,3 +108,27 @@ def topk_reduce(inp_rows, token_ids_1based, T):
     b = np.clip(np.asarray(token_ids_1based, np.int64), 0, None)
     np.add.at(out, b, np.asarray(inp_rows, F))
     return out[1:]
+
+
+def moe_block_tkg_fp8(x, gamma, eps, w_router_eh, router_bias, k, scoring, pre_norm,
+                      norm_topk_prob, post_scale, w13_q, w13_s, w2_q, w2_s, shared=None,
+                      hidden_actual=None, logits=None):
+    """_torch_moe_block_tkg_impl (moe_block_tkg.py:57-303) with fp8 128x128 experts and a
+    shared expert of weight 1: RMSNorm (padded columns 0) cast to bf16 -> fp32 router
+    matmul (+ bias) -> pre_norm: activation then top-k, else top-k then activation
+    (norm_topk_prob: / (sum + 1e-20)) -> experts on the normalized input, NO_SCALE weight
+    1 or POST_SCALE affinity. ``logits`` (optional) replaces the router matmul so that a
+    selection made from GPU logits can be compared exactly. Returns
+    (out fp32 before the final cast, logits, ids, weights)."""
+    from .router import (SOFTMAX, rms_norm_padded, route_act_topk_renorm, route_topk_act,
+                         router_logits)
+    xn = bf16_round(rms_norm_padded(x, gamma, eps, hidden_actual))
+    if logits is None:
+        logits = router_logits(xn, w_router_eh, router_bias)
+    route = route_act_topk_renorm if pre_norm else route_topk_act
+    ids, w = route(logits, k, scoring, norm_topk_prob, 1e-20, 1.0)
+    if not post_scale:
+        w = np.ones_like(w)
+    out = moe_sparse_fp8(xn, ids, w, w13_q, w13_s, w2_q, w2_s, shared=shared)
+    return out, logits, ids, w
+

@@ -6,7 +6,9 @@ Follows the torch fallbacks of vllm_neuron/functional/moe/router.py:
                                  and the router_pre_norm branch of moe_block_tkg.py:165-185
   * route_grouped             <- not in the reference: DeepSeek-V3 "noaux_tc" grouped top-k
                                  (sigmoid + selection-only correction bias + group top-2 sum)
-  * rms_norm                  <- _torch_rms_norm, router.py:681-688 / moe_block_tkg.py:135-151
+  * route_topk_scatter_act    <- _torch_router_impl_prenorm_linear_topk_scatter_act, router.py:507-566
+  * rms_norm                  <- _torch_rms_norm, router.py:681-688
+  * rms_norm_padded           <- the RMSNorm step of _torch_moe_block_tkg_impl, moe_block_tkg.py:135-151
 
 Tie rule everywhere: equal keys select the lower expert (or group) index,
 and the K outputs are ordered by descending key.
@@ -26,6 +28,19 @@ def rms_norm(x, gamma, eps):
     x = np.asarray(x, dtype=F)
     var = np.mean(x.astype(F) ** 2, axis=-1, keepdims=True, dtype=F)
     return (x * (F(1.0) / np.sqrt(var + F(eps))).astype(F) * np.asarray(gamma, F)).astype(F)
+
+
+def rms_norm_padded(x, gamma, eps, hidden_actual=None):
+    """moe_block_tkg.py:135-151: mean of squares over the first hidden_actual columns; those
+    columns become (x * rsqrt(var + eps)) * gamma, the rest 0 (the caller casts back)."""
+    x = np.asarray(x, F)
+    H = x.shape[-1]
+    ha = H if hidden_actual is None else int(hidden_actual)
+    var = np.mean(x[..., :ha] ** 2, axis=-1, keepdims=True, dtype=F)
+    r = (F(1.0) / np.sqrt((var + F(eps)).astype(F))).astype(F)
+    y = np.zeros_like(x)
+    y[..., :ha] = ((x[..., :ha] * r).astype(F) * np.asarray(gamma, F).reshape(-1)[:ha]).astype(F)
+    return y
 
 
 def router_logits(x, w_eh, bias=None):
@@ -99,6 +114,25 @@ def route_act_topk_renorm(logits, k, scoring=SOFTMAX, renorm=True, eps=0.0, scal
         w = _renorm(w, eps)
     w = (w * F(scale)).astype(F)
     return ids, w
+
+
+def route_topk_scatter_act(logits, k, scoring=SOFTMAX):
+    """router.py:507-566: top-k of the raw logits scattered into a row of -inf, then the
+    activation over the full row (softmax: sum left to right over E; sigmoid(-inf) = 0).
+    Returns the dense affinities [T, E]."""
+    logits = np.asarray(logits, F)
+    ids = topk_desc(logits, k).astype(np.int64)
+    full = np.full(logits.shape, -np.inf, F)
+    np.put_along_axis(full, ids, np.take_along_axis(logits, ids, axis=1), axis=1)
+    if scoring == SOFTMAX:
+        m = np.max(full, axis=-1, keepdims=True)
+        e = np.where(np.isinf(full), F(0), exp_f32(np.where(np.isinf(full), F(0), full - m)))
+        e = e.astype(F)
+        s = np.zeros(full.shape[0], F)
+        for j in range(full.shape[1]):
+            s = (s + e[:, j]).astype(F)
+        return (e / s[:, None]).astype(F)
+    return np.where(np.isinf(full), F(0), sigmoid_f32(np.where(np.isinf(full), F(0), full)))
 
 
 def route_grouped(logits, bias, k, n_group, topk_group, scoring=SIGMOID, renorm=True,

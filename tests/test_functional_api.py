@@ -1,0 +1,101 @@
+"""Host-side behaviour of the operator mirrors (no GPU): argument validation raises
+the reference's exception types before any kernel runs (router.py:602-678 ValueError;
+moe_block_tkg.py:534-565 / moe_cte.py:300-313 NotImplementedError), and CPU tensors
+are refused (no CPU path)."""
+import pytest
+import torch
+
+from vllm_neuron_amd.functional import moe as M
+
+FP8 = torch.float8_e4m3fn
+
+
+def _router_args(T=4, H=128, E=8):
+    return torch.zeros(T, H, dtype=torch.bfloat16), torch.zeros(H, E, dtype=torch.bfloat16)
+
+
+@pytest.mark.parametrize("mutate, exc", [
+    (lambda a: dict(a, hidden_states=torch.zeros(2, 4, 128)), ValueError),
+    (lambda a: dict(a, router_weights=torch.zeros(64, 8)), ValueError),
+    (lambda a: dict(a, top_k=0), ValueError),
+    (lambda a: dict(a, top_k=9), ValueError),
+    (lambda a: dict(a, router_bias=torch.zeros(7)), ValueError),
+    (lambda a: dict(a, gamma=torch.zeros(64)), ValueError),
+    (lambda a: dict(a, computation_dtype=torch.int32), ValueError),
+    (lambda a: dict(a, router_computation_order="prenorm_linear_topk_act_scatter"), ValueError),
+    (lambda a: dict(a, activation="relu"), ValueError),
+    (lambda a: dict(a, activation=3), ValueError),
+    (lambda a: dict(a, activation=torch.sigmoid), NotImplementedError),
+])
+def test_router_validation(mutate, exc):
+    x, w = _router_args()
+    args = dict(hidden_states=x, router_weights=w, top_k=2)
+    with pytest.raises(exc):
+        M.router(**mutate(args))
+
+
+def test_router_refuses_cpu_tensors():
+    x, w = _router_args()
+    with pytest.raises(RuntimeError, match="GPU"):
+        M.router(x, w, 2)
+
+
+def test_transposed_hidden_states_shape_check():
+    x, w = _router_args()
+    with pytest.raises(ValueError):
+        M.router(x, w, 2, transposed_hidden_states=True)   # [T,H] read as [H,T]
+
+
+def _experts(E=2, H=256, I=128):
+    return torch.zeros(E, H, 2, I, dtype=FP8), torch.zeros(E, I, H, dtype=FP8)
+
+
+@pytest.mark.parametrize("kw", [
+    dict(implementation=M.MoECTEImplementation.shard_on_block_mx),
+    dict(quantization_type=M.QuantizationType.MX),
+    dict(activation_function=M.ActFnType.GELU),
+    dict(expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.PRE_SCALE),
+    dict(gate_clamp_upper_limit=8.0),
+    dict(gate_and_up_proj_bias=torch.zeros(2, 2, 128), down_proj_bias=torch.zeros(2, 256)),
+    dict(ep_degree=2),
+])
+def test_moe_cte_unsupported_options(kw):
+    gu, dn = _experts()
+    base = dict(hidden_states=torch.zeros(4, 256, dtype=torch.bfloat16),
+                expert_affinities_masked=torch.zeros(8, 1), gate_up_proj_weight=gu,
+                down_proj_weight=dn, token_position_to_id=torch.zeros(512, dtype=torch.int32),
+                block_to_expert=torch.zeros(2, dtype=torch.int32), block_size=256,
+                implementation=M.MoECTEImplementation.shard_on_block)
+    base.update(kw)
+    with pytest.raises(NotImplementedError):
+        M.moe_cte(**base)
+
+
+def test_moe_cte_rejects_unquantized_experts():
+    with pytest.raises(NotImplementedError, match="float8_e4m3fn"):
+        M.moe_cte(torch.zeros(4, 256), torch.zeros(8, 1), torch.zeros(2, 256, 2, 128),
+                  torch.zeros(2, 128, 256), torch.zeros(512, dtype=torch.int32),
+                  torch.zeros(2, dtype=torch.int32), 256, M.MoECTEImplementation.shard_on_block)
+
+
+def test_blockwise_mapping_arguments():
+    aff = torch.zeros(4, 8)
+    with pytest.raises(NotImplementedError):
+        M.build_blockwise_mapping(aff, 8, 2, 256, tp_degree=2)
+    with pytest.raises(ValueError):
+        M.build_blockwise_mapping(aff, 6, 2, 256)
+
+
+def test_moe_block_tkg_unsupported_options():
+    gu, dn = _experts()
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    g = torch.ones(256)
+    wr = torch.zeros(256, 2, dtype=torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="placeholders"):
+        M.moe_block_tkg(x, g, wr, gu, dn, hidden_act_scale_factor=1.0)
+    with pytest.raises(NotImplementedError):
+        M.moe_block_tkg(x, g, wr, gu, dn, residual=x)
+    with pytest.raises(NotImplementedError):
+        M.moe_block_tkg(x, g, wr, gu, dn, hidden_act_fn=M.ActFnType.Swish)
+    with pytest.raises(NotImplementedError):   # 2 local experts of 4 routed
+        M.moe_block_tkg(x, g, torch.zeros(256, 4, dtype=torch.bfloat16), gu, dn)

@@ -1,0 +1,260 @@
+"""GPU parity of the operator mirrors (vllm_neuron_amd.functional.moe) against the oracle.
+
+Gates: routing, mappings and selections bit-exact when the oracle is fed the GPU's
+logits; fp32 logits and RMSNorm within fp32 rounding of a float64 evaluation; layer
+outputs rel-L2 <= 1e-2 against the fp32-accumulate dequant oracle on the same fp8
+operands."""
+import numpy as np
+import pytest
+import torch
+
+from _util import np_f32, np_u8, oracle_weights, rel_l2, say
+from oracle import blockwise as BW
+from oracle import router as R
+from oracle.fp8 import quant_weight_128x128
+from oracle.moe import bf16_round, moe_block_tkg_fp8, moe_sparse_fp8
+from vllm_neuron_amd import PRESETS, ops, synthetic
+from vllm_neuron_amd.functional import moe as M
+from vllm_neuron_amd.functional.moe import _experts
+
+pytestmark = pytest.mark.gpu
+TOL_REL_L2 = 1e-2
+
+
+def _small(cuda, seed=0):
+    cfg = PRESETS["small"]
+    return cfg, synthetic.make_weights(cfg, seed, device=cuda)
+
+
+def _nf(w):
+    """Stacked device layout -> the reference operator layout (and block scales)."""
+    E, I2, H = w.w13.shape
+    I = I2 // 2
+    gu = w.w13.view(torch.uint8).reshape(E, 2, I, H).permute(0, 3, 1, 2).contiguous()
+    gs = w.w13_scale.reshape(E, 2, I // 128, H // 128).permute(0, 3, 1, 2).contiguous()
+    dn = w.w2.view(torch.uint8).transpose(1, 2).contiguous()
+    ds = w.w2_scale.transpose(1, 2).contiguous()
+    return gu.view(torch.float8_e4m3fn), gs, dn.view(torch.float8_e4m3fn), ds
+
+
+def _ids_weights_from_dense(aff):
+    """Selected experts of each row (ascending) and their affinities."""
+    a = np_f32(aff)
+    K = int((a != 0).sum(1).max())
+    ids = np.zeros((a.shape[0], K), np.int32)
+    wts = np.zeros((a.shape[0], K), np.float32)
+    for t in range(a.shape[0]):
+        nz = np.nonzero(a[t])[0]
+        ids[t, :len(nz)] = nz
+        wts[t, :len(nz)] = a[t, nz]
+    return ids, wts
+
+
+# ---------------------------------------------------------------- kernels
+
+@pytest.mark.parametrize("x_dtype, out_dtype, ha", [
+    (torch.bfloat16, torch.bfloat16, None), (torch.bfloat16, torch.bfloat16, 1000),
+    (torch.float32, torch.float32, None), (torch.float32, torch.bfloat16, 777)])
+def test_rms_norm_kernel(cuda, x_dtype, out_dtype, ha):
+    say("rms_norm", x_dtype, out_dtype, ha)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(37, 1024, generator=g) * 3).to(x_dtype).to(cuda)
+    gamma = (1 + 0.1 * torch.randn(1024, generator=g)).to(cuda)
+    y = ops.rms_norm(x, gamma, 1e-6, ha, out_dtype=out_dtype)
+    ref = R.rms_norm_padded(np_f32(x), np_f32(gamma), 1e-6, ha)
+    got = np_f32(y)
+    if out_dtype == torch.float32:
+        assert np.allclose(got, ref, rtol=2e-6, atol=1e-30)
+    else:  # within one bf16 rounding of the fp32 result
+        assert np.allclose(got, bf16_round(ref), rtol=2 ** -7, atol=0)
+    if ha is not None:
+        assert np.all(got[:, ha:] == 0)
+
+
+@pytest.mark.parametrize("T, H, E, w_dtype", [(100, 512, 40, torch.float32),
+                                             (3000, 512, 40, torch.bfloat16),
+                                             (7, 128, 96, torch.float32), (1, 1024, 8, torch.bfloat16)])
+def test_router_logits_f32(cuda, T, H, E, w_dtype):
+    say("router_logits_f32", T, H, E, w_dtype)
+    g = torch.Generator().manual_seed(T + H)
+    x = torch.randn(T, H, generator=g).to(cuda)
+    w = (0.05 * torch.randn(E, H, generator=g)).to(w_dtype).to(cuda)
+    b = torch.randn(E, generator=g).to(cuda)
+    got = np_f32(ops.router_logits_f32(x, w, b))
+    ref = np_f32(x).astype(np.float64) @ np_f32(w).astype(np.float64).T + np_f32(b)
+    scale = np.abs(np_f32(x)).astype(np.float64) @ np.abs(np_f32(w)).astype(np.float64).T
+    assert np.all(np.abs(got - ref) <= 1e-6 * scale + 1e-6), np.max(np.abs(got - ref) / (scale + 1))
+
+
+# ---------------------------------------------------------------- router()
+
+ORDERS = [M.RouterComputationOrder.PRENORM_LINEAR_TOPK_ACT_SCATTER,
+          M.RouterComputationOrder.PRENORM_LINEAR_ACT_TOPK_RENORM_SCATTER,
+          M.RouterComputationOrder.PRENORM_LINEAR_TOPK_SCATTER_ACT]
+
+
+@pytest.mark.parametrize("order", ORDERS, ids=lambda o: o.name)
+@pytest.mark.parametrize("activation", ["softmax", "sigmoid"])
+@pytest.mark.parametrize("with_gamma", [False, True])
+def test_router_api(cuda, order, activation, with_gamma):
+    say("router", order.name, activation, with_gamma)
+    g = torch.Generator().manual_seed(3)
+    T, H, E, K = 77, 512, 24, 4
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(cuda)
+    w_param = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16).to(cuda)
+    bias = (0.1 * torch.randn(E, generator=g)).to(cuda)
+    gamma = (1 + 0.1 * torch.randn(H, generator=g)).to(cuda) if with_gamma else None
+    aff, lg = M.router(x, w_param.t(), K, router_bias=bias, activation=activation,
+                       return_logits=True, gamma=gamma, router_computation_order=order)
+    assert aff.shape == (T, E) and lg.shape == (T, E) and aff.dtype == torch.float32
+    xs = np_f32(x)
+    if with_gamma:
+        xs = R.rms_norm(xs, np_f32(gamma), 1e-6)   # fp32 normalization, fp32 operands
+    ref_lg = R.router_logits(xs, np_f32(w_param), np_f32(bias))
+    lg = np_f32(lg)
+    assert np.allclose(lg, ref_lg, rtol=1e-5, atol=1e-5)
+    sc = R.SOFTMAX if activation == "softmax" else R.SIGMOID
+    a = np_f32(aff)
+    if order == ORDERS[0]:
+        ids, wts = R.route_topk_act(lg, K, sc)
+        assert np.array_equal(a, R.scatter_dense(ids, wts, E))
+    elif order == ORDERS[1]:
+        ids, wts = R.route_act_topk_renorm(lg, K, sc, True, 0.0)
+        assert np.array_equal(a, R.scatter_dense(ids, wts, E))
+    else:
+        ref = R.route_topk_scatter_act(lg, K, sc)
+        assert np.array_equal(a != 0, ref != 0)
+        assert np.allclose(a, ref, rtol=1e-6, atol=0)
+
+
+def test_router_bf16_computation(cuda):
+    say("router bf16 computation dtype")
+    g = torch.Generator().manual_seed(4)
+    T, H, E, K = 50, 256, 16, 2
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(cuda)
+    w_param = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16).to(cuda)
+    aff, lg = M.router(x, w_param.t(), K, return_logits=True, computation_dtype=torch.bfloat16)
+    assert aff.dtype == torch.bfloat16 and lg.dtype == torch.bfloat16
+    lgf = np_f32(lg)   # logits rounded to bf16 before selection
+    ids, wts = R.route_topk_act(lgf, K, R.SOFTMAX)
+    assert np.array_equal(np_f32(aff), bf16_round(R.scatter_dense(ids, wts, E)))
+
+
+# ---------------------------------------------------------------- mapping / experts
+
+def test_build_blockwise_mapping_api(cuda):
+    say("build_blockwise_mapping api")
+    cfg, w = _small(cuda)
+    x = synthetic.hidden_states(64, cfg.hidden, 0).to(cuda)
+    aff = M.router(x, w.router_w.t(), cfg.top_k)
+    pm = torch.ones(64, dtype=torch.bool)
+    pm[60:] = False
+    for mask in (None, pm.to(cuda)):
+        am, tpid, b2e, cond = M.build_blockwise_mapping(aff, cfg.n_experts, cfg.top_k, 256,
+                                                        padding_mask=mask)
+        ref = BW.build_blockwise_mapping(np_f32(aff), cfg.n_experts, cfg.top_k, 256,
+                                         None if mask is None else mask.cpu().numpy())
+        for got, exp in zip((am, tpid, b2e, cond), ref):
+            assert np.array_equal(got.cpu().numpy().reshape(-1), np.asarray(exp).reshape(-1))
+
+
+@pytest.mark.parametrize("T", [64, 2048])
+def test_moe_cte_api(cuda, T):
+    say("moe_cte api T", T)
+    cfg, w = _small(cuda, 1)
+    E, K = cfg.n_experts, cfg.top_k
+    x = synthetic.hidden_states(T, cfg.hidden, 1).to(cuda)
+    aff = M.router(x, w.router_w.t(), K)
+    am, tpid, b2e, cond = M.build_blockwise_mapping(aff, E, K, 256)
+    gu, gs, dn, ds = _nf(w)
+    impl = M.MoECTEImplementation.shard_on_block
+    out = M.moe_cte(x, am, gu, dn, tpid, b2e, 256, impl, gate_up_proj_scale=gs,
+                    down_proj_scale=ds)
+    out_stacked = M.moe_cte(x, am, w.w13, w.w2, tpid, b2e, 256, impl,
+                            gate_up_proj_scale=w.w13_scale, down_proj_scale=w.w2_scale)
+    assert torch.equal(out, out_stacked)
+    # [T+1, H] hidden states: the last row is a padding sink and is not returned
+    xp = torch.cat([x, torch.zeros_like(x[:1])])
+    assert torch.equal(M.moe_cte(xp, am, gu, dn, tpid, b2e, 256, impl, gate_up_proj_scale=gs,
+                                 down_proj_scale=ds), out)
+    ids, wts = _ids_weights_from_dense(aff)
+    q13, s13, q2, s2 = oracle_weights(w)
+    ref = moe_sparse_fp8(np_f32(x), ids, wts, q13, s13, q2, s2)
+    err = rel_l2(np_f32(out), ref)
+    say("moe_cte rel_l2", err)
+    assert err <= TOL_REL_L2
+    no = M.moe_cte(x, am, gu, dn, tpid, b2e, 256, impl, gate_up_proj_scale=gs,
+                   down_proj_scale=ds,
+                   expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.NO_SCALE)
+    ref_no = moe_sparse_fp8(np_f32(x), ids, np.ones_like(wts), q13, s13, q2, s2)
+    assert rel_l2(np_f32(no), ref_no) <= TOL_REL_L2
+
+
+def test_moe_tkg_api(cuda):
+    say("moe_tkg api")
+    cfg, w = _small(cuda, 2)
+    E, K = cfg.n_experts, cfg.top_k
+    x = synthetic.hidden_states(32, cfg.hidden, 2).to(cuda)
+    aff = M.router(x, w.router_w.t(), K)
+    ids, _ = ops.router_topk(ops.router_logits(x, w.router_w), K, ops.ORDER_TOPK_ACT, "softmax")
+    gu, gs, dn, ds = _nf(w)
+    kw = dict(expert_gate_up_weights_scale=gs, expert_down_weights_scale=ds)
+    post = M.moe_tkg(x, gu, dn, aff, ids, False,
+                     expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.POST_SCALE, **kw)
+    no = M.moe_tkg(x, gu, dn, aff, ids, False, **kw)
+    q13, s13, q2, s2 = oracle_weights(w)
+    idn = ids.cpu().numpy()
+    wts = np.take_along_axis(np_f32(aff), idn.astype(np.int64), 1)
+    assert rel_l2(np_f32(post), moe_sparse_fp8(np_f32(x), idn, wts, q13, s13, q2, s2)) <= TOL_REL_L2
+    assert rel_l2(np_f32(no), moe_sparse_fp8(np_f32(x), idn, np.ones_like(wts), q13, s13, q2,
+                                             s2)) <= TOL_REL_L2
+    # all-expert schedule with unselected experts masked: K = E rows per token (another
+    # tile height), the same layer
+    allx = M.moe_tkg(x, gu, dn, aff, ids, True, mask_unselected_experts=True,
+                     expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.POST_SCALE, **kw)
+    assert rel_l2(np_f32(allx), moe_sparse_fp8(np_f32(x), idn, wts, q13, s13, q2, s2)) <= TOL_REL_L2
+    assert rel_l2(np_f32(allx), np_f32(post)) <= 1e-3
+
+
+@pytest.mark.parametrize("act, pre_norm, norm_topk, post, ha", [
+    (M.RouterActFnType.SIGMOID, True, True, True, None),
+    (M.RouterActFnType.SOFTMAX, False, False, False, 1000),
+    (M.RouterActFnType.SOFTMAX, True, False, True, None)])
+def test_moe_block_tkg_api(cuda, act, pre_norm, norm_topk, post, ha):
+    say("moe_block_tkg", act.name, pre_norm, norm_topk, post, ha)
+    cfg, w = _small(cuda, 3)
+    E, K, H, I = cfg.n_experts, cfg.top_k, cfg.hidden, cfg.intermediate
+    g = torch.Generator().manual_seed(9)
+    x = synthetic.hidden_states(24, H, 3).to(cuda).reshape(2, 12, H)   # [B, S, H]
+    gamma = (1 + 0.1 * torch.randn(1, H, generator=g)).to(cuda)
+    bias = (0.1 * torch.randn(1, E, generator=g)).to(cuda)
+    sh = [(0.02 * torch.randn(*s, generator=g)).to(torch.bfloat16).to(cuda)
+          for s in ((H, I), (H, I), (I, H))]
+    gu, gs, dn, ds = _nf(w)
+    mode = M.ExpertAffinityScaleMode.POST_SCALE if post else M.ExpertAffinityScaleMode.NO_SCALE
+    out, lg = M.moe_block_tkg(x, gamma, w.router_w.t(), gu, dn, top_k=K, shared_expert_gate_w=sh[0],
+                              shared_expert_up_w=sh[1], shared_expert_down_w=sh[2],
+                              expert_gate_up_weights_scale=gs, expert_down_weights_scale=ds,
+                              router_bias=bias, router_act_fn=act, router_pre_norm=pre_norm,
+                              norm_topk_prob=norm_topk, expert_affinities_scaling_mode=mode,
+                              hidden_actual=ha)
+    assert out.shape == (24, H) and out.dtype == torch.bfloat16
+    # shared expert quantization (weight preparation) equals the oracle's 128x128 quantizer
+    sq = _experts.shared_weights(sh[0], sh[1], sh[2], I)
+    q13_ref, s13_ref = quant_weight_128x128(np.concatenate([np_f32(sh[0]).T, np_f32(sh[1]).T]))
+    assert np.array_equal(np_u8(sq[0][0]), q13_ref) and np.array_equal(np_f32(sq[1][0]), s13_ref)
+    shared = (np_u8(sq[0][0]), np_f32(sq[1][0]), np_u8(sq[2][0]), np_f32(sq[3][0]))
+    xs = np_f32(x.reshape(24, H))
+    sc = R.SOFTMAX if act == M.RouterActFnType.SOFTMAX else R.SIGMOID
+    lg = np_f32(lg)
+    ref_out, ref_lg, _, _ = moe_block_tkg_fp8(xs, np_f32(gamma), 1e-6, np_f32(w.router_w),
+                                              np_f32(bias).reshape(-1), K, sc, pre_norm,
+                                              norm_topk, post, *oracle_weights(w), shared=shared,
+                                              hidden_actual=ha)
+    assert np.allclose(lg, ref_lg, rtol=1e-4, atol=1e-4)
+    ref_sel, _, _, _ = moe_block_tkg_fp8(xs, np_f32(gamma), 1e-6, np_f32(w.router_w), None, K, sc,
+                                         pre_norm, norm_topk, post, *oracle_weights(w),
+                                         shared=shared, hidden_actual=ha, logits=lg)
+    err = rel_l2(np_f32(out), ref_sel)
+    say("moe_block_tkg rel_l2", err)
+    assert err <= TOL_REL_L2

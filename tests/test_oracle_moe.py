@@ -87,3 +87,63 @@ def test_topk_reduce_docstring_examples():
     rows8 = np.arange(32, dtype=np.float32).reshape(8, 4)
     out = topk_reduce(rows8, [1, -1, 1, 2, -1, -1, 2, -1], 2)
     assert np.array_equal(out, np.stack([rows8[0] + rows8[2], rows8[3] + rows8[6]]))
+
+
+def _block_case(seed, T=10, H=256, I=128, E=4):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    gamma = rng.normal(1, 0.1, H).astype(np.float32)
+    wr = (rng.normal(0, 0.05, (E, H))).astype(np.float32)
+    q13, s13, q2, s2 = [], [], [], []
+    for _ in range(E):
+        a, sa = quant_weight_128x128(rng.normal(0, 0.02, (2 * I, H)).astype(np.float32))
+        b, sb = quant_weight_128x128(rng.normal(0, 0.02, (H, I)).astype(np.float32))
+        q13.append(a), s13.append(sa), q2.append(b), s2.append(sb)
+    return x, gamma, wr, (np.stack(q13), np.stack(s13), np.stack(q2), np.stack(s2))
+
+
+def test_block_tkg_no_scale_all_experts_is_the_dense_form():
+    from oracle.moe import bf16_round, moe_block_tkg_fp8
+    from oracle.router import SOFTMAX, rms_norm_padded
+    x, gamma, wr, (q13, s13, q2, s2) = _block_case(21)
+    E, H, I = q13.shape[0], x.shape[1], q13.shape[1] // 2
+    out, _, ids, w = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, E, SOFTMAX, True, False, False,
+                                       q13, s13, q2, s2)
+    assert np.all(w == 1)
+    xn = bf16_round(rms_norm_padded(x, gamma, 1e-6))
+    gu = np.stack([dequant_weight_128x128(q13[e], s13[e]).T.reshape(H, 2, I) for e in range(E)])
+    dn = np.stack([dequant_weight_128x128(q2[e], s2[e]).T for e in range(E)])
+    dense = moe_dense_reference(xn, np.ones((x.shape[0] * E, 1), np.float32), gu, dn)
+    # the dense form has unquantized activations: fp8 activation error only
+    err = np.linalg.norm(out - dense) / np.linalg.norm(dense)
+    assert err < 5e-2, err
+
+
+def test_block_tkg_scaling_modes_and_selection_order():
+    from oracle.moe import moe_block_tkg_fp8
+    from oracle.router import SOFTMAX
+    x, gamma, wr, ws = _block_case(22)
+    T = x.shape[0]
+    # K = 1: POST_SCALE is NO_SCALE times the affinity, exactly
+    no, lg, ids1, _ = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, 1, SOFTMAX, True, False, False, *ws)
+    post, _, ids2, w = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, 1, SOFTMAX, True, False, True, *ws)
+    assert np.array_equal(ids1, ids2)
+    assert np.array_equal(post, (no * w[:, :1]).astype(np.float32))
+    # softmax before top-k: global probabilities (sum < 1); after: softmax of the k (sum 1)
+    _, _, ia, wa = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, 2, SOFTMAX, True, False, True, *ws)
+    _, _, ib, wb = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, 2, SOFTMAX, False, False, True, *ws)
+    assert np.array_equal(ia, ib)
+    assert np.all(wa.sum(1) < 1 - 1e-3) and np.allclose(wb.sum(1), 1, atol=1e-6)
+    # padding columns do not reach the output
+    xp = x.copy()
+    xp[:, 200:] = 50.0
+    a, *_ = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, 2, SOFTMAX, True, True, True, *ws,
+                              hidden_actual=200)
+    b, *_ = moe_block_tkg_fp8(xp, gamma, 1e-6, wr, None, 2, SOFTMAX, True, True, True, *ws,
+                              hidden_actual=200)
+    assert np.array_equal(a, b)
+    # token permutation commutes with the layer
+    p = np.random.default_rng(0).permutation(T)
+    c, *_ = moe_block_tkg_fp8(x[p], gamma, 1e-6, wr, None, 2, SOFTMAX, True, True, True, *ws)
+    d, *_ = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, 2, SOFTMAX, True, True, True, *ws)
+    assert np.array_equal(c, d[p])

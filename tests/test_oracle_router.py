@@ -119,3 +119,41 @@ def test_rms_norm_closed_form():
     y = R.rms_norm(x, gamma, 1e-6)
     ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-6) * gamma
     assert np.allclose(y, ref, rtol=1e-5)
+
+
+def test_rms_norm_padded_closed_forms():
+    rng = np.random.default_rng(11)
+    H, ha = 96, 80
+    gamma = rng.normal(1, 0.2, H).astype(np.float32)
+    # a constant row c: rsqrt(c^2 + eps) * c * gamma on the real columns, 0 on the padding
+    c = np.float32(1.75)
+    x = np.full((1, H), c, np.float32)
+    x[0, ha:] = 100.0                                  # padding must not enter the variance
+    y = R.rms_norm_padded(x, gamma, 1e-6, ha)
+    ref = c / np.sqrt(float(c) ** 2 + 1e-6) * gamma[:ha].astype(np.float64)
+    assert np.allclose(y[0, :ha], ref, rtol=2e-7)
+    assert np.all(y[0, ha:] == 0)
+    # scale invariance at eps = 0 (a power of two scales every step exactly)
+    x = rng.normal(0, 2, (4, H)).astype(np.float32)
+    assert np.array_equal(R.rms_norm_padded(4 * x, gamma, 0.0, ha), R.rms_norm_padded(x, gamma, 0.0, ha))
+    # hidden_actual = H is the plain _torch_rms_norm
+    assert np.array_equal(R.rms_norm_padded(x, gamma, 1e-6), R.rms_norm(x, gamma, 1e-6))
+
+
+def test_topk_scatter_act_matches_closed_forms():
+    rng = np.random.default_rng(12)
+    lg = rng.normal(0, 2, (9, 12)).astype(np.float32)
+    k = 3
+    sm = R.route_topk_scatter_act(lg, k, R.SOFTMAX)
+    sg = R.route_topk_scatter_act(lg, k, R.SIGMOID)
+    for t in range(lg.shape[0]):
+        top = _brute_topk(lg[t], k)
+        assert sorted(np.nonzero(sm[t])[0].tolist()) == sorted(top)
+        assert sorted(np.nonzero(sg[t])[0].tolist()) == sorted(top)
+        v = lg[t, top].astype(np.float64)
+        e = np.exp(v - v.max())
+        assert np.allclose(sm[t, top], e / e.sum(), rtol=1e-6)
+        assert np.allclose(sg[t, top], 1 / (1 + np.exp(-v)), rtol=1e-6)
+    # same ids and (to rounding) weights as the topk -> act order
+    ids, w = R.route_topk_act(lg, k, R.SOFTMAX)
+    assert np.allclose(np.take_along_axis(sm, ids.astype(np.int64), 1), w, rtol=1e-6)

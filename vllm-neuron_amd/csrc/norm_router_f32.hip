@@ -1,0 +1,211 @@
+// RMSNorm and the fp32-operand router logits GEMM.
+//
+// RMSNorm follows the two reference forms:
+//   router.py:681-688 (_torch_rms_norm): y = (x * rsqrt(mean(x^2) + eps)) * gamma
+//   moe_block_tkg.py:135-151: the same over the first hidden_actual columns, the
+//   padded columns set to 0, output cast back to the input dtype.
+// Both run in fp32; mean = sum / n, rsqrt = 1 / sqrt (IEEE division and square
+// root, each correctly rounded).
+//
+// The fp32 logits GEMM serves router() when its operands are not bf16-exact:
+// router.py:236 casts hidden_states to the computation dtype (fp32) before the
+// optional RMSNorm, so with gamma (or fp32 inputs) F.linear runs on fp32
+// operands (router.py:418-424). It uses v_mfma_f32_16x16x4f32.
+#include "moe_common.h"
+#include "moe_internal.h"
+
+namespace moe {
+
+__device__ __forceinline__ float ld_act(const void* p, size_t i, int is_f32) {
+  return is_f32 ? ((const float*)p)[i] : bf16_bits_to_f32(((const uint16_t*)p)[i]);
+}
+
+// One workgroup (256 threads) per row. The sum of squares is reduced in a
+// fixed order (per-thread strided sums, then a wave butterfly, then the four
+// wave sums in order), so the result is deterministic.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ x, int x_f32,
+                                                       const float* __restrict__ gamma, int H,
+                                                       int ha, float eps, void* __restrict__ out,
+                                                       int out_f32) {
+  __shared__ float s_part[4];
+  const size_t row = (size_t)blockIdx.x * H;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < ha; c += 256) {
+    const float v = ld_act(x, row + c, x_f32);
+    ss += v * v;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
+  const float r = 1.0f / sqrtf(tot / (float)ha + eps);
+  for (int c = threadIdx.x; c < H; c += 256) {
+    float y = 0.f;
+    if (c < ha) y = (ld_act(x, row + c, x_f32) * r) * gamma[c];
+    if (out_f32)
+      ((float*)out)[row + c] = y;
+    else
+      ((uint16_t*)out)[row + c] = f32_to_bf16_bits(y);
+  }
+}
+
+// logits[t, e] = sum_h x[t, h] * w[e, h]   (fp32 x; fp32 or bf16 w; fp32 accumulate)
+//
+// Workgroup tile: 64 tokens x 64 experts, 4 waves; wave w owns experts
+// [16w, 16w + 16) for the 64 tokens (4 row tiles). K advances 64 per step in 16
+// MFMAs of K = 4. In sub-step s lane l (group g = l/16) supplies K position
+// g*16 + s of the step for row / column l%16; A and B use the same mapping, so
+// each lane's 16 weight values of a step are contiguous (vector loads) and the
+// 16 MFMAs together cover all 64 positions. blockIdx.z splits K as in the bf16
+// kernel.
+template <typename WT>
+__global__ __launch_bounds__(256) void router_logits_f32_kernel(
+    const float* __restrict__ x, const WT* __restrict__ w, const float* __restrict__ bias, int T,
+    int H, int E, int kchunk, float* __restrict__ out) {
+  __shared__ float sx[64][64 + 1];  // +1: rows land on distinct banks
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
+  const int k_begin = blockIdx.z * kchunk;
+  const int k_end = min(H, k_begin + kchunk);
+  const int g = lane >> 4, r16 = lane & 15;
+
+  int erow = e0 + wave * 16 + r16;
+  const bool erow_ok = erow < E;
+  if (!erow_ok) erow = E - 1;
+  const WT* wrow = w + (size_t)erow * H;
+
+  v4f acc[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) acc[m] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = k_begin; k0 < k_end; k0 += 64) {
+    // x tile: 64 rows x 64 floats = 1024 float4, 4 per thread.
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = threadIdx.x + c * 256;
+      const int row = idx >> 4, col = (idx & 15) * 4;
+      float4 v = {0.f, 0.f, 0.f, 0.f};
+      if (t0 + row < T) v = *(const float4*)(x + (size_t)(t0 + row) * H + k0 + col);
+      sx[row][col] = v.x;
+      sx[row][col + 1] = v.y;
+      sx[row][col + 2] = v.z;
+      sx[row][col + 3] = v.w;
+    }
+    float b[16];
+    if constexpr (sizeof(WT) == 4) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = *(const float4*)(wrow + k0 + g * 16 + q * 4);
+        b[4 * q] = v.x;
+        b[4 * q + 1] = v.y;
+        b[4 * q + 2] = v.z;
+        b[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int4 v = *(const int4*)(wrow + k0 + g * 16 + q * 8);
+        const uint32_t u[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          b[8 * q + 2 * j] = __uint_as_float(u[j] << 16);
+          b[8 * q + 2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float a = sx[m * 16 + r16][g * 16 + s];
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[s], acc[m], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // C layout: lane l, register i -> row 4*(l/16)+i of the 16-row tile, column l%16.
+  if (!erow_ok) return;
+  const int e = e0 + wave * 16 + r16;
+  const float bv = (bias != nullptr && gridDim.z == 1) ? bias[e] : 0.f;
+  float* o = out + (size_t)blockIdx.z * T * E;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = t0 + m * 16 + g * 4 + i;
+      if (t < T) o[(size_t)t * E + e] = acc[m][i] + bv;
+    }
+  }
+}
+
+// Sums the split-K partials in split order (+ bias).
+__global__ void router_logits_f32_reduce(const float* __restrict__ part,
+                                         const float* __restrict__ bias, int T, int E, int ksplit,
+                                         float* __restrict__ out) {
+  const size_t n = (size_t)T * E;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float s = 0.f;
+    for (int k = 0; k < ksplit; ++k) s += part[(size_t)k * n + i];
+    if (bias != nullptr) s += bias[i % E];
+    out[i] = s;
+  }
+}
+
+}  // namespace moe
+
+using namespace moe;
+
+extern "C" int moe_rms_norm(const void* x, int x_is_f32, const float* gamma, int T, int H,
+                            int hidden_actual, float eps, void* out, int out_is_f32,
+                            void* stream) {
+  MOE_API_BEGIN("moe_rms_norm");
+  MOE_CHECK_ARG(x && gamma && out, "null pointer argument");
+  MOE_CHECK_ARG(T >= 0 && H > 0, "bad sizes T=%d H=%d", T, H);
+  MOE_CHECK_ARG(hidden_actual >= 1 && hidden_actual <= H,
+                "hidden_actual must be in [1, H=%d], got %d", H, hidden_actual);
+  MOE_CHECK_ARG(eps >= 0.f, "eps must be >= 0");
+  if (T == 0) return MOE_OK;
+  hipLaunchKernelGGL(rms_norm_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, x,
+                     x_is_f32 ? 1 : 0, gamma, H, hidden_actual, eps, out, out_is_f32 ? 1 : 0);
+  MOE_API_END();
+}
+
+extern "C" int moe_router_logits_f32(const float* x, const void* router_w, int w_is_f32,
+                                     const float* bias, int T, int H, int E, float* logits,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  MOE_API_BEGIN("moe_router_logits_f32");
+  MOE_CHECK_ARG(x && router_w && logits, "null pointer argument");
+  MOE_CHECK_ARG(T >= 0 && H > 0 && E > 0, "bad sizes T=%d H=%d E=%d", T, H, E);
+  MOE_CHECK_ARG(H % 64 == 0, "H must be a multiple of 64, got %d", H);
+  MOE_CHECK_ARG(((uintptr_t)x & 15) == 0 && ((uintptr_t)router_w & 15) == 0,
+                "x and w must be 16-byte aligned");
+  if (T == 0) return MOE_OK;
+  hipStream_t st = (hipStream_t)stream;
+  int ks = router_logits_splits(T, H, E);
+  int kchunk = ((H / 64 + ks - 1) / ks) * 64;
+  ks = (H + kchunk - 1) / kchunk;
+  dim3 grid((T + 63) / 64, (E + 63) / 64, ks);
+  float* dst = logits;
+  if (ks > 1) {
+    const size_t need = (size_t)ks * T * E * sizeof(float);
+    MOE_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
+                  "workspace too small: need %zu bytes", need);
+    dst = (float*)workspace;
+  }
+  if (w_is_f32)
+    hipLaunchKernelGGL(router_logits_f32_kernel<float>, grid, dim3(256), 0, st, x,
+                       (const float*)router_w, bias, T, H, E, kchunk, dst);
+  else
+    hipLaunchKernelGGL(router_logits_f32_kernel<uint16_t>, grid, dim3(256), 0, st, x,
+                       (const uint16_t*)router_w, bias, T, H, E, kchunk, dst);
+  if (ks > 1) {
+    const size_t n = (size_t)T * E;
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(router_logits_f32_reduce, dim3(blocks), dim3(256), 0, st, dst, bias, T, E, ks,
+                       logits);
+  }
+  MOE_API_END();
+}

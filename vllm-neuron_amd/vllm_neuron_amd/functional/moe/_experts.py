@@ -1,0 +1,187 @@
+"""Expert weights at the operator boundary and the expert pipeline over a mapping.
+
+The operator API of the reference passes expert weights per call in its own
+layout (gate_up [E, H, 2, I], down [E, I, H]; moe_cte.py:122-131). The HIP
+kernels read the DeepSeek-V3 checkpoint stacking (w13 [E, 2I, H], w2 [E, H, I],
+128x128 fp32 block scales), which is K-contiguous. Both are accepted here; the
+reference layout is converted once per weight tensor and the result cached,
+keyed by the tensors' storage, version and shape (a second copy of the experts
+while the caller keeps the originals: pass the stacked layout to avoid it).
+"""
+import torch
+
+from ... import ops
+from ...weights import FP8, Fp8MoEWeights, quant_weight_blocks
+
+_CACHE = {}
+_CACHE_MAX = 8
+
+
+def _key(*ts):
+    return tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype) if t is not None else None
+                 for t in ts)
+
+
+def _cached(key, build):
+    hit = _CACHE.get(key)
+    if hit is None:
+        if len(_CACHE) >= _CACHE_MAX:
+            _CACHE.pop(next(iter(_CACHE)))
+        hit = build()
+        _CACHE[key] = hit
+    return hit
+
+
+def _need_fp8(t, name):
+    if t.dtype != FP8:
+        raise NotImplementedError(
+            f"{name} is {t.dtype}: this build runs float8_e4m3fn experts with 128x128 block "
+            "scales (quantize with vllm_neuron_amd.weights.quant_weight_blocks)")
+
+
+def _ones_scale(E, O, I, device):
+    return torch.ones(E, O // 128, I // 128, device=device, dtype=torch.float32)
+
+
+def routed_weights(gate_up, down, gate_up_scale=None, down_scale=None):
+    """(w13, w13_scale, w2, w2_scale) in the kernels' layout from either layout.
+
+    Stacked: gate_up [E, 2I, H], gate_up_scale [E, 2I/128, H/128]; down [E, H, I],
+    down_scale [E, H/128, I/128]. Reference: gate_up [E, H, 2, I], gate_up_scale
+    [E, H/128, 2, I/128]; down [E, I, H], down_scale [E, I/128, H/128]. Missing
+    scales mean 1.0 (codes used as values)."""
+    _need_fp8(gate_up, "gate_up_proj_weight")
+    _need_fp8(down, "down_proj_weight")
+    dev = gate_up.device
+    if gate_up.dim() == 3:
+        E, I2, H = gate_up.shape
+        I = I2 // 2
+        if tuple(down.shape) != (E, H, I):
+            raise ValueError(f"down_proj_weight must be [E, H, I] = {(E, H, I)} for a stacked "
+                             f"gate_up [E, 2I, H], got {tuple(down.shape)}")
+        s13 = gate_up_scale if gate_up_scale is not None else _ones_scale(E, I2, H, dev)
+        s2 = down_scale if down_scale is not None else _ones_scale(E, H, I, dev)
+        if tuple(s13.shape) != (E, I2 // 128, H // 128):
+            raise NotImplementedError(
+                f"gate_up_proj_scale {tuple(s13.shape)}: only 128x128 block scales "
+                f"[E, 2I/128, H/128] = {(E, I2 // 128, H // 128)} are supported")
+        if tuple(s2.shape) != (E, H // 128, I // 128):
+            raise NotImplementedError(
+                f"down_proj_scale {tuple(s2.shape)}: only 128x128 block scales "
+                f"[E, H/128, I/128] = {(E, H // 128, I // 128)} are supported")
+        return (gate_up.contiguous(), s13.float().contiguous(), down.contiguous(),
+                s2.float().contiguous())
+    if gate_up.dim() != 4 or gate_up.shape[2] != 2:
+        raise ValueError(f"gate_up_proj_weight must be [E, H, 2, I] or [E, 2I, H], got "
+                         f"{tuple(gate_up.shape)}")
+    E, H, _, I = gate_up.shape
+    if tuple(down.shape) != (E, I, H):
+        raise ValueError(f"down_proj_weight must be [E, I, H] = {(E, I, H)}, got "
+                         f"{tuple(down.shape)}")
+    if gate_up_scale is not None and tuple(gate_up_scale.shape) != (E, H // 128, 2, I // 128):
+        raise NotImplementedError(
+            f"gate_up_proj_scale {tuple(gate_up_scale.shape)}: only 128x128 block scales "
+            f"[E, H/128, 2, I/128] are supported")
+    if down_scale is not None and tuple(down_scale.shape) != (E, I // 128, H // 128):
+        raise NotImplementedError(
+            f"down_proj_scale {tuple(down_scale.shape)}: only 128x128 block scales "
+            f"[E, I/128, H/128] are supported")
+
+    def build():
+        w13 = gate_up.permute(0, 2, 3, 1).reshape(E, 2 * I, H).contiguous()
+        if gate_up_scale is None:
+            s13 = _ones_scale(E, 2 * I, H, dev)
+        else:
+            s13 = gate_up_scale.permute(0, 2, 3, 1).reshape(E, 2 * I // 128, H // 128)
+        w2 = down.transpose(1, 2).contiguous()
+        s2 = _ones_scale(E, H, I, dev) if down_scale is None else down_scale.transpose(1, 2)
+        return w13, s13.float().contiguous(), w2, s2.float().contiguous()
+
+    return _cached(("nf",) + _key(gate_up, down, gate_up_scale, down_scale), build)
+
+
+def shared_weights(gate_w, up_w, down_w, I):
+    """A shared expert given as gate [H, I_sh], up [H, I_sh], down [I_sh, H]
+    (moe_block_tkg.py:314-316) as n = I_sh / I stacked experts of intermediate I.
+
+    Floating-point weights are quantized once to e4m3fn with 128x128 block
+    scales (amax / 448, round-to-nearest-even), and cached; fp8 weights are
+    taken with unit scales."""
+    H, I_sh = gate_w.shape
+    if tuple(up_w.shape) != (H, I_sh) or tuple(down_w.shape) != (I_sh, H):
+        raise ValueError("shared expert weights must be gate [H, I], up [H, I], down [I, H]")
+    if I_sh % I:
+        raise ValueError(f"shared intermediate {I_sh} must be a multiple of the expert "
+                         f"intermediate {I}")
+
+    def build():
+        w13 = torch.cat([gate_w.t(), up_w.t()], dim=0)  # [2 I_sh, H]
+        w2 = down_w.t()                                  # [H, I_sh]
+        if w13.dtype == FP8:
+            q13, s13 = w13.contiguous(), torch.ones(2 * I_sh // 128, H // 128,
+                                                    device=w13.device)
+            q2, s2 = w2.contiguous(), torch.ones(H // 128, I_sh // 128, device=w2.device)
+        else:
+            q13, s13 = quant_weight_blocks(w13.float())
+            q2, s2 = quant_weight_blocks(w2.float())
+        n = I_sh // I
+        g, u = q13[:I_sh], q13[I_sh:]
+        gs, us = s13[:I_sh // 128], s13[I_sh // 128:]
+        w13s = torch.stack([torch.cat([g[j * I:(j + 1) * I], u[j * I:(j + 1) * I]])
+                            for j in range(n)])
+        s13s = torch.stack([torch.cat([gs[j * I // 128:(j + 1) * I // 128],
+                                       us[j * I // 128:(j + 1) * I // 128]]) for j in range(n)])
+        w2s = torch.stack([q2[:, j * I:(j + 1) * I] for j in range(n)])
+        s2s = torch.stack([s2[:, j * I // 128:(j + 1) * I // 128] for j in range(n)])
+        return (w13s.contiguous(), s13s.float().contiguous(), w2s.contiguous(),
+                s2s.float().contiguous())
+
+    return _cached(("shared", I) + _key(gate_w, up_w, down_w), build)
+
+
+def make_weights(w13, s13, w2, s2, shared=None):
+    kw = {}
+    if shared is not None:
+        kw = dict(shared_w13=shared[0], shared_w13_scale=shared[1], shared_w2=shared[2],
+                  shared_w2_scale=shared[3])
+    return Fp8MoEWeights(router_w=None, w13=w13, w13_scale=s13, w2=w2, w2_scale=s2, **kw)
+
+
+def as_bf16(x):
+    """Activations enter the fp8 quantizer as bf16."""
+    return x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
+
+
+def run_experts(x_bf16, tpid, b2e, B, k_rows, k_bound, w):
+    """gate_up -> SiLU * up -> down for every slot of a blockwise mapping.
+
+    x_bf16 [T, H]; tpid [N*B] int32 (slot -> token, -1 or >= T for padding);
+    b2e [N] int32. k_rows is the expected routed rows per token (picks the tile
+    height), k_bound an upper bound on them (sizes the tile list). Returns
+    (y [N*B + n_shared*T, H] bf16, N*B)."""
+    T = x_bf16.shape[0]
+    E, S = w.n_experts, w.n_shared
+    N = b2e.numel()
+    NB = N * B
+    xq, xs = ops.act_quant(x_bf16)
+    if ops.use_block_kernels(T, k_rows, E):
+        tiles, num, mbt = ops.build_block_tiles(tpid, b2e, B, T, k_bound, E, S)
+        hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mbt)
+        y = ops.expert_down_block(hq, hs, w, T, NB, tiles, num, mbt)
+    else:
+        mt = ops.choose_mt(T, k_rows, E)
+        tiles, num, max_tiles = ops.build_tiles(tpid, b2e, B, T, k_bound, E, S, mt)
+        hq, hs = ops.expert_gate_up(xq, xs, w, tpid, NB, tiles, num, max_tiles, mt)
+        y = ops.expert_down(hq, hs, w, T, NB, tiles, num, max_tiles, mt)
+    return y, NB
+
+
+def routed_forward(x_bf16, ids, wts, w, block_size=256):
+    """Experts of ids [T, K] int32 weighted by wts [T, K] fp32 (+ the shared
+    experts of w, weight 1), combined per token in k order: [T, H] bf16."""
+    T, K = ids.shape
+    E, H = w.n_experts, w.hidden
+    m = ops.blockwise_mapping(ids=ids.contiguous(), n_experts=E, top_k=K, block_size=block_size)
+    y, NB = run_experts(x_bf16, m["token_position_to_id"], m["block_to_expert"], block_size, K, K,
+                        w)
+    return ops.combine(y, m["inv_pos"], wts.contiguous(), T, H, NB, w.n_shared)

@@ -1,0 +1,158 @@
+"""moe_block_tkg(): fused decode MoE block, with the reference's signature.
+
+Reference: vllm_neuron/functional/moe/moe_block_tkg.py:306-591 (API),
+:57-303 (_torch_moe_block_tkg_impl, the math):
+  1. RMSNorm over the first hidden_actual columns (fp32), times gamma, cast to
+     the input dtype, padded columns 0                        (:135-151)
+  2. router logits = norm(x) . W_r in fp32 (+ bias)           (:153-163)
+  3. router_pre_norm: activation on all experts, then top-k;
+     else top-k, then activation on the k values; norm_topk_prob divides by
+     (sum + 1e-20)                                            (:165-205)
+  4. experts on norm(x); NO_SCALE adds each selected expert with weight 1,
+     POST_SCALE with its affinity, fp32 accumulation          (:225-296)
+  5. the shared expert (gate [H, I_sh], up [H, I_sh], down [I_sh, H]) is added
+     with weight 1 (kernel-only in the reference, :314-316, :389-391)
+Returns (output [T, H], router_logits [T, E] fp32), or output alone when
+skip_router_logits.
+
+Compute path (all HIP): moe_rms_norm -> moe_router_logits (bf16 operands, as
+the reference's fp32 matmul of bf16 values) -> moe_router_topk -> blockwise
+mapping -> fp8 experts -> combine. Routed experts are float8_e4m3fn with
+128x128 block scales (expert_gate_up_weights_scale / expert_down_weights_scale
+in the block-scale shapes); floating-point shared-expert weights are quantized
+once to the same format. router_mm_dtype is accepted for signature
+compatibility; the logits are always accumulated in fp32.
+"""
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from ... import ops
+from . import _experts
+from .types import ActFnType, ExpertAffinityScaleMode, RouterActFnType
+
+
+def moe_block_tkg(
+    inp: Tensor,
+    gamma: Tensor,
+    router_weights: Tensor,
+    expert_gate_up_weights: Tensor,
+    expert_down_weights: Tensor,
+    rank_id: Optional[Tensor] = None,
+    top_k: int = 1,
+    shared_expert_gate_w: Optional[Tensor] = None,
+    shared_expert_up_w: Optional[Tensor] = None,
+    shared_expert_down_w: Optional[Tensor] = None,
+    expert_gate_up_weights_scale: Optional[Tensor] = None,
+    expert_down_weights_scale: Optional[Tensor] = None,
+    router_bias: Optional[Tensor] = None,
+    expert_gate_up_bias: Optional[Tensor] = None,
+    expert_down_bias: Optional[Tensor] = None,
+    shared_expert_gate_bias: Optional[Tensor] = None,
+    shared_expert_up_bias: Optional[Tensor] = None,
+    shared_expert_down_bias: Optional[Tensor] = None,
+    eps: float = 1e-6,
+    router_act_fn: RouterActFnType = RouterActFnType.SIGMOID,
+    router_pre_norm: bool = True,
+    norm_topk_prob: bool = False,
+    expert_affinities_scaling_mode: ExpertAffinityScaleMode = ExpertAffinityScaleMode.NO_SCALE,
+    hidden_act_fn: ActFnType = ActFnType.SiLU,
+    hidden_act_scale_factor: Optional[float] = None,
+    hidden_act_bias: Optional[float] = None,
+    gate_clamp_upper_limit: Optional[float] = None,
+    gate_clamp_lower_limit: Optional[float] = None,
+    up_clamp_upper_limit: Optional[float] = None,
+    up_clamp_lower_limit: Optional[float] = None,
+    router_mm_dtype=None,
+    hidden_actual: Optional[int] = None,
+    skip_router_logits: bool = False,
+    is_all_expert: bool = False,
+    residual: Optional[Tensor] = None,
+    expert_gate_up_input_scale: Optional[Tensor] = None,
+    expert_down_input_scale: Optional[Tensor] = None,
+) -> Tuple[Tensor, ...]:
+    """See the module docstring. is_all_expert selects the reference's all-expert
+    kernel schedule; the result equals the selective one (unselected experts
+    carry zero weight), which is what runs here."""
+    if hidden_act_scale_factor is not None or hidden_act_bias is not None:
+        raise NotImplementedError(
+            "hidden_act_scale_factor and hidden_act_bias are placeholders and must be None.")
+    bad = {
+        "expert biases": any(v is not None for v in (
+            expert_gate_up_bias, expert_down_bias, shared_expert_gate_bias,
+            shared_expert_up_bias, shared_expert_down_bias)),
+        "STATIC_MX input scales": expert_gate_up_input_scale is not None
+            or expert_down_input_scale is not None,
+        "fused residual add": residual is not None,
+        "gate/up clamps": any(v is not None for v in (gate_clamp_upper_limit, gate_clamp_lower_limit,
+                                                      up_clamp_upper_limit, up_clamp_lower_limit)),
+        f"activation {getattr(hidden_act_fn, 'name', hidden_act_fn)}": hidden_act_fn != ActFnType.SiLU,
+        f"scaling mode {expert_affinities_scaling_mode.name}": expert_affinities_scaling_mode not in (
+            ExpertAffinityScaleMode.NO_SCALE, ExpertAffinityScaleMode.POST_SCALE),
+    }
+    bad = [k for k, v in bad.items() if v]
+    if bad:
+        raise NotImplementedError(f"moe_block_tkg: {', '.join(bad)} not supported by this build")
+    if router_act_fn not in (RouterActFnType.SOFTMAX, RouterActFnType.SIGMOID):
+        raise NotImplementedError(f"Router activation {router_act_fn} is not supported.")
+    if (shared_expert_gate_w is None) != (shared_expert_down_w is None) or \
+            (shared_expert_gate_w is None) != (shared_expert_up_w is None):
+        raise ValueError("shared expert gate, up and down weights must be given together")
+
+    x = inp.reshape(-1, inp.shape[-1]) if inp.dim() == 3 else inp
+    if x.dim() != 2:
+        raise ValueError(f"inp must be [B, S, H] or [T, H], got {tuple(inp.shape)}")
+    T, H = x.shape
+    if router_weights.dim() != 2 or router_weights.shape[0] != H:
+        raise ValueError(f"router_weights must be [H, E] with H={H}, got "
+                         f"{tuple(router_weights.shape)}")
+    E_global = router_weights.shape[1]
+    w13, s13, w2, s2 = _experts.routed_weights(expert_gate_up_weights, expert_down_weights,
+                                                expert_gate_up_weights_scale,
+                                                expert_down_weights_scale)
+    E_L, I = w13.shape[0], w13.shape[1] // 2
+    if w13.shape[2] != H:
+        raise ValueError(f"expert weights have H={w13.shape[2]}, inp H={H}")
+    if E_L != E_global:
+        raise NotImplementedError(
+            f"{E_L} local of {E_global} experts: expert-parallel slicing needs several GPUs; "
+            "this build keeps every expert on one")
+    if rank_id is not None and int(torch.as_tensor(rank_id).reshape(-1)[0]) != 0:
+        raise NotImplementedError("rank_id != 0: one GPU holds every expert")
+    if not 1 <= top_k <= E_global:
+        raise ValueError(f"top_k must be between 1 and {E_global}, got {top_k}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"inp must be bfloat16 or float32, got {x.dtype}")
+
+    # 1. RMSNorm, cast back to the input dtype (:135-151)
+    xn = ops.rms_norm(x.contiguous(), gamma, eps, hidden_actual, out_dtype=x.dtype)
+    # 2. fp32 router matmul on the normalized values (:153-163)
+    wt = router_weights.t()
+    wt = wt if wt.is_contiguous() else wt.contiguous()
+    bias = None if router_bias is None else router_bias.reshape(-1).float().contiguous()
+    if xn.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16:
+        logits = ops.router_logits(xn, wt, bias)
+    else:
+        if wt.dtype not in (torch.float32, torch.bfloat16):
+            wt = wt.float().contiguous()
+        logits = ops.router_logits_f32(xn.float().contiguous(), wt, bias)
+    # 3. selection (:165-205)
+    order = ops.ORDER_ACT_TOPK if router_pre_norm else ops.ORDER_TOPK_ACT
+    scoring = "softmax" if router_act_fn == RouterActFnType.SOFTMAX else "sigmoid"
+    ids, wts = ops.router_topk(logits, top_k, order, scoring, renorm=norm_topk_prob, eps=1e-20,
+                               scale=1.0)
+    if expert_affinities_scaling_mode == ExpertAffinityScaleMode.NO_SCALE:
+        wts = torch.ones_like(wts)
+    # 4./5. routed experts (+ shared expert) on the normalized values
+    shared = None
+    if shared_expert_gate_w is not None:
+        shared = _experts.shared_weights(shared_expert_gate_w, shared_expert_up_w,
+                                         shared_expert_down_w, I)
+    w = _experts.make_weights(w13, s13, w2, s2, shared)
+    out = _experts.routed_forward(_experts.as_bf16(xn), ids, wts, w)
+    if x.dtype != torch.bfloat16:
+        out = out.to(x.dtype)
+    if skip_router_logits:
+        return out
+    return out, logits

@@ -1,0 +1,141 @@
+"""moe_cte(): blockwise expert MLP over a given mapping, with the reference's signature.
+
+Reference: vllm_neuron/functional/moe/moe_cte.py:35-437 (API and dispatch),
+:465-612 (_torch_moe_impl, the math):
+    out[t] = sum_e affinity[t, e] * ( act(x_t W_g,e) * (x_t W_u,e) ) W_d,e
+summed in expert order, accumulated in fp32 (POST_SCALE), cast to the input
+dtype; T = expert_affinities_masked.shape[0] // E (:533-536).
+
+Compute path (all HIP): 1x128 fp8 activation quant -> row tiles of the given
+token_position_to_id / block_to_expert -> fp8 gate_up with SiLU * up and the
+1x128 requant of h -> fp8 down -> inverse mapping -> combine weighted by the
+dense affinities in expert order. Experts are float8_e4m3fn with 128x128 fp32
+block scales, in the reference layout (gate_up [E, H, 2, I], scales
+[E, H/128, 2, I/128]; down [E, I, H], scales [E, I/128, H/128]) or the
+checkpoint stacking (gate_up [E, 2I, H], down [E, H, I]).
+
+Supported: SiLU, POST_SCALE and NO_SCALE, implementation shard_on_block /
+shard_on_i / shard_on_i_hybrid / shard_on_i_dropping (one kernel family serves
+them all; the choice is a Trainium sharding hint). Raises NotImplementedError
+for MX implementations and quantization types, biases, clamps, GELU / Swish,
+PRE_SCALE / PRE_SCALE_DELAYED and activation checkpoint buffers.
+"""
+from typing import Any, Optional
+
+import torch
+from torch import Tensor
+
+from ... import ops
+from . import _experts
+from .types import (MX_IMPLEMENTATIONS, ActFnType, BlockShardStrategy, ExpertAffinityScaleMode,
+                    MoECTEImplementation, QuantizationType)
+
+
+def _unsupported(**kw):
+    bad = [k for k, v in kw.items() if v]
+    if bad:
+        raise NotImplementedError(f"moe_cte: {', '.join(bad)} not supported by this build "
+                                  "(fp8 128x128 blockwise experts, SiLU, POST_SCALE / NO_SCALE)")
+
+
+def moe_cte(
+    hidden_states: Tensor,
+    expert_affinities_masked: Optional[Tensor],
+    gate_up_proj_weight: Tensor,
+    down_proj_weight: Tensor,
+    token_position_to_id: Tensor,
+    block_to_expert: Tensor,
+    block_size: int,
+    implementation: MoECTEImplementation,
+    n_block_per_iter: int = 1,
+    block_sharding_strategy: BlockShardStrategy = BlockShardStrategy.PING_PONG,
+    n_static_blocks: int = -1,
+    n_dynamic_blocks: int = -1,
+    top_k: int = 1,
+    ep_degree: int = 1,
+    ep_rank: Optional[Tensor] = None,
+    checkpoint_activation: bool = False,
+    expert_affinity_multiply_on_I: bool = False,
+    num_static_block: Optional[int] = None,
+    conditions: Optional[Tensor] = None,
+    gate_and_up_proj_bias: Optional[Tensor] = None,
+    down_proj_bias: Optional[Tensor] = None,
+    gate_up_proj_scale: Optional[Tensor] = None,
+    down_proj_scale: Optional[Tensor] = None,
+    gate_up_activations_T: Optional[Tensor] = None,
+    down_activations: Optional[Tensor] = None,
+    activation_function: ActFnType = ActFnType.SiLU,
+    skip_token: bool = False,
+    skip_weight: bool = False,
+    compute_dtype: Any = None,
+    is_tensor_update_accumulating: bool = True,
+    expert_affinities_scaling_mode: ExpertAffinityScaleMode = ExpertAffinityScaleMode.POST_SCALE,
+    gate_clamp_upper_limit: Optional[float] = None,
+    gate_clamp_lower_limit: Optional[float] = None,
+    up_clamp_upper_limit: Optional[float] = None,
+    up_clamp_lower_limit: Optional[float] = None,
+    quantization_type: QuantizationType = QuantizationType.NONE,
+    gate_w_scale: Optional[Tensor] = None,
+    up_w_scale: Optional[Tensor] = None,
+    down_w_scale: Optional[Tensor] = None,
+    gate_up_in_scale: Optional[Tensor] = None,
+    down_in_scale: Optional[Tensor] = None,
+    use_packed_scales: bool = False,
+) -> Tensor:
+    """Output [T, H] in hidden_states' dtype; see the module docstring."""
+    if not isinstance(implementation, MoECTEImplementation):
+        raise ValueError(f"implementation must be a MoECTEImplementation, got {implementation!r}")
+    _unsupported(**{
+        f"implementation {implementation.name}": implementation in MX_IMPLEMENTATIONS,
+        f"quantization_type {quantization_type.name}": quantization_type != QuantizationType.NONE,
+        "expert biases": gate_and_up_proj_bias is not None or down_proj_bias is not None,
+        "gate/up clamps": any(v is not None for v in (gate_clamp_upper_limit, gate_clamp_lower_limit,
+                                                      up_clamp_upper_limit, up_clamp_lower_limit)),
+        f"activation {getattr(activation_function, 'name', activation_function)}":
+            activation_function != ActFnType.SiLU,
+        f"scaling mode {expert_affinities_scaling_mode.name}": expert_affinities_scaling_mode not in (
+            ExpertAffinityScaleMode.POST_SCALE, ExpertAffinityScaleMode.NO_SCALE),
+        "activation checkpoint buffers": gate_up_activations_T is not None
+            or down_activations is not None or checkpoint_activation,
+        "packed affinities (expert_affinities_masked=None)": expert_affinities_masked is None,
+        "ep_rank / ep_degree": ep_rank is not None or int(ep_degree) != 1,
+    })
+    if (gate_up_proj_scale is None) != (down_proj_scale is None):
+        raise ValueError("gate_up_proj_scale and down_proj_scale must be provided together")
+    if hidden_states.dim() != 2:
+        raise ValueError(f"hidden_states must be [T, H] or [T+1, H], got {tuple(hidden_states.shape)}")
+
+    w13, s13, w2, s2 = _experts.routed_weights(gate_up_proj_weight, down_proj_weight,
+                                                gate_up_proj_scale, down_proj_scale)
+    E, H = w13.shape[0], w13.shape[2]
+    if hidden_states.shape[1] != H:
+        raise ValueError(f"hidden_states has H={hidden_states.shape[1]}, weights H={H}")
+    if expert_affinities_masked.numel() % E:
+        raise ValueError(f"expert_affinities_masked holds {expert_affinities_masked.numel()} "
+                         f"values, not a multiple of E={E}")
+    T = expert_affinities_masked.numel() // E
+    if hidden_states.shape[0] not in (T, T + 1):
+        raise ValueError(f"hidden_states must have T={T} or T+1 rows, got {hidden_states.shape[0]}")
+    B = int(block_size)
+    tpid = token_position_to_id.reshape(-1)
+    b2e = block_to_expert.reshape(-1)
+    N = b2e.numel()
+    if tpid.numel() != N * B:
+        raise ValueError(f"token_position_to_id has {tpid.numel()} slots, block_to_expert "
+                         f"{N} blocks of {B}")
+    if tpid.dtype != torch.int32 or b2e.dtype != torch.int32:
+        raise ValueError("token_position_to_id and block_to_expert must be int32")
+    tpid, b2e = tpid.contiguous(), b2e.contiguous()
+
+    x = _experts.as_bf16(hidden_states[:T]).contiguous()
+    w = _experts.make_weights(w13, s13, w2, s2)
+    # Expected routed rows per token from the mapping size (N ~ T*K/B + E - 1);
+    # it only picks the tile height. Tile lists are sized for any mapping (K = E).
+    k_rows = max(1, min(E, ((N - E + 1) * B + E - 1) // max(T, 1)))
+    y, NB = _experts.run_experts(x, tpid, b2e, B, k_rows, E, w)
+    inv = ops.invert_mapping(tpid, b2e, B, T, E)  # [T, E] slot of (t, e) or -1
+    aff = expert_affinities_masked.reshape(T, E).float()
+    if expert_affinities_scaling_mode == ExpertAffinityScaleMode.NO_SCALE:
+        aff = (aff != 0).float()  # moe_block_tkg.py:280-289 binary weights
+    out = ops.combine(y, inv, aff.contiguous(), T, H, NB, 0)
+    return out if hidden_states.dtype == torch.bfloat16 else out.to(hidden_states.dtype)

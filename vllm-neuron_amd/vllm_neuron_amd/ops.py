@@ -76,6 +76,50 @@ def router_logits(x, router_w, bias=None):
     return out
 
 
+def router_logits_f32(x, router_w, bias=None):
+    """x [T,H] fp32, router_w [E,H] fp32 or bf16, bias [E] fp32 -> logits [T,E] fp32
+    (fp32 operands, fp32 MFMA)."""
+    _need_cuda(x, router_w, bias)
+    T, H = x.shape
+    E = router_w.shape[0]
+    _need(x, torch.float32, (T, H), "hidden_states")
+    if router_w.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"router weight must be float32 or bfloat16, got {router_w.dtype}")
+    _need(router_w, router_w.dtype, (E, H), "router weight [E, H]")
+    if bias is not None:
+        _need(bias, torch.float32, (E,), "router_bias")
+    out = torch.empty(T, E, device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    wsb = lib.moe_router_logits_workspace_bytes(T, H, E)
+    ws = torch.empty(max(wsb, 1), device=x.device, dtype=torch.uint8)
+    _lib.call("moe_router_logits_f32", ptr(x), ptr(router_w),
+              int(router_w.dtype == torch.float32), ptr(bias), T, H, E, ptr(out), ptr(ws), wsb,
+              _stream())
+    return out
+
+
+def rms_norm(x, gamma, eps, hidden_actual=None, out_dtype=None):
+    """RMSNorm of x [T,H] (bf16 or fp32) with gamma [H]; fp32 math; columns at or
+    beyond hidden_actual are 0. Output dtype defaults to x's."""
+    _need_cuda(x, gamma)
+    T, H = x.shape
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"hidden_states must be float32 or bfloat16, got {x.dtype}")
+    _need(x, x.dtype, (T, H), "hidden_states")
+    g = gamma.reshape(-1)
+    if g.numel() != H:
+        raise ValueError(f"gamma must hold H={H} values, got shape {tuple(gamma.shape)}")
+    g = g.to(torch.float32).contiguous()
+    od = x.dtype if out_dtype is None else out_dtype
+    if od not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"out_dtype must be float32 or bfloat16, got {od}")
+    ha = H if hidden_actual is None else int(hidden_actual)
+    out = torch.empty(T, H, device=x.device, dtype=od)
+    _lib.call("moe_rms_norm", ptr(x), int(x.dtype == torch.float32), ptr(g), T, H, ha,
+              float(eps), ptr(out), int(od == torch.float32), _stream())
+    return out
+
+
 def router_topk(logits, top_k, order, scoring, n_group=1, topk_group=1, corr_bias=None,
                 renorm=False, eps=0.0, scale=1.0, dense=False):
     """logits [T,E] fp32 -> ids [T,K] int32, weights [T,K] fp32 (+ affinities [T,E] if dense)."""

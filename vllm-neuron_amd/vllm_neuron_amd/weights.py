@@ -34,7 +34,9 @@ def quant_weight_blocks(w):
         raise ValueError("weight dims must be multiples of 128")
     b = w.float().reshape(*lead, O // 128, 128, I // 128, 128)
     amax = b.abs().amax(dim=(-3, -1))
-    s = torch.clamp(amax, min=AMAX_FLOOR) / FP8_MAX
+    # A tensor divisor keeps this an IEEE division on the GPU (a Python-scalar
+    # divisor becomes a multiply by the rounded reciprocal there).
+    s = torch.clamp(amax, min=AMAX_FLOOR) / torch.full_like(amax, FP8_MAX)
     y = (b / s[..., :, None, :, None]).clamp(-FP8_MAX, FP8_MAX)
     return y.to(FP8).reshape(*lead, O, I), s.float()
 
