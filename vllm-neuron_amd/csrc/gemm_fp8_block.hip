@@ -4,18 +4,21 @@
 // block-scaled fp8 weights), organised for experts that receive hundreds of
 // rows, where the layer becomes MFMA-bound:
 //
-//  * one workgroup (8 waves) computes a 128-row x 256-column tile: the rows are
-//    up to 128 consecutive slots of one expert, the columns 256 weight rows
-//    (gate_up: 128 gate rows + the matching 128 up rows; down: 256 outputs);
-//  * both operands are staged through LDS in three stages of 128 K each (two K
-//    blocks of lookahead), loaded with global_load_lds_dwordx4 (no register
-//    staging); 16-byte chunks are XOR-swizzled by row pairs so 16-lane fragment
-//    reads hit distinct banks of the 64-bank LDS;
-//  * wave (wm, wn) owns rows [32 wm, +32) and 128 columns as 2 x 8 tiles of
+//  * one workgroup (8 waves) computes a 256-row x 256-column tile: the rows are
+//    up to 256 consecutive slots of one expert, the columns 256 weight rows
+//    (gate_up: 128 gate rows + the matching 128 up rows; down: 256 outputs).
+//    Per 128-K step the tile moves 64 KB through L1 for 16.8 MFLOP;
+//  * both operands are staged through LDS in two stages of 128 K (one K block of
+//    look-ahead), loaded with global_load_lds_dwordx4 (no register staging);
+//    16-byte chunks are XOR-swizzled by row pairs so 16-lane fragment reads hit
+//    distinct banks of the 64-bank LDS;
+//  * wave (wm, wn) owns rows [64 wm, +64) and 128 columns as 4 x 8 tiles of
 //    v_mfma_f32_16x16x128_f8f6f4: one MFMA per tile covers a whole 128-K scale
-//    block, so the 16 products of a K block are independent and issue back to
-//    back; acc += part * (s_a[row] * s_w) promotes each in fp32 (the combined
-//    scale per row and column half is precomputed into LDS);
+//    block. The block scales s_k = s_a[row, k] * s_w[k] are folded into the
+//    running accumulator: acc = acc * (s_{k-1} / s_k) + A_k B_k, and the result
+//    is acc * s_last, which equals sum_k s_k A_k B_k (one fp32 multiply per
+//    accumulator element per K block, no separate partial products). The
+//    ratios are computed once per (row, column half) per K block into LDS;
 //  * for gate_up wave column half wn holds gate and up columns [64 wn, +64) of
 //    the tile's 128 h columns, so SiLU(g) * u is wave-local and only the row
 //    amax of the 1x128 quantization group is combined across the two halves;
@@ -30,16 +33,16 @@
 #include "moe_common.h"
 #include "moe_internal.h"
 
-typedef float v16f __attribute__((ext_vector_type(16)));
-
 namespace moe {
 
-constexpr int kBM = 128, kBN = 256, kBK = 128;
+constexpr int kBM = 256, kBN = 256, kBK = 128;
 constexpr int kBlkThreads = 512;
-constexpr int kStages = 3;
-constexpr int kStageA = kBM * kBK;  // 16 KB
+constexpr int kStageA = kBM * kBK;  // 32 KB
 constexpr int kStageB = kBN * kBK;  // 32 KB
-constexpr int kDmaPerWave = (kStageA + kStageB) / 1024 / 8;  // 6 x 1 KB regions per wave
+constexpr int kDmaPerWave = (kStageA + kStageB) / 1024 / 8;  // 8 x 1 KB regions per wave
+constexpr int kStageSA = 2 * kBM * 4;  // activation scales of the stage's block, one copy per column half
+constexpr int kStage = kStageA + kStageB;
+constexpr int kMaxKB = 128;  // K <= 16384
 
 struct BlkArgs {
   const uint8_t* a;
@@ -59,9 +62,8 @@ struct BlkArgs {
   long NB;
 };
 
-__device__ __forceinline__ v4f mfma16_fp8(const v8i& a, const v8i& b) {
-  const v4f z = {0.f, 0.f, 0.f, 0.f};
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+__device__ __forceinline__ v4f mfma16_fp8_acc(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -70,6 +72,11 @@ __device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds_wave_base
   __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
 }
 
+__device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 4, 0, 0);
+}
+
+
 // s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt[3:0] | [15:14]).
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -77,9 +84,9 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-// Workgroup barrier that waits only for this wave's LDS operations (lgkmcnt),
-// leaving the look-ahead direct-to-LDS loads in flight; __syncthreads() would
-// also drain vmcnt. LDS-DMA data is covered by the explicit vmcnt waits.
+// Workgroup barrier that waits only for this wave's LDS operations (lgkmcnt);
+// __syncthreads() would also drain vmcnt. LDS-DMA data is covered by the
+// explicit vmcnt waits.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt untouched
   __builtin_amdgcn_s_barrier();
@@ -102,17 +109,23 @@ template <int KIND>
 __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs p) {
   // Pipeline stages as distinct objects, so the compiler can tell that fragment
   // reads of one stage do not alias the direct-to-LDS loads in flight into another.
-  __shared__ __attribute__((aligned(16))) uint8_t sT0[kStageA + kStageB];  // A tile, then B tile
-  __shared__ __attribute__((aligned(16))) uint8_t sT1[kStageA + kStageB];
-  __shared__ __attribute__((aligned(16))) uint8_t sT2[kStageA + kStageB];
-  __shared__ __attribute__((aligned(16))) float sS0[2 * kBM];
-  __shared__ __attribute__((aligned(16))) float sS1[2 * kBM];
-  __shared__ __attribute__((aligned(16))) float sS2[2 * kBM];
+  __shared__ __attribute__((aligned(16))) uint8_t sT0[kStage];  // A tile, then B tile
+  __shared__ __attribute__((aligned(16))) uint8_t sT1[kStage];
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageSA];  // A scales of sT0's block
+  __shared__ __attribute__((aligned(16))) uint8_t sA1[kStageSA];
+  __shared__ __attribute__((aligned(16))) float sR0[2 * kBM];  // scale ratio per (half, row)
+  __shared__ __attribute__((aligned(16))) float sR1[2 * kBM];
+  __shared__ __attribute__((aligned(16))) float sLast[2 * kBM];  // last block scale
   __shared__ int sSrc[kBM];
   __shared__ float sRed[2][kBM];
+  __shared__ float sW[2][kMaxKB];  // weight block scales of the two column halves
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 3, wn = wave >> 2;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  // Row group wm, column half wn. Waves run on SIMD wave % 4, so the two column
+  // halves of a row group sit on different SIMDs and a tile of up to 128 rows
+  // keeps all four SIMDs busy.
+  const int wm = wave >> 1, wn = wave & 1;
   const int Kdim = (KIND == 0) ? p.H : p.I;
   const int KB = Kdim / kBK;
   const int NT = (KIND == 0) ? p.I / 128 : p.H / kBN;
@@ -161,17 +174,17 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     wb = (is_sh ? p.wsh : p.w) + (size_t)ej * p.H * p.I;
     wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (p.H / 128) * KB;
   }
-  // Loader: 48 regions of 1 KB (A: 16, B: 32), 6 per wave: A regions 2w, 2w+1 and
-  // B regions 4w..4w+3. Lane l writes region byte l*16 = row l/8, stored chunk l%8.
+  // Loader: 64 regions of 1 KB (A: 32, B: 32), 8 per wave: A regions 4w..4w+3
+  // and B regions 4w..4w+3. Lane l writes region byte l*16 = row l/8, stored
+  // chunk l%8.
   uint32_t off[kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
-    if (i < 2) {
-      const int row = 8 * (2 * wave + i) + (lane >> 3);
+    const int row = 8 * (4 * wave + (i & 3)) + (lane >> 3);
+    if (i < 4) {
       const int src = sSrc[row];
       off[i] = (uint32_t)((src >= 0 ? src : 0) * Kdim + swz(row, lane & 7) * 16);
     } else {
-      const int row = 8 * (4 * wave + i - 2) + (lane >> 3);
       int wrow;
       if (KIND == 0)
         wrow = (row < 128) ? nt * 128 + row : p.I + nt * 128 + (row - 128);
@@ -181,37 +194,55 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     }
   }
   const uint8_t* abase = p.a;
-  // Scale writers: threads 0..255 own (row tid % 128, column half tid / 128) and
-  // store s_a[row] * s_w[half] for each stage.
-  const int srow = tid & (kBM - 1), shalf = (tid >> 7) & 1;
-  const bool swriter = tid < 2 * kBM;
-  const float amask = (swriter && sSrc[srow] >= 0) ? 1.f : 0.f;
-  const float* asp = p.as + (size_t)(sSrc[srow] >= 0 ? sSrc[srow] : 0) * KB;
-  const float* swr;
-  if (KIND == 0)
-    swr = wsb + (size_t)(shalf == 0 ? nt : p.I / 128 + nt) * KB;
-  else
-    swr = wsb + (size_t)(nt * 2 + shalf) * KB;
+  // Scale writers: every thread owns one (row, column half) and keeps the
+  // previous block's scale; invalid rows use scale 1 (never stored). A zero
+  // block scale (an all-zero weight block) repeats the previous scale: that
+  // block's products are zero. The activation scales of a stage's block reach
+  // LDS with its loads (one 4-byte direct-to-LDS load per wave: wave (wm, wn)
+  // fills rows 64 wm + lane of the copy for column half wn);
+  // the weight scales are staged once per tile.
+  // Thread (wave (wm, wn), lane j) owns row 64 wm + j and half wn: the rows its
+  // own wave's scale load fills, so its own vmcnt wait covers them.
+  const int srow = 64 * wm + lane, shalf = wn;
+  const bool svalid = sSrc[srow] >= 0;
+  const uint32_t off_sa = (uint32_t)((sSrc[64 * wm + lane] >= 0 ? sSrc[64 * wm + lane] : 0) * KB * 4);
+  const int sa_dst = (wn * kBM + 64 * wm) * 4;
+  for (int i = tid; i < 2 * KB; i += kBlkThreads) {
+    const int hf = i / KB, kb = i - hf * KB;
+    const int wr = (KIND == 0) ? (hf == 0 ? nt : p.I / 128 + nt) : nt * 2 + hf;
+    sW[hf][kb] = wsb[(size_t)wr * KB + kb];
+  }
+  float s_prev = 0.f;
+  auto ratio = [&](float sa, float sw) {
+    float s = svalid ? sa * sw : 1.f;
+    if (s == 0.f) s = (s_prev != 0.f) ? s_prev : 1.f;
+    const float r = s_prev / s;
+    s_prev = s;
+    return r;
+  };
+  // Writer's activation scale from a stage's scale buffer.
+  auto stage_sa = [&](const uint8_t* ss) { return *(const float*)(ss + (shalf * kBM + srow) * 4); };
 
-  auto issue = [&](uint8_t* sa, int kb) {
+  auto issue = [&](uint8_t* sa, uint8_t* ss, int kb) {
     uint8_t* sb = sa + kStageA;
+    load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, ss + sa_dst);
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-      if (i < 2)
-        load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (2 * wave + i) * 1024);
+      if (i < 4)
+        load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (4 * wave + i) * 1024);
       else
-        load_lds16(wb + off[i] + (size_t)kb * kBK, sb + (4 * wave + i - 2) * 1024);
+        load_lds16(wb + off[i] + (size_t)kb * kBK, sb + (4 * wave + i - 4) * 1024);
     }
   };
 
-  // Accumulators: 2 row tiles (16 rows) x 8 column tiles (16 columns), v_mfma 16x16x128.
-  v4f acc[2][8];
+  // Accumulators: 4 row tiles (16 rows) x 8 column tiles (16 columns).
+  v4f acc[4][8];
 #pragma unroll
-  for (int m = 0; m < 2; ++m)
+  for (int m = 0; m < 4; ++m)
 #pragma unroll
     for (int n = 0; n < 8; ++n) acc[m][n] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  const bool active = 32 * wm < nrows;  // this wave's 32 rows hold at least one row
+  const bool active = 64 * wm < nrows;  // this wave's 64 rows hold at least one row
   const int g = lane >> 4, l16 = lane & 15;
   // B rows of this wave's eight 16-column tiles. gate_up: tiles 0-3 gate columns
   // [64 wn, +64), tiles 4-7 the matching up columns; down: columns [128 wn, +128).
@@ -224,94 +255,57 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
       brow[n] = 128 * wn + 16 * n + l16;
   }
 
-  auto compute = [&](const uint8_t* sa, const float* ssc) {
+  auto compute = [&](const uint8_t* sa, const float* sr) {
     const uint8_t* sb = sa + kStageA;
-    v8i a[2];
-    v4f cs[2][2];  // [row tile][column half]
+    v8i a[4];
+    v4f rr[4][2];  // [row tile][column half]
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      a[m] = lds_frag16(sa, 32 * wm + 16 * m + l16, g);
-      const int r4 = 32 * wm + 16 * m + 4 * g;
-      cs[m][0] = *(const v4f*)&ssc[((KIND == 0) ? 0 : wn) * kBM + r4];
-      cs[m][1] = (KIND == 0) ? *(const v4f*)&ssc[kBM + r4] : cs[m][0];
+    for (int m = 0; m < 4; ++m) {
+      a[m] = lds_frag16(sa, 64 * wm + 16 * m + l16, g);
+      const int r4 = 64 * wm + 16 * m + 4 * g;
+      rr[m][0] = *(const v4f*)&sr[((KIND == 0) ? 0 : wn) * kBM + r4];
+      rr[m][1] = (KIND == 0) ? *(const v4f*)&sr[kBM + r4] : rr[m][0];
     }
-    // Two batches of four column tiles. The fragments of batch 1 are requested
-    // before the MFMAs of batch 0 issue, and each batch's eight MFMAs are
-    // independent, so the MFMA pipe is fed back to back while earlier results
-    // get their fp32 promotion. Both row tiles are always computed (branch-free;
-    // a partial last tile wastes at most 16 rows).
-    v8i b0[4], b1[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b0[j] = lds_frag16(sb, brow[j], g);
+    for (int n = 0; n < 8; ++n) {
+      const v8i b = lds_frag16(sb, brow[n], g);
+      const int hf = (KIND == 0) ? (n >> 2) : 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b1[j] = lds_frag16(sb, brow[4 + j], g);
-#pragma unroll
-    for (int bt = 0; bt < 2; ++bt) {
-      v4f part[2][4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const v8i& b = bt == 0 ? b0[j] : b1[j];
-        part[0][j] = mfma16_fp8(a[0], b);
-        part[1][j] = mfma16_fp8(a[1], b);
-      }
-      const int hf = (KIND == 0) ? bt : 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[0][4 * bt + j] += part[0][j] * cs[0][hf];
-        acc[1][4 * bt + j] += part[1][j] * cs[1][hf];
-      }
+      for (int m = 0; m < 4; ++m) acc[m][n] = mfma16_fp8_acc(a[m], b, acc[m][n] * rr[m][hf]);
     }
-    // Schedule: all LDS fragment reads, the first 8 MFMAs, then each remaining
-    // MFMA followed by the 4 promotion FMAs of an earlier product.
-    __builtin_amdgcn_sched_group_barrier(0x100, 24, 0);  // DS reads
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);   // MFMA
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-    }
-    __builtin_amdgcn_sched_group_barrier(0x002, 40, 0);   // VALU
   };
 
-  // Raw scales ride a 3-slot register ring indexed by the unrolled step position
-  // (no loop-carried copies, which would wait on the loads in flight).
-  float ra[3] = {0.f, 0.f, 0.f}, rw[3] = {0.f, 0.f, 0.f};
-  issue(sT0, 0);
-  if (KB > 1) issue(sT1, 1);
-  ra[0] = asp[0];
-  rw[0] = swr[0];
-  ra[1] = asp[min(1, KB - 1)];
-  rw[1] = swr[min(1, KB - 1)];
+  // Prologue: block 0 and its scales.
+  issue(sT0, sA0, 0);
   wait_vm<0>();
-  if (swriter) sS0[shalf * kBM + srow] = ra[0] * rw[0] * amask;
+  __syncthreads();  // sW and block 0's stage
+  (shalf ? sR0 + kBM : sR0)[srow] = ratio(stage_sa(sA0), sW[shalf][0]);  // 0: the accumulators start at 0
   __syncthreads();
 
-  // pos = kb % 3; na_: stage of block kb + 2; n1s: scale slot of block kb + 1
-  auto step = [&](int kb, int pos, const uint8_t* ca, const float* cs_, uint8_t* na_,
-                  float* n1s) {
-    // Every step issues the same 8 vector-memory ops (past the last block it
-    // re-reads block KB - 1 into a stage that is not read again), so the
-    // in-order vmcnt wait below is exact on every path.
-    const int kn = min(kb + 2, KB - 1);
-    ra[(pos + 2) % 3] = asp[kn];
-    rw[(pos + 2) % 3] = swr[kn];
-    issue(na_, kn);
+  // One step: loads of block kb + 1 (scales first) into the other stage, the
+  // MFMAs of block kb, then the ratios of block kb + 1 once its loads landed.
+  auto step = [&](int kb, const uint8_t* ca, const float* cr, uint8_t* na, uint8_t* nsa, float* nr) {
+    // Every step issues the same loads (past the last block it re-reads block
+    // KB - 1 into the stage that is not read again), so the waits stay exact.
+    const int kn = min(kb + 1, KB - 1);
+    issue(na, nsa, kn);
     __builtin_amdgcn_sched_barrier(0);
-    if (active) compute(ca, cs_);
+    if (active) compute(ca, cr);
     __builtin_amdgcn_sched_barrier(0);
-    // Issue order per step: 2 scale loads, then 6 tile loads. Block kb + 1's tile
-    // loads (previous step) are followed by this step's 8 ops.
-    wait_vm<2 + kDmaPerWave>();
-    if (kb + 1 < KB && swriter) n1s[shalf * kBM + srow] = ra[(pos + 1) % 3] * rw[(pos + 1) % 3] * amask;
+    // Past the last block the ratio of the re-read block is 1 and lands in a
+    // stage that is not read again.
+    wait_vm<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    (shalf ? nr + kBM : nr)[srow] = ratio(stage_sa(nsa), sW[shalf][kn]);
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
   };
-  for (int kb = 0; kb < KB; kb += 3) {
-    step(kb, 0, sT0, sS0, sT2, sS1);
-    if (kb + 1 < KB) step(kb + 1, 1, sT1, sS1, sT0, sS2);
-    if (kb + 2 < KB) step(kb + 2, 2, sT2, sS2, sT1, sS0);
+  for (int kb = 0; kb < KB; kb += 2) {
+    step(kb, sT0, sR0, sT1, sA1, sR1);
+    if (kb + 1 < KB) step(kb + 1, sT1, sR1, sT0, sA0, sR0);
   }
+  (shalf ? sLast + kBM : sLast)[srow] = s_prev;
   __syncthreads();
 
   // Accumulator layout (16x16): lane l, register i holds D[4*(l/16) + i][l%16].
@@ -319,31 +313,31 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     // h = SiLU(gate) * up for this wave's 64 h columns; the row amax of the 1x128
     // group combines the two column-half waves through LDS.
     const int GI = p.I / 128;
-    float amax[2][4];
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        const int row = 64 * wm + 16 * m + 4 * g + i;
+        const float sg_ = sLast[row], su = sLast[kBM + row];
         float mx = 0.f;
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          const float gt = acc[m][n][i], up = acc[m][n + 4][i];
+          const float gt = acc[m][n][i] * sg_, up = acc[m][n + 4][i] * su;
           const float h = gt / (1.0f + __expf(-gt)) * up;
           acc[m][n][i] = h;
           mx = fmaxf(mx, fabsf(h));
         }
 #pragma unroll
         for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        amax[m][i] = mx;
-        if (l16 == 0) sRed[wn][32 * wm + 16 * m + 4 * g + i] = mx;
+        if (l16 == 0) sRed[wn][row] = mx;
       }
     __syncthreads();
     if (active) {
 #pragma unroll
-      for (int m = 0; m < 2; ++m)
+      for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int row = 32 * wm + 16 * m + 4 * g + i;
+          const int row = 64 * wm + 16 * m + 4 * g + i;
           if (row < nrows && sSrc[row] >= 0) {
             const long slot = slot0 + row;
             const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
@@ -356,18 +350,18 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
           }
         }
     }
-    (void)amax;
   } else if (active) {
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = 32 * wm + 16 * m + 4 * g + i;
+        const int row = 64 * wm + 16 * m + 4 * g + i;
         if (row < nrows) {
           const long slot = slot0 + row;
+          const float sl = sLast[wn * kBM + row];
 #pragma unroll
           for (int n = 0; n < 8; ++n)
-            p.y[(size_t)slot * p.H + nt * kBN + 128 * wn + 16 * n + l16] = f32_to_bf16_bits(acc[m][n][i]);
+            p.y[(size_t)slot * p.H + nt * kBN + 128 * wn + 16 * n + l16] = f32_to_bf16_bits(acc[m][n][i] * sl);
         }
       }
   }
@@ -504,6 +498,8 @@ static int block_gemm_common_checks(const char* _moe_fn, int T, int H, int I, in
   MOE_CHECK_ARG(T > 0 && E > 0 && NB >= 0 && max_tiles > 0, "bad sizes");
   MOE_CHECK_ARG(H > 0 && H % 256 == 0 && I > 0 && I % 128 == 0,
                 "H must be a multiple of 256 and I of 128 (H=%d I=%d)", H, I);
+  MOE_CHECK_SUPPORTED(H / 128 <= kMaxKB && I / 128 <= kMaxKB,
+                      "H and I must be at most %d (H=%d I=%d)", 128 * kMaxKB, H, I);
   return MOE_OK;
 }
 
