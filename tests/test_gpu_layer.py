@@ -151,6 +151,41 @@ def test_layer_dsv3_full_size(cuda, T, idx, tokens):
     torch.cuda.empty_cache()
 
 
+@pytest.fixture(scope="module")
+def kimi_weights(cuda):
+    w = _big_weights(PRESETS["kimi_k2"], 3, cuda)
+    yield w
+    del w
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("T,tokens", [(1, [0]), (256, [0, 131, 255]), (16384, [0, 9001, 16383])])
+def test_layer_kimi_k2_full_size(cuda, kimi_weights, T, tokens):
+    """Kimi-K2 layer (384 experts + 1 shared, sigmoid top-8 over one group, x2.827) at the
+    ends and middle of its token sweep: 1 token (row tiles), 256, and 16384 (block
+    kernels, ~341 rows per expert)."""
+    cfg = PRESETS["kimi_k2"]
+    say("layer kimi-k2 full", T)
+    x = synthetic.hidden_states(T, cfg.hidden, 3).to(cuda)
+    _check_layer(cfg, kimi_weights, x, tokens=tokens, tag=f"kimi T={T}")
+
+
+def test_layer_glm45_full_size_zipf(cuda):
+    """GLM-4.5 layer (hidden 5120, intermediate 1536, 160 experts + 1 shared) at 4096
+    tokens with Zipf(1.2) expert popularity and 10% of the experts empty: overfull
+    experts span many 256-row tiles, empty ones none."""
+    cfg = PRESETS["glm45"]
+    say("layer glm-4.5 full zipf")
+    w = synthetic.make_weights(cfg, 4, device=cuda, zipf=True, experts_device=cuda)
+    x = synthetic.hidden_states(4096, cfg.hidden, 4).to(cuda)
+    out = _check_layer(cfg, w, x, tokens=[0, 1234, 4095], tag="glm45 T=4096")
+    ids = ops.layer_forward(x, w, cfg, return_routing=True)[1].cpu().numpy()
+    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
+    assert (counts == 0).sum() >= 16 and counts.max() > 3 * counts[counts > 0].mean()
+    del w, out
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("T,E,K,S", [(2048, 8, 2, 0), (3000, 16, 4, 1), (700, 4, 2, 1)])
 def test_layer_block_kernels(cuda, T, E, K, S):
     """Prefill-sized path (> 64 rows per expert): block kernels against the oracle,
