@@ -14,6 +14,8 @@ Phases:
      two expert GEMMs on the launch stream, for the per-kernel roofline.
   C  the same layer at prefill (8192 tokens), reported under "prefill8k".
   D  the CPU oracle on a bounded token sample (rank 0, N = 1 only).
+With --extra it also times the Kimi-K2 layer over 1..16384 tokens and the
+GLM-4.5 layer with Zipf-skewed routing (reported under "extra").
 Prints one JSON line.
 """
 import argparse
@@ -117,6 +119,46 @@ def time_layer(x, w, cfg, steps, warmup, torch, ops):
     return (time.perf_counter() - t0) / steps
 
 
+def workload_report(name, x, w, cfg, steps, torch, ops):
+    """Whole-layer timing of one extra workload with its algorithmic roofline."""
+    T = x.shape[0]
+    H, I, E = cfg.hidden, cfg.intermediate, cfg.n_experts
+    sec = time_layer(x, w, cfg, steps, 2, torch, ops)
+    ids = ops.layer_forward(x, w, cfg, return_routing=True)[1]
+    active, rows = layer_counts(ids, E)
+    flops = 2 * (rows + T * cfg.n_shared) * 3 * H * I + 2 * T * H * E
+    nbytes = ((active + cfg.n_shared) * (expert_bytes(H, I, "gate_up") + expert_bytes(H, I, "down"))
+              + E * H * 2 + T * H * 2 * 2)
+    return {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
+            "tokens_per_s": round(T / sec, 1), "active_experts": active,
+            "alg_bytes": nbytes, "alg_flops": flops,
+            "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "mfma_frac": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4),
+            "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
+
+
+def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev):
+    """Kimi-K2 over its token sweep and GLM-4.5 with Zipf-skewed routing."""
+    out = []
+    cfg = PRESETS["kimi_k2"]
+    w = synthetic.make_weights(cfg, 3, device=dev, experts_device=dev)
+    for T in (1, 16, 256, 2048, 16384):
+        print(f"[bench] extra: kimi_k2 T={T}", file=sys.stderr, flush=True)
+        x = synthetic.hidden_states(T, cfg.hidden, 3).to(dev)
+        out.append(workload_report(f"Kimi-K2 MoE layer, {T} tokens", x, w, cfg, steps, torch, ops))
+    del w
+    torch.cuda.empty_cache()
+    cfg = PRESETS["glm45"]
+    print("[bench] extra: glm45 T=4096 zipf", file=sys.stderr, flush=True)
+    w = synthetic.make_weights(cfg, 4, device=dev, zipf=True, experts_device=dev)
+    x = synthetic.hidden_states(4096, cfg.hidden, 4).to(dev)
+    out.append(workload_report("GLM-4.5 MoE layer, 4096 tokens, Zipf(1.2) routing, 10% empty experts",
+                               x, w, cfg, steps, torch, ops))
+    del w
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(x, w, cfg, n_tokens):
     """The oracle (numpy, fp32) on the first n_tokens tokens of the workload."""
     import numpy as np
@@ -151,6 +193,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--extra", action="store_true",
+                    help="also time Kimi-K2 (1..16384 tokens) and GLM-4.5 (Zipf) layers")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the layer keeps all experts "
@@ -251,6 +295,10 @@ def main():
             "value": round(tps, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"first {args.cpu_tokens} of the 64 decode tokens ({nexp} routed experts + shared, "
                       f"full layer math incl. per-expert dequant), numpy fp32 BLAS, {dt:.1f} s"}
+    if args.extra:
+        del w
+        torch.cuda.empty_cache()
+        result["extra"] = extra_workloads(max(3, args.steps // 4), torch, ops, synthetic, PRESETS, dev)
     print(json.dumps(result))
 
 
