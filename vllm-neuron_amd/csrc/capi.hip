@@ -58,11 +58,12 @@ struct LayerWs {
   size_t bytes;
 };
 
-// The 256x256 ("block") kernels take over above 16 rows per expert on average:
-// measured on the DeepSeek-V3 and Kimi-K2 layers they beat every row-tile height
-// from there on (equal at 16, 18-38% faster at 32-64 rows).
+// The 256x256 ("block") kernels take over above 12 rows per expert on average:
+// measured on the DeepSeek-V3 and Kimi-K2 layers they lose to 16-row tiles at 8
+// rows (+23%) and beat every row-tile height from 16 rows on (5% at 16, 20-40%
+// at 32-64 rows).
 static bool use_block(int T, int K, int E) {
-  return ((long)T * std::min(K, E) + E - 1) / E > 16;
+  return ((long)T * std::min(K, E) + E - 1) / E > 12;
 }
 
 static inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }

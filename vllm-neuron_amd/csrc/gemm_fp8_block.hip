@@ -223,15 +223,22 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   // Writer's activation scale from a stage's scale buffer.
   auto stage_sa = [&](const uint8_t* ss) { return *(const float*)(ss + (shalf * kBM + srow) * 4); };
 
+  // A regions past the tile's last row are not loaded: their rows are never
+  // stored, and every step ends with a full vmcnt wait, so skipped loads need no
+  // accounting.
+  bool a_live[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a_live[i] = 8 * (4 * wave + i) < nrows;  // wave-uniform
   auto issue = [&](uint8_t* sa, uint8_t* ss, int kb) {
     uint8_t* sb = sa + kStageA;
     load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, ss + sa_dst);
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-      if (i < 4)
-        load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (4 * wave + i) * 1024);
-      else
+      if (i < 4) {
+        if (a_live[i]) load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (4 * wave + i) * 1024);
+      } else {
         load_lds16(wb + off[i] + (size_t)kb * kBK, sb + (4 * wave + i - 4) * 1024);
+      }
     }
   };
 

@@ -44,9 +44,9 @@ def num_blocks(T, K, E, B):
 
 
 def use_block_kernels(T, K, E):
-    """The layer switches to the 256x256 block kernels above 16 rows per expert on
+    """The layer switches to the 256x256 block kernels above 12 rows per expert on
     average (the measured crossover against every row-tile height)."""
-    return -(-T * min(K, E) // E) > 16
+    return -(-T * min(K, E) // E) > 12
 
 
 def choose_mt(T, K, E):
