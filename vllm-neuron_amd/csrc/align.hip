@@ -110,17 +110,35 @@ __global__ __launch_bounds__(256) void map_count_kernel(
   }
 }
 
+// Inclusive sum over the 1024 threads of a workgroup (wave scans, then the
+// 16 wave totals); s_wave holds 16 ints.
+__device__ __forceinline__ int block_inclusive_sum(int v, int* s_wave) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  if (lane == 63) s_wave[wave] = v;
+  __syncthreads();
+  int add = 0;
+  for (int q = 0; q < wave; ++q) add += s_wave[q];
+  __syncthreads();
+  return v + add;
+}
+
 __global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int N, int nchunks,
                                                         int32_t* __restrict__ expert_counts,
                                                         int32_t* __restrict__ block_to_expert,
                                                         int32_t* __restrict__ conditions,
-                                                        MapWs ws) {
+                                                        MapWs ws, TileOut to) {
   __shared__ int s_blk[kMapMaxE];
-  __shared__ int s_scan[kMapMaxE];
+  __shared__ int s_cnt[kMapMaxE];
+  __shared__ int s_tile[kMapMaxE];
+  __shared__ int s_wave[16];
   const int tid = threadIdx.x;
-  int blk = 0;
+  int blk = 0, run = 0;
   if (tid < E) {
-    int run = 0;
     for (int c = 0; c < nchunks; ++c) {
       int v = ws.chunk_counts[(size_t)c * E + tid];
       ws.chunk_base[(size_t)c * E + tid] = run;
@@ -129,21 +147,14 @@ __global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int
     if (expert_counts != nullptr) expert_counts[tid] = run;
     blk = (run + B - 1) / B;
   }
-  s_scan[tid] = blk;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over 1024 entries.
-  for (int o = 1; o < kMapMaxE; o <<= 1) {
-    int v = (tid >= o) ? s_scan[tid - o] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
-  }
+  const int cum = block_inclusive_sum(blk, s_wave);
   if (tid < E) {
-    ws.block_off[tid] = s_scan[tid] - blk;  // exclusive
-    s_blk[tid] = s_scan[tid];               // inclusive cumulative blocks
+    ws.block_off[tid] = cum - blk;  // exclusive
+    s_blk[tid] = cum;               // inclusive cumulative blocks
+    s_cnt[tid] = run;
   }
   __syncthreads();
-  const int total = s_scan[E - 1];
+  const int total = s_blk[E - 1];
   // block_to_expert[b] = #{ e < E-1 : cum[e] <= b }   (cum non-decreasing)
   for (int b = tid; b < N; b += blockDim.x) {
     int lo = 0, hi = E - 1;  // search in cum[0 .. E-2]
@@ -155,6 +166,48 @@ __global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int
     block_to_expert[b] = lo;
     if (conditions != nullptr) conditions[b] = (b < total) ? 1 : 0;
   }
+  if (to.tiles == nullptr) return;  // workgroup-uniform
+  // Tile list from the counts. Expert e owns slots [off_e*B, off_e*B + c_e),
+  // so its tiles follow without reading token_position_to_id: per block
+  // ceil(rows/mt) tiles (row tiles), or ceil(c_e/mt) tiles running across the
+  // expert's blocks (block tiles, span = 1).
+  const int mt = to.mt, tpb = (B + mt - 1) / mt;
+  int nt = 0;
+  if (tid < E)
+    nt = to.span ? (run + mt - 1) / mt : (run / B) * tpb + (run % B + mt - 1) / mt;
+  const int tcum = block_inclusive_sum(nt, s_wave);
+  if (tid < E) s_tile[tid] = tcum;
+  __syncthreads();
+  const int ntiles = s_tile[E - 1];
+  for (int i = tid; i < ntiles && i < to.max_tiles; i += blockDim.x) {
+    int lo = 0, hi = E - 1;  // first e with s_tile[e] > i
+    while (lo < hi) {
+      int mid = (lo + hi) >> 1;
+      if (s_tile[mid] <= i) lo = mid + 1;
+      else hi = mid;
+    }
+    const int e = lo, first = (e > 0) ? s_tile[e - 1] : 0, loc = i - first;
+    const int c = s_cnt[e];
+    const long base = (long)(s_blk[e] - (c + B - 1) / B) * B;
+    if (to.span) {
+      to.tiles[i] = make_int4(e, (int)(base + (long)loc * mt), min(mt, c - loc * mt), 0);
+      to.seg[i] = make_int2(first, s_tile[e] - first);
+    } else {
+      const int j = loc / tpb, m = loc - j * tpb;
+      const int rows = min(B, c - j * B);
+      to.tiles[i] = make_int4(e, (int)(base + (long)j * B + m * mt), min(mt, rows - m * mt), 0);
+    }
+  }
+  const int per = (T + mt - 1) / mt;
+  const long nb_total = (long)N * B;
+  for (int i = tid; i < to.n_shared * per; i += blockDim.x) {
+    const int j = i / per, m = i - j * per, idx = ntiles + i;
+    if (idx < to.max_tiles) {
+      to.tiles[idx] = make_int4(E + j, (int)(nb_total + (long)j * T + (long)m * mt), min(mt, T - m * mt), 0);
+      if (to.span) to.seg[idx] = make_int2(ntiles + j * per, per);
+    }
+  }
+  if (tid == 0) to.num_tiles[0] = min(ntiles + to.n_shared * per, to.max_tiles);
 }
 
 __global__ __launch_bounds__(256) void map_scatter_kernel(
@@ -313,14 +366,16 @@ extern "C" size_t moe_mapping_workspace_bytes(int T, int E) {
   return map_ws_bytes(std::max(T, 1), E);
 }
 
-extern "C" int moe_blockwise_mapping(const int32_t* ids, const float* affinities,
-                                     const uint8_t* padding_mask, int T, int K, int E, int B,
-                                     int N, int32_t* token_position_to_id,
-                                     int32_t* block_to_expert, int32_t* conditions,
-                                     int32_t* expert_counts, int32_t* inv_pos,
-                                     float* affinities_masked, void* workspace,
-                                     size_t workspace_bytes, void* stream) {
+int moe::blockwise_mapping(const int32_t* ids, const float* affinities,
+                           const uint8_t* padding_mask, int T, int K, int E, int B, int N,
+                           int32_t* token_position_to_id, int32_t* block_to_expert,
+                           int32_t* conditions, int32_t* expert_counts, int32_t* inv_pos,
+                           float* affinities_masked, void* workspace, size_t workspace_bytes,
+                           const TileOut& to, void* stream) {
   MOE_API_BEGIN("moe_blockwise_mapping");
+  MOE_CHECK_ARG(to.tiles == nullptr || (to.num_tiles && to.mt > 0 && to.max_tiles > 0 &&
+                                        to.n_shared >= 0 && (!to.span || to.seg)),
+                "bad tile output");
   MOE_CHECK_ARG((ids != nullptr) != (affinities != nullptr),
                 "exactly one of ids / affinities must be given");
   MOE_CHECK_ARG(token_position_to_id && block_to_expert && workspace, "null pointer argument");
@@ -339,10 +394,23 @@ extern "C" int moe_blockwise_mapping(const int32_t* ids, const float* affinities
   hipLaunchKernelGGL(map_count_kernel, dim3(grid1), dim3(256), 0, st, ids, affinities,
                      padding_mask, affinities_masked, T, K, E, nch, nbt, token_position_to_id, ws);
   hipLaunchKernelGGL(map_scan_kernel, dim3(1), dim3(1024), 0, st, T, E, B, N, nch, expert_counts,
-                     block_to_expert, conditions, ws);
+                     block_to_expert, conditions, ws, to);
   hipLaunchKernelGGL(map_scatter_kernel, dim3(nch), dim3(256), 0, st, ids, affinities, T, K, E, B,
                      nbt, token_position_to_id, inv_pos, ws);
   MOE_API_END();
+}
+
+extern "C" int moe_blockwise_mapping(const int32_t* ids, const float* affinities,
+                                     const uint8_t* padding_mask, int T, int K, int E, int B,
+                                     int N, int32_t* token_position_to_id,
+                                     int32_t* block_to_expert, int32_t* conditions,
+                                     int32_t* expert_counts, int32_t* inv_pos,
+                                     float* affinities_masked, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  return moe::blockwise_mapping(ids, affinities, padding_mask, T, K, E, B, N,
+                                token_position_to_id, block_to_expert, conditions, expert_counts,
+                                inv_pos, affinities_masked, workspace, workspace_bytes, TileOut{},
+                                stream);
 }
 
 extern "C" int moe_mapping_status(const void* workspace, void* stream, int* dropped) {

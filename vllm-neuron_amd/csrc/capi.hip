@@ -53,8 +53,6 @@ struct LayerWs {
   uint16_t* y;
   int32_t* btiles;
   int32_t* bnum;
-  void* btiles_ws;
-  size_t btiles_ws_bytes;
   size_t bytes;
 };
 
@@ -105,8 +103,6 @@ static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, in
     const int mbt = moe_max_block_tiles(T, K, E, N, B, n_sh);
     w.btiles = (int32_t*)take((size_t)mbt * 24);
     w.bnum = (int32_t*)take(16);
-    w.btiles_ws_bytes = moe_block_tiles_workspace_bytes(N, mbt);
-    w.btiles_ws = take(w.btiles_ws_bytes);
   }
   w.bytes = off;
   return w;
@@ -169,13 +165,28 @@ extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E,
                              w.router_ws_bytes, stream));
   MOE_STEP(moe_router_topk(logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
                            renorm_eps, routed_scale, ids, wts, nullptr, stream));
-  MOE_STEP(moe_blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond,
-                                 w.counts, w.inv, nullptr, w.map_ws, w.map_ws_bytes, stream));
+  // The mapping's scan kernel also writes the expert tile list, from the counts.
+  const bool block = use_block(T, K, E);
+  const int mbt = block ? moe_max_block_tiles(T, K, E, N, B, n_shared) : 0;
+  TileOut to{};
+  if (block) {
+    to.tiles = (int4*)w.btiles;
+    to.seg = (int2*)(w.btiles + 4 * (size_t)mbt);
+    to.num_tiles = w.bnum;
+    to.max_tiles = mbt;
+    to.mt = kBlockTileRows;
+    to.span = 1;
+  } else {
+    to.tiles = (int4*)w.tiles;
+    to.num_tiles = w.num_tiles;
+    to.max_tiles = max_tiles;
+    to.mt = mt;
+  }
+  to.n_shared = n_shared;
+  MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
+                             w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
   MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
-  if (use_block(T, K, E)) {
-    const int mbt = moe_max_block_tiles(T, K, E, N, B, n_shared);
-    MOE_STEP(moe_build_block_tiles(w.tpid, w.b2e, N, B, T, E, n_shared, w.btiles, mbt, w.bnum,
-                                   w.btiles_ws, w.btiles_ws_bytes, stream));
+  if (block) {
     MOE_STEP(moe_expert_gate_up_block(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
                                       w13_shared_scale, n_shared, w.tpid, (int)NB, w.btiles,
                                       w.bnum, mbt, w.hq, w.hs, stream));
@@ -183,8 +194,6 @@ extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E,
                                    w2_shared_scale, n_shared, (int)NB, w.btiles, w.bnum, mbt,
                                    w.y, stream));
   } else {
-    MOE_STEP(moe_build_tiles(w.tpid, w.b2e, N, B, T, E, n_shared, mt, w.tiles, max_tiles,
-                             w.num_tiles, stream));
     MOE_STEP(moe_expert_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
                                 w13_shared_scale, n_shared, w.tpid, (int)NB, w.tiles,
                                 w.num_tiles, max_tiles, mt, w.hq, w.hs, stream));

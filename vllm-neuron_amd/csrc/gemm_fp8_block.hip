@@ -36,6 +36,7 @@
 namespace moe {
 
 constexpr int kBM = 256, kBN = 256, kBK = 128;
+static_assert(kBM == kBlockTileRows, "block tile rows");
 constexpr int kBlkThreads = 512;
 constexpr int kStageA = kBM * kBK;  // 32 KB
 constexpr int kStageB = kBN * kBK;  // 32 KB

@@ -22,6 +22,30 @@ inline int router_logits_splits(int T, int H, int E) {
   return (int)std::max(1L, std::min(ks, kmax));
 }
 
+// Rows per tile of the 256x256 expert GEMM kernels.
+constexpr int kBlockTileRows = 256;
+
+// Tile list written by the mapping's scan kernel from the expert counts
+// (tiles == nullptr: none). Row tiles stay inside one block; block tiles
+// (span = 1) run across an expert's blocks and carry seg = (first tile of the
+// expert, its tile count). Shared-expert tiles follow the routed ones.
+struct TileOut {
+  int4* tiles;
+  int2* seg;
+  int32_t* num_tiles;
+  int max_tiles;
+  int mt;
+  int span;
+  int n_shared;
+};
+
+// moe_blockwise_mapping plus an optional tile list (same checks and errors).
+int blockwise_mapping(const int32_t* ids, const float* affinities, const uint8_t* padding_mask,
+                      int T, int K, int E, int B, int N, int32_t* token_position_to_id,
+                      int32_t* block_to_expert, int32_t* conditions, int32_t* expert_counts,
+                      int32_t* inv_pos, float* affinities_masked, void* workspace,
+                      size_t workspace_bytes, const TileOut& to, void* stream);
+
 }  // namespace moe
 
 #define MOE_API_BEGIN(name)   \

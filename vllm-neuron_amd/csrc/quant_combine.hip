@@ -32,46 +32,63 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
 
 // out[t] = sum_s w[t,s] * y[inv[t,s]] (inv >= 0) + sum_j y[NB + j*T + t], fp32 accumulation,
 // one workgroup per token, 8 bf16 (16 B) per thread per step.
+// One workgroup per (token, column chunk). The token's live rows are listed in
+// slot order (ballot compaction, so the order and the fp32 sums are the same as a
+// sequential scan), then each thread sums its 8 columns over the rows, loading
+// four rows ahead of the accumulation.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const int32_t* __restrict__ inv,
                                                       const float* __restrict__ w, int S, int T,
-                                                      int H, long NB, int n_shared,
+                                                      int H, long NB, int n_shared, int col_chunk,
                                                       uint16_t* __restrict__ out) {
   __shared__ long s_row[1024 + 16];
   __shared__ float s_w[1024 + 16];
-  __shared__ int s_n;
-  const int t = blockIdx.x;
-  if (threadIdx.x == 0) {
-    int n = 0;
-    for (int s = 0; s < S; ++s) {
-      int p = inv[(size_t)t * S + s];
-      if (p >= 0) {
-        s_row[n] = p;
-        s_w[n] = (w != nullptr) ? w[(size_t)t * S + s] : 1.f;
-        ++n;
-      }
+  __shared__ int s_wave_n[4];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int n = 0;
+  for (int s0 = 0; s0 < S; s0 += 256) {
+    const int s = s0 + tid;
+    const int p = (s < S) ? inv[(size_t)t * S + s] : -1;
+    const unsigned long long live = __ballot(p >= 0);
+    if (lane == 0) s_wave_n[wave] = __popcll(live);
+    __syncthreads();
+    int before = n;
+    for (int q = 0; q < wave; ++q) before += s_wave_n[q];
+    if (p >= 0) {
+      const int pos = before + __popcll(live & ((1ull << lane) - 1ull));
+      s_row[pos] = p;
+      s_w[pos] = (w != nullptr) ? w[(size_t)t * S + s] : 1.f;
     }
-    for (int j = 0; j < n_shared; ++j) {
-      s_row[n] = NB + (long)j * T + t;
-      s_w[n] = 1.f;
-      ++n;
-    }
-    s_n = n;
+    n += s_wave_n[0] + s_wave_n[1] + s_wave_n[2] + s_wave_n[3];
+    __syncthreads();
   }
+  if (tid < n_shared) {
+    s_row[n + tid] = NB + (long)tid * T + t;
+    s_w[n + tid] = 1.f;
+  }
+  n += n_shared;
   __syncthreads();
-  const int n = s_n;
-  for (int c = threadIdx.x; c < H / 8; c += blockDim.x) {
+  const int c_begin = blockIdx.y * col_chunk, c_end = min(H / 8, c_begin + col_chunk);
+  for (int c = c_begin + tid; c < c_end; c += blockDim.x) {
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-    for (int r = 0; r < n; ++r) {
-      const float wt = s_w[r];
-      int4 v = *(const int4*)(y + (size_t)s_row[r] * H + c * 8);
-      const uint32_t u[4] = {(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+    for (int r0 = 0; r0 < n; r0 += 4) {
+      int4 v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += wt * bf16_bits_to_f32((uint16_t)(u[i] & 0xffffu));
-        acc[2 * i + 1] += wt * bf16_bits_to_f32((uint16_t)(u[i] >> 16));
+      for (int q = 0; q < 4; ++q)
+        if (r0 + q < n) v[q] = *(const int4*)(y + (size_t)s_row[r0 + q] * H + c * 8);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (r0 + q < n) {
+          const float wt = s_w[r0 + q];
+          const uint32_t u[4] = {(uint32_t)v[q].x, (uint32_t)v[q].y, (uint32_t)v[q].z, (uint32_t)v[q].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[2 * i] += wt * bf16_bits_to_f32((uint16_t)(u[i] & 0xffffu));
+            acc[2 * i + 1] += wt * bf16_bits_to_f32((uint16_t)(u[i] >> 16));
+          }
+        }
       }
     }
     int4 o;
@@ -112,8 +129,13 @@ extern "C" int moe_combine(const void* y_bf16, const int32_t* inv, const float* 
   MOE_CHECK_ARG(((uintptr_t)y_bf16 & 15) == 0 && ((uintptr_t)out_bf16 & 15) == 0,
                 "y and out must be 16-byte aligned");
   if (T == 0) return MOE_OK;
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)y_bf16, inv, w, S, T, H, (long)NB, n_shared,
+  // Enough (token, column chunk) workgroups to cover the chip: at least 512.
+  const int chunks = H / 8;
+  int splits = std::max(1, std::min((512 + T - 1) / T, (chunks + 127) / 128));
+  const int col_chunk = (chunks + splits - 1) / splits;
+  splits = (chunks + col_chunk - 1) / col_chunk;
+  hipLaunchKernelGGL(combine_kernel, dim3(T, splits), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)y_bf16, inv, w, S, T, H, (long)NB, n_shared, col_chunk,
                      (uint16_t*)out_bf16);
   MOE_API_END();
 }
