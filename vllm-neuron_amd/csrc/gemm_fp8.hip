@@ -107,23 +107,31 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
     }
     __syncthreads();
 
-    // activation chunk sources
+    // Activation chunk sources. Every load below is issued unconditionally (chunks
+    // and scales without a row read row 0 and are zeroed after the load), so the
+    // compiler counts the loads in flight exactly and keeps the weight prefetch
+    // ring in flight instead of draining it.
     const uint8_t* aptr[APT];
     int aoff[APT];
+    bool alive[APT];
 #pragma unroll
     for (int c = 0; c < APT; ++c) {
       const int chunk = tid + 256 * c;
-      aptr[c] = nullptr;
+      aptr[c] = p.a;
       aoff[c] = -1;
+      alive[c] = false;
       if (chunk < ACH) {
         const int row = chunk >> 3, col = (chunk & 7) * 16;
         aoff[c] = row * LDA + col;
         const long src = sSrc[row];
-        if (src >= 0) aptr[c] = p.a + (size_t)src * Kdim + col;
+        if (src >= 0) {
+          aptr[c] = p.a + (size_t)src * Kdim + col;
+          alive[c] = true;
+        }
       }
     }
-    const float* asp = nullptr;
-    if (tid < MT && sSrc[tid] >= 0) asp = p.as + (size_t)sSrc[tid] * KB;
+    const bool as_alive = tid < MT && sSrc[tid] >= 0;
+    const float* asp = as_alive ? p.as + (size_t)sSrc[tid] * KB : p.as;
 
     // weight fragments and scale rows
     const uint8_t* wb;
@@ -159,16 +167,16 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
       for (int j = 0; j < 4; ++j) bq[slot][j] = load_frag_global(bp[j] + (size_t)kb * MOE_GROUP);
 #pragma unroll
       for (int c = 0; c < APT; ++c)
-        aq[slot][c] = aptr[c] ? *(const int4*)(aptr[c] + (size_t)kb * MOE_GROUP) : make_int4(0, 0, 0, 0);
-      asq[slot] = asp ? asp[kb] : 0.f;
+        aq[slot][c] = *(const int4*)(aptr[c] + (alive[c] ? (size_t)kb * MOE_GROUP : 0));
+      asq[slot] = asp[as_alive ? kb : 0];
       swq[slot][0] = sw0[kb];
       swq[slot][1] = sw1[kb];
     };
     auto store_A = [&](int buf, int slot) {
 #pragma unroll
       for (int c = 0; c < APT; ++c)
-        if (aoff[c] >= 0) *(int4*)&sA[buf][aoff[c]] = aq[slot][c];
-      if (tid < MT) sAs[buf][tid] = asq[slot];
+        if (aoff[c] >= 0) *(int4*)&sA[buf][aoff[c]] = alive[c] ? aq[slot][c] : make_int4(0, 0, 0, 0);
+      if (tid < MT) sAs[buf][tid] = as_alive ? asq[slot] : 0.f;
     };
 
     v4f acc[MS][4];
@@ -178,35 +186,40 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
       for (int j = 0; j < 4; ++j) acc[ms][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-    for (int s = 0; s < PD - 1; ++s)
-      if (s < KB) load_stage(s, s);
+    for (int s = 0; s < PD - 1; ++s) load_stage(s, min(s, KB - 1));
     store_A(0, 0);
     __syncthreads();
 
-    for (int kb0 = 0; kb0 < KB; kb0 += PD) {
+    // One K block: prefetch block kb + PD - 1 (past the end, the last block again,
+    // into a slot that is not read again), MFMAs of block kb from slot s, stage
+    // block kb + 1's activations into the other LDS buffer.
+    auto kstep = [&](int kb, int s) {
+      load_stage((s + PD - 1) % PD, min(kb + PD - 1, KB - 1));
+      const int buf = kb & 1;
 #pragma unroll
-      for (int s = 0; s < PD; ++s) {
-        const int kb = kb0 + s;
-        if (kb < KB) {
-          if (kb + PD - 1 < KB) load_stage((s + PD - 1) % PD, kb + PD - 1);
-          const int buf = kb & 1;
+      for (int ms = 0; ms < MS; ++ms) {
+        const v8i a = load_frag_lds(&sA[buf][(ms * 16 + r16) * LDA + g * 16]);
+        const v4f sa = *(const v4f*)&sAs[buf][ms * 16 + 4 * g];
+        const v4f c0 = sa * swq[s][0];
+        const v4f c1 = sa * swq[s][1];
 #pragma unroll
-          for (int ms = 0; ms < MS; ++ms) {
-            const v8i a = load_frag_lds(&sA[buf][(ms * 16 + r16) * LDA + g * 16]);
-            const v4f sa = *(const v4f*)&sAs[buf][ms * 16 + 4 * g];
-            const v4f c0 = sa * swq[s][0];
-            const v4f c1 = sa * swq[s][1];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const v4f part = mfma_fp8(a, bq[s][j]);
-              acc[ms][j] += part * ((KIND == 0 && j >= 2) ? c1 : c0);
-            }
-          }
-          if (kb + 1 < KB) store_A((kb + 1) & 1, (s + 1) % PD);
-          __syncthreads();
+        for (int j = 0; j < 4; ++j) {
+          const v4f part = mfma_fp8(a, bq[s][j]);
+          acc[ms][j] += part * ((KIND == 0 && j >= 2) ? c1 : c0);
         }
       }
+      if (kb + 1 < KB) store_A((kb + 1) & 1, (s + 1) % PD);
+      // Orders the activation double buffer only; the weight prefetches stay in flight.
+      lds_barrier();
+    };
+    int kb0 = 0;
+    for (; kb0 + PD <= KB; kb0 += PD) {
+#pragma unroll
+      for (int s = 0; s < PD; ++s) kstep(kb0 + s, s);
     }
+#pragma unroll
+    for (int s = 0; s < PD - 1; ++s)
+      if (kb0 + s < KB) kstep(kb0 + s, s);
 
     if (KIND == 0) {
       // h = SiLU(gate) * up, written over the gate accumulators.

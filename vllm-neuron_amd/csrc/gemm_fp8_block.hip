@@ -78,21 +78,6 @@ __device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base)
 }
 
 
-// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt[3:0] | [15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
-// Workgroup barrier that waits only for this wave's LDS operations (lgkmcnt);
-// __syncthreads() would also drain vmcnt. LDS-DMA data is covered by the
-// explicit vmcnt waits.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt untouched
-  __builtin_amdgcn_s_barrier();
-}
-
 // Logical 16-byte chunk c of row r lives at chunk c ^ ((r >> 1) & 7): any 16
 // consecutive rows read at one logical chunk touch 16 distinct 16-byte bank
 // groups of the 64-bank LDS (two 128-byte rows span the banks once).

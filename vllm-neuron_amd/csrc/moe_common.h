@@ -78,6 +78,21 @@ __device__ __forceinline__ float det_sigmoid_f32(float x) {
   return 1.0f / (1.0f + e);
 }
 
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt[3:0] | [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Workgroup barrier that waits only for this wave's LDS operations (lgkmcnt).
+// __syncthreads() also drains vmcnt: it waits for every global load in flight,
+// prefetches included. Direct-to-LDS data needs its own explicit vmcnt wait.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt/expcnt untouched
+  __builtin_amdgcn_s_barrier();
+}
+
 // ---------------------------------------------------------------------------
 // Wave reductions (wave64).
 // ---------------------------------------------------------------------------
