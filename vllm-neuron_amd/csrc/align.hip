@@ -127,30 +127,24 @@ __device__ __forceinline__ int block_inclusive_sum(int v, int* s_wave) {
   return v + add;
 }
 
-__global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int N, int nchunks,
-                                                        int32_t* __restrict__ expert_counts,
-                                                        int32_t* __restrict__ block_to_expert,
-                                                        int32_t* __restrict__ conditions,
-                                                        MapWs ws, TileOut to) {
-  __shared__ int s_blk[kMapMaxE];
-  __shared__ int s_cnt[kMapMaxE];
-  __shared__ int s_tile[kMapMaxE];
-  __shared__ int s_wave[16];
+// Everything after the per-expert counts: block offsets (exclusive scan of
+// ceil(count/B)), expert_counts, block_to_expert, conditions and the optional tile
+// list. Thread tid < E holds run = count of expert tid. Leaves the inclusive
+// block scan in s_blk and the counts in s_cnt; 1024 threads.
+__device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __restrict__ expert_counts,
+                               int32_t* __restrict__ block_to_expert, int32_t* __restrict__ conditions,
+                               int32_t* __restrict__ block_off, const TileOut& to, int* s_blk, int* s_cnt,
+                               int* s_tile, int* s_wave) {
   const int tid = threadIdx.x;
-  int blk = 0, run = 0;
+  int blk = 0;
   if (tid < E) {
-    for (int c = 0; c < nchunks; ++c) {
-      int v = ws.chunk_counts[(size_t)c * E + tid];
-      ws.chunk_base[(size_t)c * E + tid] = run;
-      run += v;
-    }
     if (expert_counts != nullptr) expert_counts[tid] = run;
     blk = (run + B - 1) / B;
   }
   const int cum = block_inclusive_sum(blk, s_wave);
   if (tid < E) {
-    ws.block_off[tid] = cum - blk;  // exclusive
-    s_blk[tid] = cum;               // inclusive cumulative blocks
+    if (block_off != nullptr) block_off[tid] = cum - blk;  // exclusive
+    s_blk[tid] = cum;                                      // inclusive cumulative blocks
     s_cnt[tid] = run;
   }
   __syncthreads();
@@ -208,6 +202,75 @@ __global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int
     }
   }
   if (tid == 0) to.num_tiles[0] = min(ntiles + to.n_shared * per, to.max_tiles);
+}
+
+__global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int N, int nchunks,
+                                                        int32_t* __restrict__ expert_counts,
+                                                        int32_t* __restrict__ block_to_expert,
+                                                        int32_t* __restrict__ conditions,
+                                                        MapWs ws, TileOut to) {
+  __shared__ int s_blk[kMapMaxE];
+  __shared__ int s_cnt[kMapMaxE];
+  __shared__ int s_tile[kMapMaxE];
+  __shared__ int s_wave[16];
+  const int tid = threadIdx.x;
+  int run = 0;
+  if (tid < E) {
+    for (int c = 0; c < nchunks; ++c) {
+      int v = ws.chunk_counts[(size_t)c * E + tid];
+      ws.chunk_base[(size_t)c * E + tid] = run;
+      run += v;
+    }
+  }
+  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off, to,
+                 s_blk, s_cnt, s_tile, s_wave);
+}
+
+// The whole mapping in one workgroup, for ids and at most one 256-token chunk
+// (decode): fill, bitmask, counts, scan, tiles and scatter without the three
+// launches of the chunked path. Same outputs, same slot order.
+__global__ __launch_bounds__(1024) void map_small_kernel(
+    const int32_t* __restrict__ ids, int T, int K, int E, int B, int N,
+    int32_t* __restrict__ tpid, int32_t* __restrict__ block_to_expert,
+    int32_t* __restrict__ conditions, int32_t* __restrict__ expert_counts,
+    int32_t* __restrict__ inv_pos, MapWs ws, TileOut to) {
+  __shared__ uint32_t bm[kMapMaxE][8];
+  __shared__ int s_blk[kMapMaxE];
+  __shared__ int s_cnt[kMapMaxE];
+  __shared__ int s_tile[kMapMaxE];
+  __shared__ int s_wave[16];
+  const int tid = threadIdx.x;
+  const long nb_total = (long)N * B;
+  for (long i = tid; i < nb_total; i += blockDim.x) tpid[i] = -1;
+  if (tid == 0) ws.status[0] = 0;
+  __syncthreads();  // the fill and the status reset land before the scatter below
+  build_chunk_mask(bm, ids, nullptr, T, K, E, 0, ws.status);
+  int run = 0;
+  if (tid < E) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) run += __popc(bm[tid][w]);
+  }
+  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off, to,
+                 s_blk, s_cnt, s_tile, s_wave);
+  for (int i = tid; i < T * K; i += blockDim.x) {
+    const int t = i / K;
+    const int e = ids[i];
+    int out = -1;
+    if (e >= 0 && e < E) {
+      int rank = 0;
+      const int wq = t >> 5;
+      for (int w = 0; w < wq; ++w) rank += __popc(bm[e][w]);
+      rank += __popc(bm[e][wq] & ((1u << (t & 31)) - 1u));
+      const long slot = (long)(s_blk[e] - (s_cnt[e] + B - 1) / B) * B + rank;
+      if (slot < nb_total) {
+        tpid[slot] = t;
+        out = (int)slot;
+      } else {
+        atomicAdd(ws.status, 1);
+      }
+    }
+    if (inv_pos != nullptr) inv_pos[i] = out;
+  }
 }
 
 __global__ __launch_bounds__(256) void map_scatter_kernel(
@@ -391,6 +454,12 @@ int moe::blockwise_mapping(const int32_t* ids, const float* affinities,
   const int nch = (T + kChunk - 1) / kChunk;
   const long nbt = (long)N * B;
   int grid1 = std::max(nch, (int)std::min<long>(1024, (nbt + 255) / 256));
+  if (ids != nullptr && nch == 1) {
+    hipLaunchKernelGGL(map_small_kernel, dim3(1), dim3(1024), 0, st, ids, T, K, E, B, N,
+                       token_position_to_id, block_to_expert, conditions, expert_counts, inv_pos, ws,
+                       to);
+    MOE_API_END();
+  }
   hipLaunchKernelGGL(map_count_kernel, dim3(grid1), dim3(256), 0, st, ids, affinities,
                      padding_mask, affinities_masked, T, K, E, nch, nbt, token_position_to_id, ws);
   hipLaunchKernelGGL(map_scan_kernel, dim3(1), dim3(1024), 0, st, T, E, B, N, nch, expert_counts,

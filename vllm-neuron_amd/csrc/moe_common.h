@@ -108,3 +108,23 @@ __device__ __forceinline__ float group16_max_f32(float v) {
   for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, MOE_WAVE));
   return v;
 }
+
+// One 1x128 activation quantization group by one wave: lane l holds columns 2l,
+// 2l + 1 (`pair`, two bf16 bit patterns) and writes their codes to q + 2l; lane 0
+// writes the scale. s = max(amax, 1e-10) / 448 and q = RNE_e4m3fn(clamp(x / s,
+// +-448)), both IEEE fp32 divisions, so codes and scales match the oracle bit for bit.
+__device__ __forceinline__ void quant_pair_1x128(uint32_t pair, uint8_t* q, float* s, int lane) {
+  const float v0 = bf16_bits_to_f32((uint16_t)(pair & 0xffffu));
+  const float v1 = bf16_bits_to_f32((uint16_t)(pair >> 16));
+  const float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
+  const float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
+  const float y0 = fminf(fmaxf(v0 / sc, -448.0f), 448.0f);
+  const float y1 = fminf(fmaxf(v1 / sc, -448.0f), 448.0f);
+  *(uint16_t*)(q + 2 * lane) = (uint16_t)(f32_to_e4m3fn(y0) | (f32_to_e4m3fn(y1) << 8));
+  if (lane == 0) *s = sc;
+}
+
+// The same, loading the group from x (bf16, 128 columns).
+__device__ __forceinline__ void quant_group_1x128(const uint16_t* x, uint8_t* q, float* s, int lane) {
+  quant_pair_1x128(*(const uint32_t*)(x + 2 * lane), q, s, lane);
+}

@@ -4,9 +4,7 @@
 
 namespace moe {
 
-// One wave per (row, 128-column group): lane l holds columns 2l, 2l+1.
-// s = max(amax, 1e-10) / 448 and q = RNE_e4m3fn(clamp(x / s, +-448)), both IEEE
-// fp32 divisions, so codes and scales match the oracle bit for bit.
+// One wave per (row, 128-column group), quant_group_1x128.
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int rows,
                                                         int cols, uint8_t* __restrict__ q,
                                                         float* __restrict__ s) {
@@ -16,17 +14,8 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   for (long gi = (long)blockIdx.x * 4 + wave; gi < total; gi += (long)gridDim.x * 4) {
     const long r = gi / G;
     const int g = (int)(gi - r * G);
-    const size_t off = (size_t)r * cols + (size_t)g * MOE_GROUP + 2 * lane;
-    uint32_t pair = *(const uint32_t*)(x + off);
-    float v0 = bf16_bits_to_f32((uint16_t)(pair & 0xffffu));
-    float v1 = bf16_bits_to_f32((uint16_t)(pair >> 16));
-    float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
-    float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
-    float y0 = fminf(fmaxf(v0 / sc, -448.0f), 448.0f);
-    float y1 = fminf(fmaxf(v1 / sc, -448.0f), 448.0f);
-    uint32_t c = f32_to_e4m3fn(y0) | (f32_to_e4m3fn(y1) << 8);
-    *(uint16_t*)(q + off) = (uint16_t)c;
-    if (lane == 0) s[r * G + g] = sc;
+    const size_t off = (size_t)r * cols + (size_t)g * MOE_GROUP;
+    quant_group_1x128(x + off, q + off, s + r * G + g, lane);
   }
 }
 
