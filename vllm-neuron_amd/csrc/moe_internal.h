@@ -13,11 +13,11 @@ namespace moe {
 void set_error(const char* fn, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 
-// K splits for the router logits GEMM: aim for >= 512 workgroups, each split
-// at least 256 columns of H.
+// K splits for the router logits GEMM: aim for >= 1024 workgroups (4 per CU
+// fit, and the loop is latency-bound), each split at least 256 columns of H.
 inline int router_logits_splits(int T, int H, int E) {
   long base = (long)((T + 63) / 64) * ((E + 63) / 64);
-  long ks = (512 + base - 1) / base;
+  long ks = (1024 + base - 1) / base;
   long kmax = std::max(1, H / 256);
   return (int)std::max(1L, std::min(ks, kmax));
 }

@@ -4,18 +4,27 @@
 
 namespace moe {
 
-// One wave per (row, 128-column group), quant_group_1x128.
+// One wave per (row, 128-column group), quant_pair_1x128; each wave loads 8 of
+// its groups at a time (all in flight together) before quantizing them.
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x, int rows,
                                                         int cols, uint8_t* __restrict__ q,
                                                         float* __restrict__ s) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = cols / MOE_GROUP;
   const long total = (long)rows * G;
-  for (long gi = (long)blockIdx.x * 4 + wave; gi < total; gi += (long)gridDim.x * 4) {
-    const long r = gi / G;
-    const int g = (int)(gi - r * G);
-    const size_t off = (size_t)r * cols + (size_t)g * MOE_GROUP;
-    quant_group_1x128(x + off, q + off, s + r * G + g, lane);
+  const long nwaves = (long)gridDim.x * 4;
+  for (long g0 = (long)blockIdx.x * 4 + wave; g0 < total; g0 += 8 * nwaves) {
+    uint32_t pr[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const long gi = g0 + u * nwaves;
+      pr[u] = (gi < total) ? *(const uint32_t*)(x + gi * MOE_GROUP + 2 * lane) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const long gi = g0 + u * nwaves;  // group gi = row * G + column group: offset gi * 128
+      if (gi < total) quant_pair_1x128(pr[u], q + gi * MOE_GROUP, s + gi, lane);
+    }
   }
 }
 
@@ -102,7 +111,7 @@ extern "C" int moe_act_quant_1x128(const void* x_bf16, int rows, int cols, uint8
   MOE_CHECK_ARG(((uintptr_t)x_bf16 & 3) == 0 && ((uintptr_t)q & 1) == 0, "misaligned x or q");
   if (rows == 0) return MOE_OK;
   long groups = (long)rows * (cols / MOE_GROUP);
-  int grid = (int)std::min<long>((groups + 3) / 4, 8192);
+  int grid = (int)std::min<long>((groups + 3) / 4, 2048);
   hipLaunchKernelGGL(act_quant_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)x_bf16, rows, cols, q, scales);
   MOE_API_END();

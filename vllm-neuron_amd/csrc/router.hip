@@ -13,9 +13,10 @@ namespace moe {
 // logits[t, e] = sum_h x[t, h] * w[e, h]   (bf16 operands, fp32 accumulation)
 //
 // Workgroup tile: 64 tokens x 64 experts, 4 waves; wave w owns experts
-// [16w, 16w + 16) for all 64 tokens (4 MFMA row tiles). K advances 64 per step
-// (two v_mfma_f32_16x16x32_bf16). The x tile goes through LDS (shared by the
-// four waves); each wave streams its 16 router rows straight into registers.
+// [16w, 16w + 16) for all 64 tokens (4 MFMA row tiles). K advances 256 per
+// iteration (four steps of two v_mfma_f32_16x16x32_bf16), in ascending K for
+// every accumulator. The x tile goes through LDS (shared by the four waves);
+// each wave streams its 16 router rows straight into registers.
 // Operand lane layout: lane l holds row l%16 and the 8 K-values
 // [s*32 + (l/16)*8, +8) of sub-step s; A and B use the same mapping, so the
 // MFMA forms the full 32-long dot product per sub-step.
@@ -26,8 +27,10 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const float* __restrict__ bias, int T, int H, int E, int kchunk,
     float* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) uint16_t sx[64][64 + 8];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // x tile: 64 rows x 256 columns (four 64-column K steps), rows padded by 8.
+  constexpr int KW = 256, LDX = KW + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t sx[64][LDX];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
   const int k_begin = blockIdx.z * kchunk;
   const int k_end = min(H, k_begin + kchunk);
@@ -42,11 +45,46 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 #pragma unroll
   for (int m = 0; m < 4; ++m) acc[m] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  // x tile load: 64 rows x 64 bf16 = 512 chunks of 16 B, 2 per thread.
-  for (int k0 = k_begin; k0 < k_end; k0 += 64) {
+  // Main loop: 256 columns per iteration. All of an iteration's global loads
+  // (8 x-tile chunks and 8 router fragments per thread) are issued together,
+  // so each iteration waits for one memory latency instead of four.
+  int k0 = k_begin;
+  for (; k0 + KW <= k_end; k0 += KW) {
+    int4 xv[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int idx = tid + c * 256, row = idx >> 5, col = (idx & 31) * 8;
+      const int tr = min(t0 + row, T - 1);  // rows past T load row T-1 and are zeroed
+      xv[c] = *(const int4*)(x + (size_t)tr * H + k0 + col);
+      if (t0 + row >= T) xv[c] = make_int4(0, 0, 0, 0);
+    }
+    v8bf b[4][2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) b[q][s] = *(const v8bf*)(wrow + k0 + q * 64 + s * 32 + g * 8);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int idx = tid + c * 256, row = idx >> 5, col = (idx & 31) * 8;
+      *(int4*)&sx[row][col] = xv[c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          v8bf a = *(const v8bf*)&sx[m * 16 + r16][q * 64 + s * 32 + g * 8];
+          acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[q][s], acc[m], 0, 0, 0);
+        }
+    __syncthreads();
+  }
+  // Remaining columns, 64 at a time (H is a multiple of 64).
+  for (; k0 < k_end; k0 += 64) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      int idx = threadIdx.x + c * 256;
+      int idx = tid + c * 256;
       int row = idx >> 3, col = (idx & 7) * 8;
       int4 v = {0, 0, 0, 0};
       if (t0 + row < T) v = *(const int4*)(x + (size_t)(t0 + row) * H + k0 + col);
