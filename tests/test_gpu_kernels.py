@@ -115,6 +115,29 @@ def test_router_topk_bit_exact(cuda, case, T):
     assert np.array_equal(aff.cpu().numpy(), R.scatter_dense(oi, ow, E))
 
 
+@pytest.mark.parametrize("gs", [32, 8])
+def test_router_grouped_nonfinite_group_scores(cuda, gs):
+    """Correction biases of +-inf give group scores of +inf, -inf and NaN (+inf + -inf):
+    a NaN group ranks below a -inf group, which ranks below every finite group."""
+    E, K, ng = 8 * gs, 8, 8
+    say("router_topk_nonfinite", gs)
+    rng = np.random.default_rng(gs)
+    lg = rng.normal(0, 1.5, (64, E)).astype(np.float32)
+    bias = rng.normal(0, 0.01, E).astype(np.float32)
+    bias[0] = np.inf                  # group 0: +inf and the rest -inf -> NaN
+    bias[1:gs] = -np.inf
+    bias[gs:2 * gs] = -np.inf         # group 1: all -inf -> -inf
+    bias[2 * gs + 3] = np.inf         # group 2: one +inf among finite -> +inf
+    for tg in (2, 6, 7):
+        ids, w = ops.router_topk(torch.from_numpy(lg).to(cuda), K, 2, 1, ng, tg,
+                                 torch.from_numpy(bias).to(cuda), True, 1e-20, 2.5)
+        with np.errstate(invalid="ignore"):
+            oi, ow = R.route_grouped(lg, bias, K, ng, tg, R.SIGMOID, True, 1e-20, 2.5)
+        assert not (oi == 0).any()    # the NaN group is never kept while finite or -inf groups are left
+        assert np.array_equal(ids.cpu().numpy(), oi), tg
+        assert np.array_equal(w.cpu().numpy(), ow), tg
+
+
 MAP_CASES = [(1, 8, 256, 256), (7, 2, 8, 4), (64, 2, 8, 256), (64, 8, 256, 256), (300, 8, 160, 16),
              (4096, 8, 160, 256), (8192, 8, 256, 256), (1000, 6, 384, 64), (513, 1, 5, 1)]
 

@@ -158,17 +158,50 @@ __device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
   return v > v2 || (v == v2 && i < i2);
 }
 
-__device__ __forceinline__ KeyIdx wave_argmax(float v, int i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    float v2 = __shfl_xor(v, o, 64);
-    int i2 = __shfl_xor(i, o, 64);
-    if (better(v2, i2, v, i)) {
-      v = v2;
-      i = i2;
-    }
+// DPP lane moves (gfx9 encodings): quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror, row_bcast:15, row_bcast:31. Lanes a move does
+// not write keep `old`, their own value.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(v)));
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void argmax_step(float& v, int& i) {
+  const float v2 = dpp_f<CTRL, ROW_MASK>(v);
+  const int i2 = dpp_i<CTRL, ROW_MASK>(i);
+  if (better(v2, i2, v, i)) {
+    v = v2;
+    i = i2;
   }
-  return {v, i};
+}
+
+// Wave argmax under better() (larger value, then lower index). Candidates are
+// never NaN (a NaN key is never taken as a lane's candidate), so better() is a
+// total order and the result does not depend on the reduction tree: rows of 16
+// lanes by quad swaps and mirrors, then the rows into lane 63, read as scalars.
+__device__ __forceinline__ KeyIdx wave_argmax(float v, int i) {
+  argmax_step<0xB1, 0xF>(v, i);
+  argmax_step<0x4E, 0xF>(v, i);
+  argmax_step<0x141, 0xF>(v, i);
+  argmax_step<0x140, 0xF>(v, i);
+  argmax_step<0x142, 0xA>(v, i);
+  argmax_step<0x143, 0xC>(v, i);
+  return {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)),
+          __builtin_amdgcn_readlane(i, 63)};
+}
+
+// Top-2 values of (t1, t2) pairs under fmaxf/fminf (inputs never NaN).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void top2_step(float& t1, float& t2) {
+  const float b1 = dpp_f<CTRL, ROW_MASK>(t1), b2 = dpp_f<CTRL, ROW_MASK>(t2);
+  const float lo = fminf(t1, b1);
+  t1 = fmaxf(t1, b1);
+  t2 = fmaxf(lo, fmaxf(t2, b2));
 }
 
 __global__ __launch_bounds__(256) void router_topk_kernel(
@@ -251,7 +284,32 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     const int gs = E / n_group;
     float gscore = NEG_INF;
     int gidx = 0x7fffffff;
-    if (lane < n_group) {
+    if (gs == 32 && P * 64 == E) {
+      // Groups of 32: group 2j + lane / 32 is register j of one 32-lane half,
+      // so its top 2 is a DPP reduction within the half (lane 31 / 63 gets it).
+      // NaN keys count as -inf, as in the sequential scan, which skips them.
+#pragma unroll
+      for (int j = 0; j < kTopkMaxP; ++j) {
+        if (j < P) {
+          float t1 = (key[j] == key[j]) ? key[j] : NEG_INF, t2 = NEG_INF;
+          top2_step<0xB1, 0xF>(t1, t2);
+          top2_step<0x4E, 0xF>(t1, t2);
+          top2_step<0x141, 0xF>(t1, t2);
+          top2_step<0x140, 0xF>(t1, t2);
+          top2_step<0x142, 0xA>(t1, t2);
+          const float g_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1 + t2), 31));
+          const float g_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1 + t2), 63));
+          if (lane == 2 * j) {
+            gscore = g_lo;
+            gidx = lane;
+          }
+          if (lane == 2 * j + 1) {
+            gscore = g_hi;
+            gidx = lane;
+          }
+        }
+      }
+    } else if (lane < n_group) {
       float t1 = NEG_INF, t2 = NEG_INF;
       for (int q = 0; q < gs; ++q) {
         float v = s_key[wave][lane * gs + q];
@@ -265,11 +323,17 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       gscore = (gs == 1) ? t1 : t1 + t2;
       gidx = lane;
     }
+    // A NaN group score (+inf + -inf) ranks below every number, -inf included,
+    // lower group first: it competes as -inf with its index moved past 63.
+    if (gidx < n_group && gscore != gscore) {
+      gscore = NEG_INF;
+      gidx += 64;
+    }
     uint64_t keep = 0;
     for (int q = 0; q < topk_group; ++q) {
       KeyIdx b = wave_argmax(gscore, gidx);
-      if (b.i < n_group) keep |= 1ull << b.i;
-      if (lane == b.i) {
+      if (b.i < 128) keep |= 1ull << (b.i & 63);
+      if (lane == (b.i & 63)) {
         gscore = NEG_INF;
         gidx = 0x7fffffff;
       }
