@@ -95,8 +95,10 @@ template <int KIND>
 __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs p) {
   // Pipeline stages as distinct objects, so the compiler can tell that fragment
   // reads of one stage do not alias the direct-to-LDS loads in flight into another.
-  __shared__ __attribute__((aligned(16))) uint8_t sT0[kStage];  // A tile, then B tile
-  __shared__ __attribute__((aligned(16))) uint8_t sT1[kStage];
+  __shared__ __attribute__((aligned(16))) uint8_t sTA0[kStageA];  // A tile of stage 0
+  __shared__ __attribute__((aligned(16))) uint8_t sTB0[kStageB];  // B tile of stage 0
+  __shared__ __attribute__((aligned(16))) uint8_t sTA1[kStageA];
+  __shared__ __attribute__((aligned(16))) uint8_t sTB1[kStageB];
   __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageSA];  // A scales of sT0's block
   __shared__ __attribute__((aligned(16))) uint8_t sA1[kStageSA];
   __shared__ __attribute__((aligned(16))) float sR0[2 * kBM];  // scale ratio per (half, row)
@@ -215,8 +217,7 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   bool a_live[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) a_live[i] = 8 * (4 * wave + i) < nrows;  // wave-uniform
-  auto issue = [&](uint8_t* sa, uint8_t* ss, int kb) {
-    uint8_t* sb = sa + kStageA;
+  auto issue = [&](uint8_t* sa, uint8_t* sb, uint8_t* ss, int kb) {
     load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, ss + sa_dst);
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
@@ -237,39 +238,66 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
 
   const bool active = 64 * wm < nrows;  // this wave's 64 rows hold at least one row
   const int g = lane >> 4, l16 = lane & 15;
+  // Fragment reads. Every fragment starts at a 16-aligned row, so row l16 of it
+  // has swizzle (l16 >> 1) & 7 whatever the tile: a fragment is one per-lane
+  // offset (f_lo / f_hi) plus a constant, and the reads use immediate offsets.
+  const uint32_t f_lo = l16 * kBK + ((g ^ ((l16 >> 1) & 7)) << 4);
+  const uint32_t f_hi = l16 * kBK + (((g + 4) ^ ((l16 >> 1) & 7)) << 4);
+  const uint32_t a_wave = 64 * wm * kBK;
   // B rows of this wave's eight 16-column tiles. gate_up: tiles 0-3 gate columns
   // [64 wn, +64), tiles 4-7 the matching up columns; down: columns [128 wn, +128).
-  int brow[8];
-#pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    if (KIND == 0)
-      brow[n] = (n < 4) ? 64 * wn + 16 * n + l16 : 128 + 64 * wn + 16 * (n - 4) + l16;
-    else
-      brow[n] = 128 * wn + 16 * n + l16;
-  }
+  const uint32_t b_wave = (KIND == 0 ? 64 * wn : 128 * wn) * kBK;
+  auto frag = [&](const uint8_t* t) -> v8i {
+    const int4 lo = *(const int4*)(t + f_lo);
+    const int4 hi = *(const int4*)(t + f_hi);
+    return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  };
+  auto brow0 = [](int n) { return (KIND == 0) ? ((n < 4) ? 16 * n : 128 + 16 * (n - 4)) : 16 * n; };
 
-  auto compute = [&](const uint8_t* sa, const float* sr) {
-    const uint8_t* sb = sa + kStageA;
+  auto compute = [&](const uint8_t* sa, const uint8_t* sb, const float* sr) {
+    const uint8_t* ta = sa + a_wave;
+    const uint8_t* tb = sb + b_wave;
     v8i a[4];
-    v4f rr[4][2];  // [row tile][column half]
+    v4f rr[4];  // ratios of the column half in use: gate, then up (gate_up)
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      a[m] = lds_frag16(sa, 64 * wm + 16 * m + l16, g);
-      const int r4 = 64 * wm + 16 * m + 4 * g;
-      rr[m][0] = *(const v4f*)&sr[((KIND == 0) ? 0 : wn) * kBM + r4];
-      rr[m][1] = (KIND == 0) ? *(const v4f*)&sr[kBM + r4] : rr[m][0];
+      a[m] = frag(ta + 16 * m * kBK);
+      rr[m] = *(const v4f*)&sr[((KIND == 0) ? 0 : wn) * kBM + 64 * wm + 16 * m + 4 * g];
     }
+    // B fragments double-buffered: the reads of column tile n + 1 are issued
+    // before the MFMAs of tile n, so LDS latency hides under them.
+    v8i b = frag(tb + brow0(0) * kBK);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      const v8i b = lds_frag16(sb, brow[n], g);
-      const int hf = (KIND == 0) ? (n >> 2) : 0;
+      v8i bn = b;
+      if (n + 1 < 8) bn = frag(tb + brow0(n + 1) * kBK);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc[m][n] = mfma16_fp8_acc(a[m], b, acc[m][n] * rr[m][hf]);
+      for (int m = 0; m < 4; ++m) {
+        const v4f c = acc[m][n] * rr[m];
+        if (KIND == 0 && n == 3) rr[m] = *(const v4f*)&sr[kBM + 64 * wm + 16 * m + 4 * g];
+        acc[m][n] = mfma16_fp8_acc(a[m], b, c);
+      }
+      b = bn;
+    }
+    // Instruction order for the scheduler (it would otherwise sink each B read
+    // next to its first use): the A, ratio and first B reads; then per column
+    // tile the next tile's B reads and four (4 ratio multiplies, 1 MFMA) pairs;
+    // gate_up reads the up-half ratios once the gate-half ones are used.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8 + 4 + 2, 0);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      if (n + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+        if (KIND == 0 && n == 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
     }
   };
 
   // Prologue: block 0 and its scales.
-  issue(sT0, sA0, 0);
+  issue(sTA0, sTB0, sA0, 0);
   wait_vm<0>();
   __syncthreads();  // sW and block 0's stage
   (shalf ? sR0 + kBM : sR0)[srow] = ratio(stage_sa(sA0), sW[shalf][0]);  // 0: the accumulators start at 0
@@ -277,13 +305,14 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
 
   // One step: loads of block kb + 1 (scales first) into the other stage, the
   // MFMAs of block kb, then the ratios of block kb + 1 once its loads landed.
-  auto step = [&](int kb, const uint8_t* ca, const float* cr, uint8_t* na, uint8_t* nsa, float* nr) {
+  auto step = [&](int kb, const uint8_t* ca, const uint8_t* cb, const float* cr, uint8_t* na,
+                  uint8_t* nb, uint8_t* nsa, float* nr) {
     // Every step issues the same loads (past the last block it re-reads block
     // KB - 1 into the stage that is not read again), so the waits stay exact.
     const int kn = min(kb + 1, KB - 1);
-    issue(na, nsa, kn);
+    issue(na, nb, nsa, kn);
     __builtin_amdgcn_sched_barrier(0);
-    if (active) compute(ca, cr);
+    if (active) compute(ca, cb, cr);
     __builtin_amdgcn_sched_barrier(0);
     // Past the last block the ratio of the re-read block is 1 and lands in a
     // stage that is not read again.
@@ -295,13 +324,24 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     __builtin_amdgcn_sched_barrier(0);
   };
   for (int kb = 0; kb < KB; kb += 2) {
-    step(kb, sT0, sR0, sT1, sA1, sR1);
-    if (kb + 1 < KB) step(kb + 1, sT1, sR1, sT0, sA0, sR0);
+    step(kb, sTA0, sTB0, sR0, sTA1, sTB1, sA1, sR1);
+    if (kb + 1 < KB) step(kb + 1, sTA1, sTB1, sR1, sTA0, sTB0, sA0, sR0);
   }
   (shalf ? sLast + kBM : sLast)[srow] = s_prev;
   __syncthreads();
 
   // Accumulator layout (16x16): lane l, register i holds D[4*(l/16) + i][l%16].
+  // Each wave stages its output block in LDS (16 KB: stage array wave / 2, half
+  // wave % 2; the stages are free once every wave passed the barrier above) and
+  // writes it back in 16-byte row chunks: scattered 1- and 2-byte stores of the
+  // accumulator layout cost more than the whole K loop.
+  uint8_t* const stg = ((wave >> 1) == 0 ? sTA0 : (wave >> 1) == 1 ? sTB0 : (wave >> 1) == 2 ? sTA1 : sTB1) +
+                       (wave & 1) * 16384;
+  auto wave_lds_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
   if (KIND == 0) {
     // h = SiLU(gate) * up for this wave's 64 h columns; the row amax of the 1x128
     // group combines the two column-half waves through LDS.
@@ -326,37 +366,48 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
       }
     __syncthreads();
     if (active) {
+      // codes of local row r (0..63), h column c (0..63) at stg[r * 64 + c]
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int row = 64 * wm + 16 * m + 4 * g + i;
-          if (row < nrows && sSrc[row] >= 0) {
-            const long slot = slot0 + row;
-            const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
+          const int lr = 16 * m + 4 * g + i, row = 64 * wm + lr;
+          const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
 #pragma unroll
-            for (int n = 0; n < 4; ++n) {
-              const float yv = fminf(fmaxf(acc[m][n][i] / sc, -448.0f), 448.0f);
-              p.hq[(size_t)slot * p.I + nt * 128 + 64 * wn + 16 * n + l16] = (uint8_t)f32_to_e4m3fn(yv);
-            }
-            if (wn == 0 && l16 == 0) p.hs[(size_t)slot * GI + nt] = sc;
+          for (int n = 0; n < 4; ++n) {
+            const float yv = fminf(fmaxf(acc[m][n][i] / sc, -448.0f), 448.0f);
+            stg[lr * 64 + 16 * n + l16] = (uint8_t)f32_to_e4m3fn(yv);
           }
+          if (wn == 0 && l16 == 0 && row < nrows && sSrc[row] >= 0)
+            p.hs[(size_t)(slot0 + row) * GI + nt] = sc;
         }
+      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = lane + 64 * j, lr = c >> 2, ch = c & 3, row = 64 * wm + lr;
+        if (row < nrows && sSrc[row] >= 0)
+          *(int4*)(p.hq + (size_t)(slot0 + row) * p.I + nt * 128 + 64 * wn + 16 * ch) = *(const int4*)(stg + lr * 64 + 16 * ch);
+      }
     }
   } else if (active) {
+    // bf16 of local row r (0..63), column c (0..127) at stg[(r * 128 + c) * 2]
+    uint16_t* const stg16 = (uint16_t*)stg;
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = 64 * wm + 16 * m + 4 * g + i;
-        if (row < nrows) {
-          const long slot = slot0 + row;
-          const float sl = sLast[wn * kBM + row];
+        const int lr = 16 * m + 4 * g + i;
+        const float sl = sLast[wn * kBM + 64 * wm + lr];
 #pragma unroll
-          for (int n = 0; n < 8; ++n)
-            p.y[(size_t)slot * p.H + nt * kBN + 128 * wn + 16 * n + l16] = f32_to_bf16_bits(acc[m][n][i] * sl);
-        }
+        for (int n = 0; n < 8; ++n) stg16[lr * 128 + 16 * n + l16] = f32_to_bf16_bits(acc[m][n][i] * sl);
       }
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int c = lane + 64 * j, lr = c >> 4, ch = c & 15, row = 64 * wm + lr;
+      if (row < nrows)
+        *(int4*)(p.y + (size_t)(slot0 + row) * p.H + nt * kBN + 128 * wn + 8 * ch) = *(const int4*)(stg + lr * 256 + 16 * ch);
+    }
   }
 }
 
@@ -508,7 +559,8 @@ extern "C" int moe_expert_gate_up_block(const uint8_t* xq, const float* xs, int 
   int rc = block_gemm_common_checks(_moe_fn, T, H, I, E, NB, max_tiles);
   if (rc != MOE_OK) return rc;
   MOE_CHECK_ARG(n_shared == 0 || (w13_shared && w13_shared_scale), "shared weights missing");
-  MOE_CHECK_ARG(((uintptr_t)xq & 15) == 0 && ((uintptr_t)w13 & 15) == 0, "misaligned operands");
+  MOE_CHECK_ARG(((uintptr_t)xq & 15) == 0 && ((uintptr_t)w13 & 15) == 0 && ((uintptr_t)hq & 15) == 0,
+                "xq, w13 and hq must be 16-byte aligned");
   BlkArgs a{};
   a.a = xq;
   a.as = xs;
@@ -543,7 +595,8 @@ extern "C" int moe_expert_down_block(const uint8_t* hq, const float* hs, int T, 
   int rc = block_gemm_common_checks(_moe_fn, T, H, I, E, NB, max_tiles);
   if (rc != MOE_OK) return rc;
   MOE_CHECK_ARG(n_shared == 0 || (w2_shared && w2_shared_scale), "shared weights missing");
-  MOE_CHECK_ARG(((uintptr_t)hq & 15) == 0 && ((uintptr_t)w2 & 15) == 0, "misaligned operands");
+  MOE_CHECK_ARG(((uintptr_t)hq & 15) == 0 && ((uintptr_t)w2 & 15) == 0 && ((uintptr_t)y_bf16 & 15) == 0,
+                "hq, w2 and y must be 16-byte aligned");
   BlkArgs a{};
   a.a = hq;
   a.as = hs;
