@@ -81,6 +81,18 @@ int moe_router_logits_f32(const float* x, const void* router_w, int w_is_f32, co
 int moe_rms_norm(const void* x, int x_is_f32, const float* gamma, int T, int H, int hidden_actual,
                  float eps, void* out, int out_is_f32, void* stream);
 
+/* Decode prologue, fused: v = x (or bf16(x + residual) when residual is given,
+ * written to residual_out as the next residual stream), xn = RMSNorm(v) exactly
+ * as moe_rms_norm with bf16 output, and q/s = the 1x128 e4m3fn quantization of
+ * xn exactly as moe_act_quant_1x128. All bf16 [T,H]; q [T,H]; s fp32 [T,H/128].
+ * H % 128 == 0. Replaces the RMSNorm step of moe_block_tkg (moe_block_tkg.py:
+ * 135-151) with its fused residual add (moe_block_tkg.py:341,421-428; the
+ * pre-norm sum model_mxfp4.py:1589-1609) and the norm + quantize prologue of
+ * rmsnorm_router_topk_tkg.py:247-343. */
+int moe_rms_norm_quant(const void* x_bf16, const void* residual_bf16, const float* gamma, int T,
+                       int H, int hidden_actual, float eps, void* xn_bf16, void* residual_out_bf16,
+                       uint8_t* q, float* s, void* stream);
+
 /* Top-k selection + activation (+ renorm, * routed_scale) from fp32 logits.
  * ids/weights [T,K] in descending key order (ties -> lower expert index);
  * affinities [T,E] (optional, NULL to skip) is the dense scatter the reference

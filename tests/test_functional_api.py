@@ -93,8 +93,8 @@ def test_moe_block_tkg_unsupported_options():
     wr = torch.zeros(256, 2, dtype=torch.bfloat16)
     with pytest.raises(NotImplementedError, match="placeholders"):
         M.moe_block_tkg(x, g, wr, gu, dn, hidden_act_scale_factor=1.0)
-    with pytest.raises(NotImplementedError):
-        M.moe_block_tkg(x, g, wr, gu, dn, residual=x)
+    with pytest.raises(NotImplementedError):   # fused residual add on float32 input
+        M.moe_block_tkg(x.float(), g, wr, gu, dn, residual=x.float())
     with pytest.raises(NotImplementedError):
         M.moe_block_tkg(x, g, wr, gu, dn, hidden_act_fn=M.ActFnType.Swish)
     with pytest.raises(NotImplementedError):   # 2 local experts of 4 routed

@@ -71,6 +71,44 @@ def test_rms_norm_kernel(cuda, x_dtype, out_dtype, ha):
         assert np.all(got[:, ha:] == 0)
 
 
+@pytest.mark.parametrize("T, H, ha, with_res", [(1, 7168, None, False), (64, 7168, None, True),
+                                                (37, 1024, 1000, True), (300, 1024, None, False)])
+def test_rms_norm_quant_fused(cuda, T, H, ha, with_res):
+    """The fused prologue equals residual add -> rms_norm -> act_quant bit for bit; the
+    sum is the bf16 rounding of the fp32 sum, the codes the oracle's 1x128 quantization
+    of the normalized rows, and those rows within one bf16 rounding of the fp32 norm."""
+    from oracle.fp8 import quant_act_1x128
+    say("rms_norm_quant", T, H, ha, with_res)
+    g = torch.Generator().manual_seed(T + H)
+    x = (torch.randn(T, H, generator=g) * 3).to(torch.bfloat16).to(cuda)
+    r = torch.randn(T, H, generator=g).to(torch.bfloat16).to(cuda) if with_res else None
+    gamma = (1 + 0.1 * torch.randn(H, generator=g)).to(cuda)
+    xn, q, s, v = ops.rms_norm_quant(x, gamma, 1e-6, ha, r)
+    v_ref = x + r if with_res else x
+    if with_res:
+        assert torch.equal(v, v_ref)
+        assert np.array_equal(np_f32(v), bf16_round(np_f32(x) + np_f32(r)))
+    else:
+        assert v is None
+    xn_ref = ops.rms_norm(v_ref, gamma, 1e-6, ha)
+    q_ref, s_ref = ops.act_quant(xn_ref)
+    assert torch.equal(xn, xn_ref)
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8)) and torch.equal(s, s_ref)
+    ref = R.rms_norm_padded(np_f32(v_ref), np_f32(gamma), 1e-6, ha)
+    assert np.allclose(np_f32(xn), bf16_round(ref), rtol=2 ** -7, atol=0)
+    oq, os_ = quant_act_1x128(np_f32(xn))
+    assert np.array_equal(np_u8(q), oq) and np.array_equal(np_f32(s), os_)
+
+
+def test_rms_norm_quant_rejects_bad_arguments(cuda):
+    x = torch.zeros(4, 1000, dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(ValueError):                         # H not a multiple of 128
+        ops.rms_norm_quant(x, torch.ones(1000, device=cuda), 1e-6)
+    x = torch.zeros(4, 1024, dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(ValueError):                         # hidden_actual beyond H
+        ops.rms_norm_quant(x, torch.ones(1024, device=cuda), 1e-6, hidden_actual=2000)
+
+
 @pytest.mark.parametrize("T, H, E, w_dtype", [(100, 512, 40, torch.float32),
                                              (3000, 512, 40, torch.bfloat16),
                                              (7, 128, 96, torch.float32), (1, 1024, 8, torch.bfloat16)])
@@ -258,3 +296,27 @@ def test_moe_block_tkg_api(cuda, act, pre_norm, norm_topk, post, ha):
     err = rel_l2(np_f32(out), ref_sel)
     say("moe_block_tkg rel_l2", err)
     assert err <= TOL_REL_L2
+
+
+def test_moe_block_tkg_fused_residual(cuda):
+    """residual: the block normalizes inp + residual and returns that sum last; the
+    output and logits equal those of the block run on the sum (same kernels)."""
+    say("moe_block_tkg residual")
+    cfg, w = _small(cuda, 4)
+    K, H = cfg.top_k, cfg.hidden
+    g = torch.Generator().manual_seed(11)
+    x = synthetic.hidden_states(24, H, 4).to(cuda).reshape(2, 12, H)
+    res = torch.randn(2, 12, H, generator=g).to(torch.bfloat16).to(cuda)
+    gamma = (1 + 0.1 * torch.randn(1, H, generator=g)).to(cuda)
+    gu, gs, dn, ds = _nf(w)
+    kw = dict(top_k=K, expert_gate_up_weights_scale=gs, expert_down_weights_scale=ds,
+              router_act_fn=M.RouterActFnType.SIGMOID, norm_topk_prob=True,
+              expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.POST_SCALE)
+    out, lg, ro = M.moe_block_tkg(x, gamma, w.router_w.t(), gu, dn, residual=res, **kw)
+    s = x + res
+    out2, lg2 = M.moe_block_tkg(s, gamma, w.router_w.t(), gu, dn, **kw)
+    assert torch.equal(ro, s) and ro.shape == x.shape
+    assert torch.equal(out, out2) and torch.equal(lg, lg2)
+    only = M.moe_block_tkg(x, gamma, w.router_w.t(), gu, dn, residual=res, skip_router_logits=True,
+                           **kw)
+    assert len(only) == 2 and torch.equal(only[0], out) and torch.equal(only[1], s)

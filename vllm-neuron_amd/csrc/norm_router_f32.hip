@@ -50,6 +50,49 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ 
   }
 }
 
+// Decode prologue in one pass per row: optional residual add (the pre-norm sum
+// v = bf16(x + residual) is written out as the next residual stream), RMSNorm of
+// v exactly as rms_norm_kernel computes it (same fixed-order sum), the bf16
+// normalized row, and its 1x128 e4m3fn quantization as act_quant_kernel computes
+// it. The outputs are bit-identical to moe_rms_norm followed by
+// moe_act_quant_1x128 (after a bf16 residual add), without the round trip of the
+// normalized row through HBM.
+__global__ __launch_bounds__(256) void rms_norm_quant_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res, const float* __restrict__ gamma,
+    int H, int ha, float eps, uint16_t* __restrict__ xn, uint16_t* __restrict__ res_out,
+    uint8_t* __restrict__ q, float* __restrict__ qs) {
+  __shared__ float s_part[4];
+  const size_t row = (size_t)blockIdx.x * H;
+  auto val = [&](int c) -> float {
+    float v = bf16_bits_to_f32(x[row + c]);
+    if (res != nullptr) v = bf16_bits_to_f32(f32_to_bf16_bits(v + bf16_bits_to_f32(res[row + c])));
+    return v;
+  };
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < ha; c += 256) {
+    const float v = val(c);
+    ss += v * v;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
+  const float r = 1.0f / sqrtf(tot / (float)ha + eps);
+  const int lane = threadIdx.x & 63, G = H / 128;
+  for (int gi = threadIdx.x >> 6; gi < G; gi += 4) {
+    const int c0 = gi * 128 + 2 * lane;
+    const float v0 = val(c0), v1 = val(c0 + 1);
+    const float y0 = (c0 < ha) ? (v0 * r) * gamma[c0] : 0.f;
+    const float y1 = (c0 + 1 < ha) ? (v1 * r) * gamma[c0 + 1] : 0.f;
+    const uint32_t pair = (uint32_t)f32_to_bf16_bits(y0) | ((uint32_t)f32_to_bf16_bits(y1) << 16);
+    *(uint32_t*)(xn + row + c0) = pair;
+    if (res_out != nullptr)
+      *(uint32_t*)(res_out + row + c0) = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
+    quant_pair_1x128(pair, q + row + gi * 128, qs + (size_t)blockIdx.x * G + gi, lane);
+  }
+}
+
 // logits[t, e] = sum_h x[t, h] * w[e, h]   (fp32 x; fp32 or bf16 w; fp32 accumulate)
 //
 // Workgroup tile: 64 tokens x 64 experts, 4 waves; wave w owns experts
@@ -170,6 +213,27 @@ extern "C" int moe_rms_norm(const void* x, int x_is_f32, const float* gamma, int
   if (T == 0) return MOE_OK;
   hipLaunchKernelGGL(rms_norm_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, x,
                      x_is_f32 ? 1 : 0, gamma, H, hidden_actual, eps, out, out_is_f32 ? 1 : 0);
+  MOE_API_END();
+}
+
+extern "C" int moe_rms_norm_quant(const void* x_bf16, const void* residual_bf16, const float* gamma,
+                                  int T, int H, int hidden_actual, float eps, void* xn_bf16,
+                                  void* residual_out_bf16, uint8_t* q, float* s, void* stream) {
+  MOE_API_BEGIN("moe_rms_norm_quant");
+  MOE_CHECK_ARG(x_bf16 && gamma && xn_bf16 && q && s, "null pointer argument");
+  MOE_CHECK_ARG((residual_bf16 == nullptr) == (residual_out_bf16 == nullptr),
+                "residual and residual_out must be given together");
+  MOE_CHECK_ARG(T >= 0 && H > 0 && H % 128 == 0, "H must be a positive multiple of 128 (T=%d H=%d)", T, H);
+  MOE_CHECK_ARG(hidden_actual >= 1 && hidden_actual <= H,
+                "hidden_actual must be in [1, H=%d], got %d", H, hidden_actual);
+  MOE_CHECK_ARG(eps >= 0.f, "eps must be >= 0");
+  MOE_CHECK_ARG(((uintptr_t)x_bf16 & 3) == 0 && ((uintptr_t)xn_bf16 & 3) == 0 && ((uintptr_t)q & 1) == 0 &&
+                    ((uintptr_t)residual_bf16 & 3) == 0 && ((uintptr_t)residual_out_bf16 & 3) == 0,
+                "x, residual, xn and residual_out must be 4-byte aligned, q 2-byte aligned");
+  if (T == 0) return MOE_OK;
+  hipLaunchKernelGGL(rms_norm_quant_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, (const uint16_t*)residual_bf16, gamma, H, hidden_actual,
+                     eps, (uint16_t*)xn_bf16, (uint16_t*)residual_out_bf16, q, s);
   MOE_API_END();
 }
 

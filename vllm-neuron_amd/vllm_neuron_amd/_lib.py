@@ -28,6 +28,7 @@ PROTOTYPES = {
     "moe_router_logits": (_i, [_p, _p, _p, _i, _i, _i, _p, _p, _sz, _p]),
     "moe_router_logits_f32": (_i, [_p, _p, _i, _p, _i, _i, _i, _p, _p, _sz, _p]),
     "moe_rms_norm": (_i, [_p, _i, _p, _i, _i, _i, _f, _p, _i, _p]),
+    "moe_rms_norm_quant": (_i, [_p, _p, _p, _i, _i, _i, _f, _p, _p, _p, _p, _p]),
     "moe_router_topk": (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _p, _p, _p, _p]),
     "moe_num_blocks": (_i, [_i, _i, _i, _i]),
     "moe_mapping_workspace_bytes": (_sz, [_i, _i]),

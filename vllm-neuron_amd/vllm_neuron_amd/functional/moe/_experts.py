@@ -152,18 +152,20 @@ def as_bf16(x):
     return x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
 
 
-def run_experts(x_bf16, tpid, b2e, B, k_rows, k_bound, w):
+def run_experts(x_bf16, tpid, b2e, B, k_rows, k_bound, w, xq=None, xs=None):
     """gate_up -> SiLU * up -> down for every slot of a blockwise mapping.
 
     x_bf16 [T, H]; tpid [N*B] int32 (slot -> token, -1 or >= T for padding);
     b2e [N] int32. k_rows is the expected routed rows per token (picks the tile
     height), k_bound an upper bound on them (sizes the tile list). Returns
-    (y [N*B + n_shared*T, H] bf16, N*B)."""
+    (y [N*B + n_shared*T, H] bf16, N*B). xq/xs: x's 1x128 codes and scales when
+    already computed (the fused norm prologue)."""
     T = x_bf16.shape[0]
     E, S = w.n_experts, w.n_shared
     N = b2e.numel()
     NB = N * B
-    xq, xs = ops.act_quant(x_bf16)
+    if xq is None:
+        xq, xs = ops.act_quant(x_bf16)
     if ops.use_block_kernels(T, k_rows, E):
         tiles, num, mbt = ops.build_block_tiles(tpid, b2e, B, T, k_bound, E, S)
         hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mbt)
@@ -176,12 +178,12 @@ def run_experts(x_bf16, tpid, b2e, B, k_rows, k_bound, w):
     return y, NB
 
 
-def routed_forward(x_bf16, ids, wts, w, block_size=256):
+def routed_forward(x_bf16, ids, wts, w, block_size=256, xq=None, xs=None):
     """Experts of ids [T, K] int32 weighted by wts [T, K] fp32 (+ the shared
     experts of w, weight 1), combined per token in k order: [T, H] bf16."""
     T, K = ids.shape
     E, H = w.n_experts, w.hidden
     m = ops.blockwise_mapping(ids=ids.contiguous(), n_experts=E, top_k=K, block_size=block_size)
     y, NB = run_experts(x_bf16, m["token_position_to_id"], m["block_to_expert"], block_size, K, K,
-                        w)
+                        w, xq, xs)
     return ops.combine(y, m["inv_pos"], wts.contiguous(), T, H, NB, w.n_shared)

@@ -13,9 +13,11 @@ Reference: vllm_neuron/functional/moe/moe_block_tkg.py:306-591 (API),
   5. the shared expert (gate [H, I_sh], up [H, I_sh], down [I_sh, H]) is added
      with weight 1 (kernel-only in the reference, :314-316, :389-391)
 Returns (output [T, H], router_logits [T, E] fp32), or output alone when
-skip_router_logits.
+skip_router_logits; with a residual [T, H] (bf16), the pre-norm sum inp + residual
+is normalized and returned last as residual_out (moe_block_tkg.py:421-428).
 
-Compute path (all HIP): moe_rms_norm -> moe_router_logits (bf16 operands, as
+Compute path (all HIP): moe_rms_norm_quant (bf16 input: residual add, RMSNorm and
+the experts' 1x128 quantization in one pass; fp32 input: moe_rms_norm) -> moe_router_logits (bf16 operands, as
 the reference's fp32 matmul of bf16 values) -> moe_router_topk -> blockwise
 mapping -> fp8 experts -> combine. Routed experts are float8_e4m3fn with
 128x128 block scales (expert_gate_up_weights_scale / expert_down_weights_scale
@@ -84,7 +86,7 @@ def moe_block_tkg(
             shared_expert_up_bias, shared_expert_down_bias)),
         "STATIC_MX input scales": expert_gate_up_input_scale is not None
             or expert_down_input_scale is not None,
-        "fused residual add": residual is not None,
+        "fused residual add on float32 input": residual is not None and inp.dtype != torch.bfloat16,
         "gate/up clamps": any(v is not None for v in (gate_clamp_upper_limit, gate_clamp_lower_limit,
                                                       up_clamp_upper_limit, up_clamp_lower_limit)),
         f"activation {getattr(hidden_act_fn, 'name', hidden_act_fn)}": hidden_act_fn != ActFnType.SiLU,
@@ -125,8 +127,20 @@ def moe_block_tkg(
     if x.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"inp must be bfloat16 or float32, got {x.dtype}")
 
-    # 1. RMSNorm, cast back to the input dtype (:135-151)
-    xn = ops.rms_norm(x.contiguous(), gamma, eps, hidden_actual, out_dtype=x.dtype)
+    # 1. (residual add, :341, :421-428) RMSNorm, cast back to the input dtype (:135-151).
+    # bf16 input: one fused pass that also quantizes the normalized rows for the experts.
+    xq = xs = res_out = None
+    if x.dtype == torch.bfloat16:
+        r = None
+        if residual is not None:
+            r = residual.reshape(-1, residual.shape[-1]) if residual.dim() == 3 else residual
+            if tuple(r.shape) != (T, H) or r.dtype != torch.bfloat16:
+                raise ValueError(f"residual must be bfloat16 [T, H] = [{T}, {H}], got "
+                                 f"{r.dtype} {tuple(residual.shape)}")
+            r = r.contiguous()
+        xn, xq, xs, res_out = ops.rms_norm_quant(x.contiguous(), gamma, eps, hidden_actual, r)
+    else:
+        xn = ops.rms_norm(x.contiguous(), gamma, eps, hidden_actual, out_dtype=x.dtype)
     # 2. fp32 router matmul on the normalized values (:153-163)
     wt = router_weights.t()
     wt = wt if wt.is_contiguous() else wt.contiguous()
@@ -150,9 +164,11 @@ def moe_block_tkg(
         shared = _experts.shared_weights(shared_expert_gate_w, shared_expert_up_w,
                                          shared_expert_down_w, I)
     w = _experts.make_weights(w13, s13, w2, s2, shared)
-    out = _experts.routed_forward(_experts.as_bf16(xn), ids, wts, w)
+    out = _experts.routed_forward(_experts.as_bf16(xn), ids, wts, w, xq=xq, xs=xs)
     if x.dtype != torch.bfloat16:
         out = out.to(x.dtype)
-    if skip_router_logits:
-        return out
-    return out, logits
+    # (output, router_logits[, residual_out]) as the reference's kernel path (:480)
+    res = (out,) if skip_router_logits else (out, logits)
+    if res_out is not None:
+        res = res + (res_out.reshape(inp.shape),)
+    return res[0] if len(res) == 1 else res

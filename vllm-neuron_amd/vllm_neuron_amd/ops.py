@@ -121,6 +121,29 @@ def rms_norm(x, gamma, eps, hidden_actual=None, out_dtype=None):
     return out
 
 
+def rms_norm_quant(x, gamma, eps, hidden_actual=None, residual=None):
+    """Fused decode prologue on bf16 x [T,H]: v = x, or bf16(x + residual) when a
+    residual is given; xn = RMSNorm(v) (bf16, as rms_norm); q, s = act_quant(xn).
+    Returns (xn, q, s, v or None)."""
+    _need_cuda(x, gamma, residual)
+    T, H = x.shape
+    _need(x, torch.bfloat16, (T, H), "hidden_states")
+    if residual is not None:
+        _need(residual, torch.bfloat16, (T, H), "residual")
+    g = gamma.reshape(-1)
+    if g.numel() != H:
+        raise ValueError(f"gamma must hold H={H} values, got shape {tuple(gamma.shape)}")
+    g = g.to(torch.float32).contiguous()
+    ha = H if hidden_actual is None else int(hidden_actual)
+    xn = torch.empty(T, H, device=x.device, dtype=torch.bfloat16)
+    q = torch.empty(T, H, device=x.device, dtype=FP8)
+    sc = torch.empty(T, H // 128, device=x.device, dtype=torch.float32)
+    v = None if residual is None else torch.empty(T, H, device=x.device, dtype=torch.bfloat16)
+    _lib.call("moe_rms_norm_quant", ptr(x), ptr(residual), ptr(g), T, H, ha, float(eps), ptr(xn),
+              ptr(v), ptr(_u8(q)), ptr(sc), _stream())
+    return xn, q, sc, v
+
+
 def router_topk(logits, top_k, order, scoring, n_group=1, topk_group=1, corr_bias=None,
                 renorm=False, eps=0.0, scale=1.0, dense=False):
     """logits [T,E] fp32 -> ids [T,K] int32, weights [T,K] fp32 (+ affinities [T,E] if dense)."""
