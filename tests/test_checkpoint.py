@@ -15,7 +15,7 @@ from vllm_neuron_amd.checkpoint import CheckpointIndex, load_moe_layer
 LAYER = 3
 
 
-def _hf_tensors(w, layer=LAYER, shared_split=1):
+def _hf_tensors(w, layer=LAYER):
     """The checkpoint keys of one MoE layer from a stacked Fp8MoEWeights."""
     E, I2, H = w.w13.shape
     I = I2 // 2

@@ -42,7 +42,6 @@ constexpr int kStageA = kBM * kBK;  // 32 KB
 constexpr int kStageB = kBN * kBK;  // 32 KB
 constexpr int kDmaPerWave = (kStageA + kStageB) / 1024 / 8;  // 8 x 1 KB regions per wave
 constexpr int kStageSA = 2 * kBM * 4;  // activation scales of the stage's block, one copy per column half
-constexpr int kStage = kStageA + kStageB;
 constexpr int kMaxKB = 128;  // K <= 16384
 
 struct BlkArgs {
@@ -83,14 +82,6 @@ __device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base)
 // groups of the 64-bank LDS (two 128-byte rows span the banks once).
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
-// 16x16x128 operand fragment of `row`: logical chunks g and g + 4 (g = lane / 16).
-__device__ __forceinline__ v8i lds_frag16(const uint8_t* base, int row, int g) {
-  const uint8_t* rp = base + row * kBK;
-  int4 lo = *(const int4*)(rp + swz(row, g) * 16);
-  int4 hi = *(const int4*)(rp + swz(row, g + 4) * 16);
-  return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-}
-
 template <int KIND>
 __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs p) {
   // Pipeline stages as distinct objects, so the compiler can tell that fragment
@@ -99,7 +90,7 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   __shared__ __attribute__((aligned(16))) uint8_t sTB0[kStageB];  // B tile of stage 0
   __shared__ __attribute__((aligned(16))) uint8_t sTA1[kStageA];
   __shared__ __attribute__((aligned(16))) uint8_t sTB1[kStageB];
-  __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageSA];  // A scales of sT0's block
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageSA];  // A scales of stage 0's block
   __shared__ __attribute__((aligned(16))) uint8_t sA1[kStageSA];
   __shared__ __attribute__((aligned(16))) float sR0[2 * kBM];  // scale ratio per (half, row)
   __shared__ __attribute__((aligned(16))) float sR1[2 * kBM];
