@@ -137,42 +137,9 @@ def workload_report(name, x, w, cfg, steps, torch, ops):
             "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
 
 
-def prologue_report(torch, ops, dev, T=64, H=7168, reps=50):
-    """Decode prologue (residual add, RMSNorm, 1x128 quantization) fused in one kernel
-    against the same work as separate launches, with its HBM bytes per call."""
-    g = torch.Generator(device="cpu").manual_seed(7)
-    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
-    r = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
-    gamma = (1 + 0.1 * torch.randn(H, generator=g)).to(dev)
-
-    def fused():
-        ops.rms_norm_quant(x, gamma, 1e-6, None, r)
-
-    def separate():
-        v = x + r
-        ops.act_quant(ops.rms_norm(v, gamma, 1e-6))
-
-    res = {}
-    for name, fn in (("fused_us", fused), ("separate_us", separate)):
-        fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        res[name] = round(e0.elapsed_time(e1) / reps * 1e3, 2)
-    nbytes = T * H * (2 + 2 + 2 + 2 + 1) + T * (H // 128) * 4 + H * 4
-    return {"workload": f"decode prologue, {T} tokens x {H}: residual add + RMSNorm + 1x128 quant",
-            **res, "alg_bytes": nbytes,
-            "hbm_frac_fused": round(nbytes / (res["fused_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-
-
 def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev):
-    """Kimi-K2 over its token sweep, GLM-4.5 with Zipf-skewed routing, and the
-    fused decode prologue."""
-    out = [prologue_report(torch, ops, dev)]
+    """Kimi-K2 over its token sweep and GLM-4.5 with Zipf-skewed routing."""
+    out = []
     cfg = PRESETS["kimi_k2"]
     w = synthetic.make_weights(cfg, 3, device=dev, experts_device=dev)
     for T in (1, 16, 256, 2048, 16384):

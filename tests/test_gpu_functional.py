@@ -52,14 +52,16 @@ def _ids_weights_from_dense(aff):
 
 # ---------------------------------------------------------------- kernels
 
-@pytest.mark.parametrize("x_dtype, out_dtype, ha", [
-    (torch.bfloat16, torch.bfloat16, None), (torch.bfloat16, torch.bfloat16, 1000),
-    (torch.float32, torch.float32, None), (torch.float32, torch.bfloat16, 777)])
-def test_rms_norm_kernel(cuda, x_dtype, out_dtype, ha):
-    say("rms_norm", x_dtype, out_dtype, ha)
+@pytest.mark.parametrize("x_dtype, out_dtype, ha, H", [
+    (torch.bfloat16, torch.bfloat16, None, 1024), (torch.bfloat16, torch.bfloat16, 1000, 1024),
+    (torch.float32, torch.float32, None, 1024), (torch.float32, torch.bfloat16, 777, 1024),
+    (torch.bfloat16, torch.float32, None, 7168), (torch.bfloat16, torch.bfloat16, 1000, 1004)])
+def test_rms_norm_kernel(cuda, x_dtype, out_dtype, ha, H):
+    """H % 8 == 0 runs the vector kernel (row held in registers), H = 1004 the scalar one."""
+    say("rms_norm", x_dtype, out_dtype, ha, H)
     g = torch.Generator().manual_seed(5)
-    x = (torch.randn(37, 1024, generator=g) * 3).to(x_dtype).to(cuda)
-    gamma = (1 + 0.1 * torch.randn(1024, generator=g)).to(cuda)
+    x = (torch.randn(37, H, generator=g) * 3).to(x_dtype).to(cuda)
+    gamma = (1 + 0.1 * torch.randn(H, generator=g)).to(cuda)
     y = ops.rms_norm(x, gamma, 1e-6, ha, out_dtype=out_dtype)
     ref = R.rms_norm_padded(np_f32(x), np_f32(gamma), 1e-6, ha)
     got = np_f32(y)

@@ -47,9 +47,12 @@ def test_mfma_fp8_wide_range_accumulation(cuda):
     assert err.max() < 1e-3
 
 
-@pytest.mark.parametrize("R_,C", [(64, 1024), (3, 7168), (1, 128), (257, 5120), (8192, 7168)])
-def test_act_quant_bit_exact(cuda, R_, C):
-    say("act_quant", R_, C)
+@pytest.mark.parametrize("R_,C,offset", [(64, 1024, 0), (3, 7168, 0), (1, 128, 0), (257, 5120, 0),
+                                         (8192, 7168, 0), (5, 384, 2), (33, 1024, 6)])
+def test_act_quant_bit_exact(cuda, R_, C, offset):
+    """offset > 0 starts x that many bf16 elements into its buffer (4-byte but not
+    16-byte aligned), which takes the scalar kernel instead of the vector one."""
+    say("act_quant", R_, C, offset)
     g = torch.Generator().manual_seed(R_ * 7 + C)
     x = torch.randn(R_, C, generator=g)
     if R_ > 2:
@@ -57,7 +60,13 @@ def test_act_quant_bit_exact(cuda, R_, C):
         x[1, :256] *= 1e-30          # bf16 subnormal / tiny range
         x[2, 128:256] *= 1e4
     xb = x.to(torch.bfloat16)
-    q, s = ops.act_quant(xb.to(cuda))
+    xd = xb.to(cuda)
+    if offset:
+        buf = torch.empty(R_ * C + offset, dtype=torch.bfloat16, device=cuda)
+        xd = buf[offset:].view(R_, C)
+        xd.copy_(xb.to(cuda))
+        assert xd.data_ptr() % 16 != 0
+    q, s = ops.act_quant(xd)
     torch.cuda.synchronize()
     oq, os_ = quant_act_1x128(xb.float().numpy())
     assert np.array_equal(np_u8(q), oq)

@@ -124,6 +124,37 @@ __device__ __forceinline__ void quant_pair_1x128(uint32_t pair, uint8_t* q, floa
   if (lane == 0) *s = sc;
 }
 
+// One 1x128 group held by 16 consecutive lanes (a 16-aligned lane segment): each
+// lane holds 8 consecutive values v (bf16 values widened to fp32) and writes their
+// codes as 8 bytes at q; the segment's first lane writes the scale. Same arithmetic
+// as quant_pair_1x128 (exact amax, IEEE divisions), so the codes are identical.
+__device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t* q, float* s, bool first) {
+  float a = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(v[e]));
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, MOE_WAVE));
+  const float sc = fmaxf(a, 0x1.b7cdfep-34f) / 448.0f;
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    lo |= f32_to_e4m3fn(fminf(fmaxf(v[e] / sc, -448.0f), 448.0f)) << (8 * e);
+    hi |= f32_to_e4m3fn(fminf(fmaxf(v[e + 4] / sc, -448.0f), 448.0f)) << (8 * e);
+  }
+  *(uint2*)q = make_uint2(lo, hi);
+  if (first) *s = sc;
+}
+
+// Widen 8 bf16 values (one 16-byte chunk) to fp32.
+__device__ __forceinline__ void bf16x8_to_f32(const int4 c, float (&v)[8]) {
+  const uint32_t w[4] = {(uint32_t)c.x, (uint32_t)c.y, (uint32_t)c.z, (uint32_t)c.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
 // The same, loading the group from x (bf16, 128 columns).
 __device__ __forceinline__ void quant_group_1x128(const uint16_t* x, uint8_t* q, float* s, int lane) {
   quant_pair_1x128(*(const uint32_t*)(x + 2 * lane), q, s, lane);

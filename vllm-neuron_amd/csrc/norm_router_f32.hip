@@ -50,46 +50,95 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const void* __restrict__ 
   }
 }
 
-// Decode prologue in one pass per row: optional residual add (the pre-norm sum
-// v = bf16(x + residual) is written out as the next residual stream), RMSNorm of
-// v exactly as rms_norm_kernel computes it (same fixed-order sum), the bf16
-// normalized row, and its 1x128 e4m3fn quantization as act_quant_kernel computes
-// it. The outputs are bit-identical to moe_rms_norm followed by
-// moe_act_quant_1x128 (after a bf16 residual add), without the round trip of the
-// normalized row through HBM.
-__global__ __launch_bounds__(256) void rms_norm_quant_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res, const float* __restrict__ gamma,
-    int H, int ha, float eps, uint16_t* __restrict__ xn, uint16_t* __restrict__ res_out,
+// Vector RMSNorm for H % 8 == 0: one workgroup per row holds the row in registers
+// as 16-byte chunks of 8 values (chunk c = thread + 256 j, j < NJ), so the row is
+// read once.
+// The sum of squares runs in a fixed order: each thread over its chunks and their 8
+// values in order, a wave butterfly, then the four wave sums in order.
+// RES: the row is first v = bf16(x + residual) (written to res_out: the next residual
+// stream). QUANT (H % 128 == 0): the bf16 normalized row is also quantized 1x128 to
+// e4m3fn, one group per 16-lane segment, with act_quant's arithmetic. rms_norm and the
+// fused prologue both run this kernel, so the prologue's normalized row is bit-identical
+// to moe_rms_norm's and its codes to moe_act_quant_1x128 of that row.
+constexpr int kNormMaxChunks = 8;  // H <= 256 * 8 * 8 = 16384
+template <bool XF32, bool OF32, bool RES, bool QUANT, int NJ>
+__global__ __launch_bounds__(256) void rms_norm_vec_kernel(
+    const void* __restrict__ x, const uint16_t* __restrict__ res, const float* __restrict__ gamma,
+    int H, int ha, float eps, void* __restrict__ out, uint16_t* __restrict__ res_out,
     uint8_t* __restrict__ q, float* __restrict__ qs) {
   __shared__ float s_part[4];
-  const size_t row = (size_t)blockIdx.x * H;
-  auto val = [&](int c) -> float {
-    float v = bf16_bits_to_f32(x[row + c]);
-    if (res != nullptr) v = bf16_bits_to_f32(f32_to_bf16_bits(v + bf16_bits_to_f32(res[row + c])));
-    return v;
-  };
+  const int tid = threadIdx.x, nch = H >> 3;
+  const size_t base = (size_t)blockIdx.x * H;
+  float v[NJ][8];
+  float4 gv[NJ][2];  // gamma, loaded with the row so its latency overlaps
   float ss = 0.f;
-  for (int c = threadIdx.x; c < ha; c += 256) {
-    const float v = val(c);
-    ss += v * v;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = tid + 256 * j;
+    if (c < nch) {
+      gv[j][0] = *(const float4*)(gamma + 8 * c);
+      gv[j][1] = *(const float4*)(gamma + 8 * c + 4);
+      if (XF32) {
+        const float4 a = *(const float4*)((const float*)x + base + 8 * c);
+        const float4 b = *(const float4*)((const float*)x + base + 8 * c + 4);
+        v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
+        v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
+      } else {
+        bf16x8_to_f32(*(const int4*)((const uint16_t*)x + base + 8 * c), v[j]);
+      }
+      if (RES) {
+        float r[8];
+        bf16x8_to_f32(*(const int4*)(res + base + 8 * c), r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = bf16_bits_to_f32(f32_to_bf16_bits(v[j][e] + r[e]));
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (8 * c + e < ha) ss += v[j][e] * v[j][e];
+    }
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
-  if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
+  if ((tid & 63) == 0) s_part[tid >> 6] = ss;
   __syncthreads();
   const float tot = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
-  const float r = 1.0f / sqrtf(tot / (float)ha + eps);
-  const int lane = threadIdx.x & 63, G = H / 128;
-  for (int gi = threadIdx.x >> 6; gi < G; gi += 4) {
-    const int c0 = gi * 128 + 2 * lane;
-    const float v0 = val(c0), v1 = val(c0 + 1);
-    const float y0 = (c0 < ha) ? (v0 * r) * gamma[c0] : 0.f;
-    const float y1 = (c0 + 1 < ha) ? (v1 * r) * gamma[c0 + 1] : 0.f;
-    const uint32_t pair = (uint32_t)f32_to_bf16_bits(y0) | ((uint32_t)f32_to_bf16_bits(y1) << 16);
-    *(uint32_t*)(xn + row + c0) = pair;
-    if (res_out != nullptr)
-      *(uint32_t*)(res_out + row + c0) = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
-    quant_pair_1x128(pair, q + row + gi * 128, qs + (size_t)blockIdx.x * G + gi, lane);
+  const float rn = 1.0f / sqrtf(tot / (float)ha + eps);
+  const int G = H / MOE_GROUP;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int c = tid + 256 * j;
+    if (c >= nch) continue;  // whole 16-lane segments leave together when H % 128 == 0
+    const float gm[8] = {gv[j][0].x, gv[j][0].y, gv[j][0].z, gv[j][0].w,
+                         gv[j][1].x, gv[j][1].y, gv[j][1].z, gv[j][1].w};
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = (8 * c + e < ha) ? (v[j][e] * rn) * gm[e] : 0.f;
+    if (RES) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16_bits(v[j][2 * i]) | ((uint32_t)f32_to_bf16_bits(v[j][2 * i + 1]) << 16);
+      *(int4*)(res_out + base + 8 * c) = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+    }
+    if (OF32) {
+      *(float4*)((float*)out + base + 8 * c) = make_float4(y[0], y[1], y[2], y[3]);
+      *(float4*)((float*)out + base + 8 * c + 4) = make_float4(y[4], y[5], y[6], y[7]);
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16_bits(y[2 * i]) | ((uint32_t)f32_to_bf16_bits(y[2 * i + 1]) << 16);
+      *(int4*)((uint16_t*)out + base + 8 * c) = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+      if (QUANT) {
+        float yb[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          yb[2 * i] = __uint_as_float(w[i] << 16);
+          yb[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+        quant8_1x128(yb, q + base + 8 * c, qs + (size_t)blockIdx.x * G + (c >> 4), (tid & 15) == 0);
+      }
+    }
   }
 }
 
@@ -197,6 +246,26 @@ __global__ void router_logits_f32_reduce(const float* __restrict__ part,
   }
 }
 
+// Launch rms_norm_vec_kernel with the smallest chunk count per thread that covers H.
+template <bool XF32, bool OF32, bool RES, bool QUANT>
+static void launch_rms_norm_vec(int T, int H, hipStream_t st, const void* x, const uint16_t* res,
+                                const float* gamma, int ha, float eps, void* out,
+                                uint16_t* res_out, uint8_t* q, float* qs) {
+  const int nj = (H / 8 + 255) / 256;
+  if (nj <= 1)
+    hipLaunchKernelGGL((rms_norm_vec_kernel<XF32, OF32, RES, QUANT, 1>), dim3(T), dim3(256), 0, st, x, res,
+                       gamma, H, ha, eps, out, res_out, q, qs);
+  else if (nj <= 2)
+    hipLaunchKernelGGL((rms_norm_vec_kernel<XF32, OF32, RES, QUANT, 2>), dim3(T), dim3(256), 0, st, x, res,
+                       gamma, H, ha, eps, out, res_out, q, qs);
+  else if (nj <= 4)
+    hipLaunchKernelGGL((rms_norm_vec_kernel<XF32, OF32, RES, QUANT, 4>), dim3(T), dim3(256), 0, st, x, res,
+                       gamma, H, ha, eps, out, res_out, q, qs);
+  else
+    hipLaunchKernelGGL((rms_norm_vec_kernel<XF32, OF32, RES, QUANT, kNormMaxChunks>), dim3(T), dim3(256), 0,
+                       st, x, res, gamma, H, ha, eps, out, res_out, q, qs);
+}
+
 }  // namespace moe
 
 using namespace moe;
@@ -211,8 +280,25 @@ extern "C" int moe_rms_norm(const void* x, int x_is_f32, const float* gamma, int
                 "hidden_actual must be in [1, H=%d], got %d", H, hidden_actual);
   MOE_CHECK_ARG(eps >= 0.f, "eps must be >= 0");
   if (T == 0) return MOE_OK;
-  hipLaunchKernelGGL(rms_norm_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, x,
-                     x_is_f32 ? 1 : 0, gamma, H, hidden_actual, eps, out, out_is_f32 ? 1 : 0);
+  hipStream_t st = (hipStream_t)stream;
+  const bool vec = H % 8 == 0 && H <= 256 * 8 * kNormMaxChunks && ((uintptr_t)x & 15) == 0 &&
+                   ((uintptr_t)out & 15) == 0 && ((uintptr_t)gamma & 15) == 0;
+  if (!vec) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(T), dim3(256), 0, st, x, x_is_f32 ? 1 : 0, gamma, H,
+                       hidden_actual, eps, out, out_is_f32 ? 1 : 0);
+  } else if (x_is_f32 && out_is_f32) {
+    launch_rms_norm_vec<true, true, false, false>(T, H, st, x, nullptr, gamma, hidden_actual, eps, out, nullptr,
+                                                  nullptr, nullptr);
+  } else if (x_is_f32) {
+    launch_rms_norm_vec<true, false, false, false>(T, H, st, x, nullptr, gamma, hidden_actual, eps, out, nullptr,
+                                                  nullptr, nullptr);
+  } else if (out_is_f32) {
+    launch_rms_norm_vec<false, true, false, false>(T, H, st, x, nullptr, gamma, hidden_actual, eps, out, nullptr,
+                                                  nullptr, nullptr);
+  } else {
+    launch_rms_norm_vec<false, false, false, false>(T, H, st, x, nullptr, gamma, hidden_actual, eps, out, nullptr,
+                                                  nullptr, nullptr);
+  }
   MOE_API_END();
 }
 
@@ -227,13 +313,20 @@ extern "C" int moe_rms_norm_quant(const void* x_bf16, const void* residual_bf16,
   MOE_CHECK_ARG(hidden_actual >= 1 && hidden_actual <= H,
                 "hidden_actual must be in [1, H=%d], got %d", H, hidden_actual);
   MOE_CHECK_ARG(eps >= 0.f, "eps must be >= 0");
-  MOE_CHECK_ARG(((uintptr_t)x_bf16 & 3) == 0 && ((uintptr_t)xn_bf16 & 3) == 0 && ((uintptr_t)q & 1) == 0 &&
-                    ((uintptr_t)residual_bf16 & 3) == 0 && ((uintptr_t)residual_out_bf16 & 3) == 0,
-                "x, residual, xn and residual_out must be 4-byte aligned, q 2-byte aligned");
+  MOE_CHECK_SUPPORTED(H <= 256 * 8 * kNormMaxChunks, "H must be at most %d, got %d",
+                      256 * 8 * kNormMaxChunks, H);
+  MOE_CHECK_ARG(((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)xn_bf16 & 15) == 0 &&
+                    ((uintptr_t)residual_bf16 & 15) == 0 && ((uintptr_t)residual_out_bf16 & 15) == 0 &&
+                    ((uintptr_t)gamma & 15) == 0 && ((uintptr_t)q & 7) == 0,
+                "x, residual, xn, residual_out and gamma must be 16-byte aligned, q 8-byte aligned");
   if (T == 0) return MOE_OK;
-  hipLaunchKernelGGL(rms_norm_quant_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x_bf16, (const uint16_t*)residual_bf16, gamma, H, hidden_actual,
-                     eps, (uint16_t*)xn_bf16, (uint16_t*)residual_out_bf16, q, s);
+  if (residual_bf16 != nullptr)
+    launch_rms_norm_vec<false, false, true, true>(T, H, (hipStream_t)stream, x_bf16,
+                                                  (const uint16_t*)residual_bf16, gamma, hidden_actual,
+                                                  eps, xn_bf16, (uint16_t*)residual_out_bf16, q, s);
+  else
+    launch_rms_norm_vec<false, false, false, true>(T, H, (hipStream_t)stream, x_bf16, nullptr, gamma,
+                                                   hidden_actual, eps, xn_bf16, nullptr, q, s);
   MOE_API_END();
 }
 

@@ -28,6 +28,35 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   }
 }
 
+// Vector form for 16-byte aligned x and 8-byte aligned q: lane l of a wave takes
+// the 16-byte chunk (l & 15) of group 4 * quad + l / 16, so a wave covers four
+// groups per load instruction; each wave keeps U quads of loads in flight.
+__global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __restrict__ x, long groups,
+                                                            uint8_t* __restrict__ q,
+                                                            float* __restrict__ s) {
+  constexpr int U = 4;
+  const int lane = threadIdx.x & 63;
+  const long quads = (groups + 3) / 4;
+  const long nwaves = (long)gridDim.x * 4;
+  for (long q0 = (long)blockIdx.x * 4 + (threadIdx.x >> 6); q0 < quads; q0 += U * nwaves) {
+    int4 c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long gi = 4 * (q0 + u * nwaves) + (lane >> 4);
+      c[u] = (gi < groups) ? *(const int4*)(x + gi * MOE_GROUP + 8 * (lane & 15)) : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long gi = 4 * (q0 + u * nwaves) + (lane >> 4);  // whole 16-lane segments share gi
+      if (gi < groups) {
+        float v[8];
+        bf16x8_to_f32(c[u], v);
+        quant8_1x128(v, q + gi * MOE_GROUP + 8 * (lane & 15), s + gi, (lane & 15) == 0);
+      }
+    }
+  }
+}
+
 // out[t] = sum_s w[t,s] * y[inv[t,s]] (inv >= 0) + sum_j y[NB + j*T + t], fp32 accumulation,
 // one workgroup per token, 8 bf16 (16 B) per thread per step.
 // One workgroup per (token, column chunk). The token's live rows are listed in
@@ -111,9 +140,15 @@ extern "C" int moe_act_quant_1x128(const void* x_bf16, int rows, int cols, uint8
   MOE_CHECK_ARG(((uintptr_t)x_bf16 & 3) == 0 && ((uintptr_t)q & 1) == 0, "misaligned x or q");
   if (rows == 0) return MOE_OK;
   long groups = (long)rows * (cols / MOE_GROUP);
-  int grid = (int)std::min<long>((groups + 3) / 4, 2048);
-  hipLaunchKernelGGL(act_quant_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x_bf16, rows, cols, q, scales);
+  if (((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)q & 7) == 0) {
+    const int grid = (int)std::max(1L, std::min<long>((groups + 15) / 16, 2048));
+    hipLaunchKernelGGL(act_quant_vec_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x_bf16, groups, q, scales);
+  } else {
+    int grid = (int)std::min<long>((groups + 3) / 4, 2048);
+    hipLaunchKernelGGL(act_quant_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x_bf16, rows, cols, q, scales);
+  }
   MOE_API_END();
 }
 
