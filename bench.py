@@ -137,6 +137,21 @@ def workload_report(name, x, w, cfg, steps, torch, ops):
             "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
 
 
+def run_prologue(calls, torch, ops, dev, H=7168):
+    """Residual add + RMSNorm + 1x128 quantization, fused (moe_rms_norm_quant) and as
+    separate launches (bf16 add, moe_rms_norm, moe_act_quant_1x128), for a kernel trace."""
+    g = torch.Generator().manual_seed(7)
+    for T in (64, 8192):
+        print(f"[bench] prologue T={T}", file=sys.stderr, flush=True)
+        x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+        r = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+        gamma = (1 + 0.1 * torch.randn(H, generator=g)).to(dev)
+        for _ in range(calls):
+            ops.rms_norm_quant(x, gamma, 1e-6, None, r)
+            ops.act_quant(ops.rms_norm(x + r, gamma, 1e-6))
+        torch.cuda.synchronize()
+
+
 def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev):
     """Kimi-K2 over its token sweep and GLM-4.5 with Zipf-skewed routing."""
     out = []
@@ -195,6 +210,9 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--extra", action="store_true",
                     help="also time Kimi-K2 (1..16384 tokens) and GLM-4.5 (Zipf) layers")
+    ap.add_argument("--prologue-calls", type=int, default=0,
+                    help="only run the decode prologue (fused, then as separate launches) this "
+                         "many times at 64 and 8192 tokens, for a kernel trace; no timing")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the layer keeps all experts "
@@ -205,6 +223,9 @@ def main():
     from vllm_neuron_amd import PRESETS, ops, synthetic
 
     dev = torch.device("cuda:0")
+    if args.prologue_calls:
+        run_prologue(args.prologue_calls, torch, ops, dev)
+        return
     cfg = PRESETS["dsv3"]
     H, I, E, K = cfg.hidden, cfg.intermediate, cfg.n_experts, cfg.top_k
     print(f"[bench] generating DeepSeek-V3 weights on {torch.cuda.get_device_name(0)}", file=sys.stderr, flush=True)
