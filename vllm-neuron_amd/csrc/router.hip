@@ -20,19 +20,31 @@ namespace moe {
 // Operand lane layout: lane l holds row l%16 and the 8 K-values
 // [s*32 + (l/16)*8, +8) of sub-step s; A and B use the same mapping, so the
 // MFMA forms the full 32-long dot product per sub-step.
-// blockIdx.z splits K; with more than one split the kernel writes fp32
-// partials [ksplit, T, E] that router_logits_reduce sums in split order.
+// K is split into ks chunks; with more than one chunk the kernel writes fp32
+// partials [ks, T, E] that router_logits_reduce sums in chunk order.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const float* __restrict__ bias, int T, int H, int E, int kchunk,
+    const float* __restrict__ bias, int T, int H, int E, int kchunk, int ks,
     float* __restrict__ out) {
   // x tile: 64 rows x 256 columns (four 64-column K steps), rows padded by 8.
   constexpr int KW = 256, LDX = KW + 8;
   __shared__ __attribute__((aligned(16))) uint16_t sx[64][LDX];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t0 = blockIdx.x * 64, e0 = blockIdx.y * 64;
-  const int k_begin = blockIdx.z * kchunk;
+  // Tiles (64 tokens x 64 experts x one K chunk) are numbered expert tile fastest,
+  // then K chunk, then token tile, and workgroup b takes tile (b % 8) * per + b / 8:
+  // each XCD (b % 8) runs a contiguous tile range, so the expert tiles that share
+  // an x tile run together on one L2 and x is read from HBM once.
+  const int nct = (E + 63) / 64;
+  const long total = (long)nct * ((T + 63) / 64) * ks;
+  const long per = (total + 7) / 8;
+  const long L = (long)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (L >= total) return;  // whole workgroup
+  const int ct = (int)(L % nct);
+  const long rk = L / nct;
+  const int kz = (int)(rk % ks), rt = (int)(rk / ks);
+  const int t0 = rt * 64, e0 = ct * 64;
+  const int k_begin = kz * kchunk;
   const int k_end = min(H, k_begin + kchunk);
   const int g = lane >> 4, r16 = lane & 15;
 
@@ -107,8 +119,8 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   // C layout: lane l, register i -> row 4*(l/16)+i of the 16-row tile, column l%16.
   if (!erow_ok) return;
   const int e = e0 + wave * 16 + r16;
-  float bv = (bias != nullptr && gridDim.z == 1) ? bias[e] : 0.f;
-  float* o = out + (size_t)blockIdx.z * T * E;
+  float bv = (bias != nullptr && ks == 1) ? bias[e] : 0.f;
+  float* o = out + (size_t)kz * T * E;
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
 #pragma unroll
@@ -428,17 +440,18 @@ extern "C" int moe_router_logits(const void* x_bf16, const void* w_bf16, const f
   int ks = router_logits_splits(T, H, E);
   int kchunk = ((H / 64 + ks - 1) / ks) * 64;
   ks = (H + kchunk - 1) / kchunk;
-  dim3 grid((T + 63) / 64, (E + 63) / 64, ks);
+  const long tiles = (long)((T + 63) / 64) * ((E + 63) / 64) * ks;
+  const dim3 grid((unsigned)(((tiles + 7) / 8) * 8));
   if (ks == 1) {
     hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, st, (const uint16_t*)x_bf16,
-                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, logits);
+                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, ks, logits);
   } else {
     size_t need = (size_t)ks * T * E * sizeof(float);
     MOE_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                   "workspace too small: need %zu bytes", need);
     float* part = (float*)workspace;
     hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, st, (const uint16_t*)x_bf16,
-                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, part);
+                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, ks, part);
     size_t n = (size_t)T * E;
     int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
     hipLaunchKernelGGL(router_logits_reduce, dim3(blocks), dim3(256), 0, st, part, bias, T, E, ks,
