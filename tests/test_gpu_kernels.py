@@ -250,3 +250,31 @@ def test_block_tiles_cover_every_slot_once(cuda, T, K, E, B, S):
             assert np.all(b2e[np.arange(s0, s0 + rows) // B] == e)
     assert np.all(seen[:NB][tpid >= 0] == 1) and np.all(seen[NB:] == 1)
     assert np.all(seen[:NB][tpid < 0] <= 1)
+
+
+@pytest.mark.parametrize("T,K,S,with_w", [(64, 8, 1, True), (300, 6, 0, True), (5, 2, 2, False),
+                                         (1000, 8, 1, True)])
+def test_combine_matches_sequential_sum(cuda, T, K, S, with_w):
+    """out[t] = sum over t's live slots in slot order of w * y[slot] (+ shared rows, weight 1),
+    fp32 accumulation, bf16 result: within one bf16 rounding of the float64 sum. Dead slots
+    (-1) are skipped."""
+    say("combine", T, K, S, with_w)
+    H, NB = 1024, 4096
+    rng = np.random.default_rng(T + K + S)
+    y = rng.normal(0, 1, (NB + S * T, H)).astype(np.float32)
+    inv = rng.choice(NB, (T, K), replace=True).astype(np.int32)
+    inv[rng.random((T, K)) < 0.15] = -1
+    w = rng.uniform(0.1, 1, (T, K)).astype(np.float32) if with_w else None
+    yb = torch.from_numpy(y).to(torch.bfloat16)
+    out = ops.combine(yb.to(cuda), torch.from_numpy(inv).to(cuda),
+                      None if w is None else torch.from_numpy(w).to(cuda), T, H, NB, S)
+    y64 = yb.double().numpy()
+    ref = np.zeros((T, H))
+    for t in range(T):
+        for k in range(K):
+            if inv[t, k] >= 0:
+                ref[t] += (1.0 if w is None else float(w[t, k])) * y64[inv[t, k]]
+        for j in range(S):
+            ref[t] += y64[NB + j * T + t]
+    got = out.float().cpu().numpy()
+    assert np.allclose(got, ref, rtol=2 ** -7, atol=1e-5)

@@ -61,8 +61,8 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __re
 // one workgroup per token, 8 bf16 (16 B) per thread per step.
 // One workgroup per (token, column chunk). The token's live rows are listed in
 // slot order (ballot compaction, so the order and the fp32 sums are the same as a
-// sequential scan), then each thread sums its 8 columns over the rows, loading
-// four rows ahead of the accumulation.
+// sequential scan), then each thread sums its 8 columns over the rows, eight rows
+// of loads at a time.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const int32_t* __restrict__ inv,
                                                       const float* __restrict__ w, int S, int T,
@@ -100,14 +100,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-    for (int r0 = 0; r0 < n; r0 += 4) {
-      int4 v[4];
+    for (int r0 = 0; r0 < n; r0 += 8) {
+      // Eight rows in flight; rows past n reload row n - 1 and are not accumulated
+      // (unconditional loads keep the compiler's wait counts exact).
+      int4 v[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (r0 + q < n) v[q] = *(const int4*)(y + (size_t)s_row[r0 + q] * H + c * 8);
+      for (int q = 0; q < 8; ++q)
+        v[q] = *(const int4*)(y + (size_t)s_row[min(r0 + q, n - 1)] * H + c * 8);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (r0 + q < n) {
+      for (int q = 0; q < 8; ++q) {
+        if (r0 + q < n) {  // workgroup-uniform
           const float wt = s_w[r0 + q];
           const uint32_t u[4] = {(uint32_t)v[q].x, (uint32_t)v[q].y, (uint32_t)v[q].z, (uint32_t)v[q].w};
 #pragma unroll
