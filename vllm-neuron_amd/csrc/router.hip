@@ -216,12 +216,13 @@ __device__ __forceinline__ void top2_step(float& t1, float& t2) {
   t2 = fmaxf(lo, fmaxf(t2, b2));
 }
 
+template <int PM>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ corr_bias, int T, int E, int K,
     int order, int scoring, int n_group, int topk_group, int renorm, float eps, float scale,
     int32_t* __restrict__ ids, float* __restrict__ weights, float* __restrict__ aff) {
-  __shared__ float s_act[4][kTopkMaxE];
-  __shared__ float s_key[4][kTopkMaxE];
+  __shared__ float s_act[4][PM * 64];
+  __shared__ float s_key[4][PM * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;  // wave-uniform; no workgroup barrier below
@@ -230,9 +231,9 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   const float NEG_INF = -__builtin_inff();
   const bool need_act = order != MOE_ORDER_TOPK_ACT;
 
-  float lg[kTopkMaxP];
+  float lg[PM];
 #pragma unroll
-  for (int j = 0; j < kTopkMaxP; ++j) {
+  for (int j = 0; j < PM; ++j) {
     int e = lane + 64 * j;
     lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
   }
@@ -240,17 +241,17 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   if (need_act) {
     if (scoring == MOE_SCORING_SIGMOID) {
 #pragma unroll
-      for (int j = 0; j < kTopkMaxP; ++j) {
+      for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
         if (j < P && e < E) s_act[wave][e] = det_sigmoid_f32(lg[j]);
       }
     } else {
       float m = NEG_INF;
 #pragma unroll
-      for (int j = 0; j < kTopkMaxP; ++j) m = fmaxf(m, lg[j]);
+      for (int j = 0; j < PM; ++j) m = fmaxf(m, lg[j]);
       m = wave_max_f32(m);
 #pragma unroll
-      for (int j = 0; j < kTopkMaxP; ++j) {
+      for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
         if (j < P && e < E) s_act[wave][e] = det_exp_f32(lg[j] - m);
       }
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       for (int e = 0; e < E; ++e) sum += s_act[wave][e];
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int j = 0; j < kTopkMaxP; ++j) {
+      for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
         if (j < P && e < E) s_act[wave][e] = s_act[wave][e] / sum;
       }
@@ -270,10 +271,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 
   // Selection keys (kept in registers, mirrored in LDS for the group scan).
-  float key[kTopkMaxP];
-  bool valid[kTopkMaxP];
+  float key[PM];
+  bool valid[PM];
 #pragma unroll
-  for (int j = 0; j < kTopkMaxP; ++j) {
+  for (int j = 0; j < PM; ++j) {
     int e = lane + 64 * j;
     valid[j] = (j < P && e < E);
     float kv = NEG_INF;
@@ -301,7 +302,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       // so its top 2 is a DPP reduction within the half (lane 31 / 63 gets it).
       // NaN keys count as -inf, as in the sequential scan, which skips them.
 #pragma unroll
-      for (int j = 0; j < kTopkMaxP; ++j) {
+      for (int j = 0; j < PM; ++j) {
         if (j < P) {
           float t1 = (key[j] == key[j]) ? key[j] : NEG_INF, t2 = NEG_INF;
           top2_step<0xB1, 0xF>(t1, t2);
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       }
     }
 #pragma unroll
-    for (int j = 0; j < kTopkMaxP; ++j) {
+    for (int j = 0; j < PM; ++j) {
       int e = lane + 64 * j;
       if (valid[j] && !((keep >> (e / gs)) & 1ull)) valid[j] = false;
     }
@@ -360,14 +361,14 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   // K rounds of wave argmax; lane k keeps the k-th winner.
   int my_id = -1;
   float my_key = 0.f;
-  int taken[kTopkMaxP];
+  int taken[PM];
 #pragma unroll
-  for (int j = 0; j < kTopkMaxP; ++j) taken[j] = -1;
+  for (int j = 0; j < PM; ++j) taken[j] = -1;
   for (int k = 0; k < K; ++k) {
     float bv = NEG_INF;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < kTopkMaxP; ++j) {
+    for (int j = 0; j < PM; ++j) {
       int e = lane + 64 * j;
       if (valid[j] && taken[j] < 0 && better(key[j], e, bv, bi)) {
         bv = key[j];
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     }
     KeyIdx b = wave_argmax(bv, bi);
 #pragma unroll
-    for (int j = 0; j < kTopkMaxP; ++j)
+    for (int j = 0; j < PM; ++j)
       if (lane + 64 * j == b.i) taken[j] = k;
     if (lane == k) {
       my_id = (b.i < E) ? b.i : -1;  // no valid candidate left (NaN keys): id -1
@@ -413,7 +414,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   }
   if (aff != nullptr) {
 #pragma unroll
-    for (int j = 0; j < kTopkMaxP; ++j) {
+    for (int j = 0; j < PM; ++j) {
       int e = lane + 64 * j;
       int k = taken[j];
       float v = __shfl(wv, k < 0 ? 0 : k, 64);  // all lanes take part in the shuffle
@@ -487,8 +488,23 @@ extern "C" int moe_router_topk(const float* logits, const float* corr_bias, int 
                   "topk_group * group size must be >= top_k");
   }
   if (T == 0) return MOE_OK;
-  hipLaunchKernelGGL(router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream,
-                     logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
-                     renorm_eps, routed_scale, ids, weights, affinities);
+  // Registers and LDS sized for the smallest power-of-two count of 64-expert chunks
+  // that covers E, so the per-chunk loops unroll without dead iterations.
+  const int P = (E + 63) / 64;
+#define MOE_TOPK_LAUNCH(PMV)                                                                   \
+  hipLaunchKernelGGL(router_topk_kernel<PMV>, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, \
+                     logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,     \
+                     renorm_eps, routed_scale, ids, weights, affinities)
+  if (P <= 1)
+    MOE_TOPK_LAUNCH(1);
+  else if (P <= 2)
+    MOE_TOPK_LAUNCH(2);
+  else if (P <= 4)
+    MOE_TOPK_LAUNCH(4);
+  else if (P <= 8)
+    MOE_TOPK_LAUNCH(8);
+  else
+    MOE_TOPK_LAUNCH(kTopkMaxP);
+#undef MOE_TOPK_LAUNCH
   MOE_API_END();
 }
