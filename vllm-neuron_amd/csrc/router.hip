@@ -136,8 +136,16 @@ __global__ void router_logits_reduce(const float* __restrict__ part, const float
   size_t n = (size_t)T * E;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
        i += (size_t)gridDim.x * blockDim.x) {
+    // Sum in split order, eight partial loads in flight at a time.
     float s = 0.f;
-    for (int k = 0; k < ksplit; ++k) s += part[(size_t)k * n + i];
+    for (int k0 = 0; k0 < ksplit; k0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = part[(size_t)min(k0 + q, ksplit - 1) * n + i];
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (k0 + q < ksplit) s += v[q];
+    }
     if (bias != nullptr) s += bias[i % E];
     out[i] = s;
   }
