@@ -241,7 +241,12 @@ __global__ __launch_bounds__(1024) void map_small_kernel(
   __shared__ int s_wave[16];
   const int tid = threadIdx.x;
   const long nb_total = (long)N * B;
-  for (long i = tid; i < nb_total; i += blockDim.x) tpid[i] = -1;
+  long filled = 0;
+  if (((uintptr_t)tpid & 15) == 0) {  // 16-byte stores while they fit
+    filled = nb_total & ~3L;
+    for (long i = tid; i < filled / 4; i += blockDim.x) ((int4*)tpid)[i] = make_int4(-1, -1, -1, -1);
+  }
+  for (long i = filled + tid; i < nb_total; i += blockDim.x) tpid[i] = -1;
   if (tid == 0) ws.status[0] = 0;
   __syncthreads();  // the fill and the status reset land before the scatter below
   build_chunk_mask(bm, ids, nullptr, T, K, E, 0, ws.status);
