@@ -193,7 +193,7 @@ def test_layer_glm45_full_size_zipf(cuda):
 
 @pytest.mark.parametrize("T,E,K,S", [(2048, 8, 2, 0), (3000, 16, 4, 1), (700, 4, 2, 1)])
 def test_layer_block_kernels(cuda, T, E, K, S):
-    """Block-kernel path (> 12 rows per expert): block kernels against the oracle,
+    """Block-kernel path (> 20 rows per expert): block kernels against the oracle,
     including partial 256-row tiles, and agreement with the row-tile kernels."""
     cfg = MoEConfig(1024, 512, E, K, n_shared=S, scoring="sigmoid", grouped=True, n_group=1,
                     topk_group=1, renorm=True, routed_scaling=1.0)
@@ -213,3 +213,34 @@ def test_layer_block_kernels(cuda, T, E, K, S):
     y = ops.expert_down(hq, hs, w, T, NB, tiles, num, mx, 128)
     alt = ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, S)
     assert rel_l2(np_f32(out), np_f32(alt)) < 5e-3
+
+
+def test_block_kernels_every_tile_height(cuda):
+    """Block kernels on fixed expert counts whose tiles cover every row-group size
+    (1-64, 65-128, 129-192 and 193-256 rows, full 256-row tiles before each
+    remainder, and a 141-row shared-expert tail), against the oracle."""
+    cfg = MoEConfig(1024, 512, 8, 1, n_shared=1, scoring="sigmoid", routed_scaling=1.0)
+    counts = [256 + 30, 256 + 100, 256 + 170, 256 + 250, 50, 120, 190, 255]
+    T = sum(counts)
+    say("block kernels tile heights", T, counts)
+    rng = np.random.default_rng(7)
+    ids_np = rng.permutation(np.repeat(np.arange(8), counts)).astype(np.int32).reshape(T, 1)
+    wts_np = rng.uniform(0.5, 1.5, size=(T, 1)).astype(np.float32)
+    w = synthetic.make_weights(cfg, 40, device=cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, 40).to(cuda)
+    ids, wts = torch.from_numpy(ids_np).to(cuda), torch.from_numpy(wts_np).to(cuda)
+    m = ops.blockwise_mapping(ids=ids, n_experts=8, block_size=256)
+    tpid, b2e = m["token_position_to_id"], m["block_to_expert"]
+    NB = tpid.numel()
+    xq, xs = ops.act_quant(x)
+    tiles, num, mx = ops.build_block_tiles(tpid, b2e, 256, T, 1, 8, 1)
+    rows = sorted(tiles[:4 * int(num.item())].cpu().numpy().reshape(-1, 4)[:, 2].tolist())
+    assert {(r - 1) // 64 for r in rows} == {0, 1, 2, 3}, rows
+    hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mx)
+    y = ops.expert_down_block(hq, hs, w, T, NB, tiles, num, mx)
+    out = ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, 1)
+    q13, s13, q2, s2 = oracle_weights(w, None)
+    ref = moe_sparse_fp8(np_f32(x), ids_np, wts_np, q13, s13, q2, s2, shared=oracle_shared(w))
+    err = rel_l2(np_f32(out), ref)
+    say("tile heights rel_l2", err)
+    assert err <= TOL_REL_L2, err

@@ -21,11 +21,11 @@ void set_error(const char* fn, const char* fmt, ...) {
 
 void clear_error() { g_err[0] = 0; }
 
-// Rows per expert tile: the average routed rows per expert, rounded up to the
-// next supported MFMA tile height.
+// Rows per expert tile: 16 up to 8 routed rows per expert on average (measured
+// ahead of 32-row tiles there), else the next supported MFMA tile height.
 static int choose_mt(int T, int K, int E) {
   long avg = ((long)T * std::min(K, E) + E - 1) / E;
-  if (avg <= 16) return 16;
+  if (avg <= 8) return 16;
   if (avg <= 32) return 32;
   if (avg <= 64) return 64;
   return 128;
@@ -56,12 +56,13 @@ struct LayerWs {
   size_t bytes;
 };
 
-// The 256x256 ("block") kernels take over above 12 rows per expert on average:
-// measured on the DeepSeek-V3 and Kimi-K2 layers they lose to 16-row tiles at 8
-// rows (+23%) and beat every row-tile height from 16 rows on (5% at 16, 20-40%
-// at 32-64 rows).
+// The 256x256 ("block") kernels take over above 20 rows per expert on average.
+// Expert GEMM time on the DeepSeek-V3 and Kimi-K2 layers: 16-row tiles are best
+// up to 8 rows, 32-row tiles from 10 to 16 rows (3-6 % ahead of the block
+// kernels), the two are level at 20 rows and the block kernels lead from 24 rows
+// on (5-25 % at 24-32 rows).
 static bool use_block(int T, int K, int E) {
-  return ((long)T * std::min(K, E) + E - 1) / E > 12;
+  return ((long)T * std::min(K, E) + E - 1) / E > 20;
 }
 
 static inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }

@@ -82,50 +82,47 @@ __device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base)
 // groups of the 64-bank LDS (two 128-byte rows span the banks once).
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
-template <int KIND>
-__global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs p) {
-  // Pipeline stages as distinct objects, so the compiler can tell that fragment
-  // reads of one stage do not alias the direct-to-LDS loads in flight into another.
-  __shared__ __attribute__((aligned(16))) uint8_t sTA0[kStageA];  // A tile of stage 0
-  __shared__ __attribute__((aligned(16))) uint8_t sTB0[kStageB];  // B tile of stage 0
-  __shared__ __attribute__((aligned(16))) uint8_t sTA1[kStageA];
-  __shared__ __attribute__((aligned(16))) uint8_t sTB1[kStageB];
-  __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageSA];  // A scales of stage 0's block
-  __shared__ __attribute__((aligned(16))) uint8_t sA1[kStageSA];
-  __shared__ __attribute__((aligned(16))) float sR0[2 * kBM];  // scale ratio per (half, row)
-  __shared__ __attribute__((aligned(16))) float sR1[2 * kBM];
-  __shared__ __attribute__((aligned(16))) float sLast[2 * kBM];  // last block scale
-  __shared__ int sSrc[kBM];
-  __shared__ float sRed[2][kBM];
-  __shared__ float sW[2][kMaxKB];  // weight block scales of the two column halves
+// The workgroup's LDS, allocated once by the kernel. The pipeline stages are
+// distinct objects, so the compiler can tell that fragment reads of one stage do
+// not alias the direct-to-LDS loads in flight into another.
+struct BlkLds {
+  uint8_t *ta0, *tb0, *ta1, *tb1;  // A and B tiles of stages 0 and 1
+  uint8_t *sa0, *sa1;              // A scales of each stage's block
+  float *r0, *r1;                  // scale ratio per (half, row) of each stage
+  float* last;                     // last block scale per (half, row)
+  int* src;                        // token (gate_up) or slot (down) of each tile row
+  float (*red)[kBM];               // row amax of the two column halves
+  float (*w)[kMaxKB];              // weight block scales of the two column halves
+};
+
+// One work item: tile rows [slot0, slot0 + nrows) of expert e against column
+// tile nt. MF is the number of 16-row fragments per wave: the four row groups
+// hold 16 * MF rows each, so a tile of up to 64 * MF rows keeps all eight waves
+// (two per SIMD) busy and its MFMA, ratio and fragment-read work scales with MF.
+template <int KIND, int MF>
+__device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, const int e,
+                                           const long slot0, const int nrows, const int nt) {
+  uint8_t* const sTA0 = s.ta0;
+  uint8_t* const sTB0 = s.tb0;
+  uint8_t* const sTA1 = s.ta1;
+  uint8_t* const sTB1 = s.tb1;
+  uint8_t* const sA0 = s.sa0;
+  uint8_t* const sA1 = s.sa1;
+  float* const sR0 = s.r0;
+  float* const sR1 = s.r1;
+  float* const sLast = s.last;
+  int* const sSrc = s.src;
+  float(*const sRed)[kBM] = s.red;
+  float(*const sW)[kMaxKB] = s.w;
+  constexpr int RG = 16 * MF;  // rows per row group
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   // Row group wm, column half wn. Waves run on SIMD wave % 4, so the two column
-  // halves of a row group sit on different SIMDs and a tile of up to 128 rows
-  // keeps all four SIMDs busy.
+  // halves of a row group sit on different SIMDs.
   const int wm = wave >> 1, wn = wave & 1;
   const int Kdim = (KIND == 0) ? p.H : p.I;
   const int KB = Kdim / kBK;
-  const int NT = (KIND == 0) ? p.I / 128 : p.H / kBN;
-
-  // XCD-aware item index: workgroup b runs on XCD b % 8; XCD x takes the
-  // contiguous item range [x * per, (x + 1) * per).
-  const int count = p.num_tiles[0] * NT;
-  const int per = (count + 7) / 8;
-  const int jx = blockIdx.x >> 3;
-  if (jx >= per) return;
-  const int L = (blockIdx.x & 7) * per + jx;
-  if (L >= count) return;
-  const int2 sg = p.seg[L / NT];
-  const int r0 = L - NT * sg.x;
-  const int nt = r0 / sg.y;
-  const int tile = sg.x + (r0 - nt * sg.y);
-  if (tile >= p.num_tiles[0]) return;  // truncated tile list
-  const int4 td = p.tiles[tile];
-  const int e = td.x, nrows = td.z;
-  const long slot0 = td.y;
-  if (e < 0 || e >= p.E + p.nsh) return;
   const bool is_sh = e >= p.E;
   const int ej = is_sh ? e - p.E : e;
 
@@ -220,21 +217,21 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     }
   };
 
-  // Accumulators: 4 row tiles (16 rows) x 8 column tiles (16 columns).
-  v4f acc[4][8];
+  // Accumulators: MF row tiles (16 rows) x 8 column tiles (16 columns).
+  v4f acc[MF][8];
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int m = 0; m < MF; ++m)
 #pragma unroll
     for (int n = 0; n < 8; ++n) acc[m][n] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  const bool active = 64 * wm < nrows;  // this wave's 64 rows hold at least one row
+  const bool active = RG * wm < nrows;  // this wave's row group holds at least one row
   const int g = lane >> 4, l16 = lane & 15;
   // Fragment reads. Every fragment starts at a 16-aligned row, so row l16 of it
   // has swizzle (l16 >> 1) & 7 whatever the tile: a fragment is one per-lane
   // offset (f_lo / f_hi) plus a constant, and the reads use immediate offsets.
   const uint32_t f_lo = l16 * kBK + ((g ^ ((l16 >> 1) & 7)) << 4);
   const uint32_t f_hi = l16 * kBK + (((g + 4) ^ ((l16 >> 1) & 7)) << 4);
-  const uint32_t a_wave = 64 * wm * kBK;
+  const uint32_t a_wave = RG * wm * kBK;
   // B rows of this wave's eight 16-column tiles. gate_up: tiles 0-3 gate columns
   // [64 wn, +64), tiles 4-7 the matching up columns; down: columns [128 wn, +128).
   const uint32_t b_wave = (KIND == 0 ? 64 * wn : 128 * wn) * kBK;
@@ -248,12 +245,12 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   auto compute = [&](const uint8_t* sa, const uint8_t* sb, const float* sr) {
     const uint8_t* ta = sa + a_wave;
     const uint8_t* tb = sb + b_wave;
-    v8i a[4];
-    v4f rr[4];  // ratios of the column half in use: gate, then up (gate_up)
+    v8i a[MF];
+    v4f rr[MF];  // ratios of the column half in use: gate, then up (gate_up)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < MF; ++m) {
       a[m] = frag(ta + 16 * m * kBK);
-      rr[m] = *(const v4f*)&sr[((KIND == 0) ? 0 : wn) * kBM + 64 * wm + 16 * m + 4 * g];
+      rr[m] = *(const v4f*)&sr[((KIND == 0) ? 0 : wn) * kBM + RG * wm + 16 * m + 4 * g];
     }
     // B fragments double-buffered: the reads of column tile n + 1 are issued
     // before the MFMAs of tile n, so LDS latency hides under them.
@@ -263,9 +260,9 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
       v8i bn = b;
       if (n + 1 < 8) bn = frag(tb + brow0(n + 1) * kBK);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
+      for (int m = 0; m < MF; ++m) {
         const v4f c = acc[m][n] * rr[m];
-        if (KIND == 0 && n == 3) rr[m] = *(const v4f*)&sr[kBM + 64 * wm + 16 * m + 4 * g];
+        if (KIND == 0 && n == 3) rr[m] = *(const v4f*)&sr[kBM + RG * wm + 16 * m + 4 * g];
         acc[m][n] = mfma16_fp8_acc(a[m], b, c);
       }
       b = bn;
@@ -274,12 +271,12 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     // next to its first use): the A, ratio and first B reads; then per column
     // tile the next tile's B reads and four (4 ratio multiplies, 1 MFMA) pairs;
     // gate_up reads the up-half ratios once the gate-half ones are used.
-    __builtin_amdgcn_sched_group_barrier(0x100, 8 + 4 + 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 3 * MF + 2, 0);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       if (n + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
+      for (int m = 0; m < MF; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
         if (KIND == 0 && n == 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -338,10 +335,10 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     // group combines the two column-half waves through LDS.
     const int GI = p.I / 128;
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < MF; ++m)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = 64 * wm + 16 * m + 4 * g + i;
+        const int row = RG * wm + 16 * m + 4 * g + i;
         const float sg_ = sLast[row], su = sLast[kBM + row];
         float mx = 0.f;
 #pragma unroll
@@ -359,10 +356,10 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     if (active) {
       // codes of local row r (0..63), h column c (0..63) at stg[r * 64 + c]
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
+      for (int m = 0; m < MF; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int lr = 16 * m + 4 * g + i, row = 64 * wm + lr;
+          const int lr = 16 * m + 4 * g + i, row = RG * wm + lr;
           const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
 #pragma unroll
           for (int n = 0; n < 4; ++n) {
@@ -374,8 +371,8 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
         }
       wave_lds_sync();
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = lane + 64 * j, lr = c >> 2, ch = c & 3, row = 64 * wm + lr;
+      for (int j = 0; j < MF; ++j) {
+        const int c = lane + 64 * j, lr = c >> 2, ch = c & 3, row = RG * wm + lr;
         if (row < nrows && sSrc[row] >= 0)
           *(int4*)(p.hq + (size_t)(slot0 + row) * p.I + nt * 128 + 64 * wn + 16 * ch) = *(const int4*)(stg + lr * 64 + 16 * ch);
       }
@@ -384,22 +381,66 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
     // bf16 of local row r (0..63), column c (0..127) at stg[(r * 128 + c) * 2]
     uint16_t* const stg16 = (uint16_t*)stg;
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < MF; ++m)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int lr = 16 * m + 4 * g + i;
-        const float sl = sLast[wn * kBM + 64 * wm + lr];
+        const float sl = sLast[wn * kBM + RG * wm + lr];
 #pragma unroll
         for (int n = 0; n < 8; ++n) stg16[lr * 128 + 16 * n + l16] = f32_to_bf16_bits(acc[m][n][i] * sl);
       }
     wave_lds_sync();
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int c = lane + 64 * j, lr = c >> 4, ch = c & 15, row = 64 * wm + lr;
+    for (int j = 0; j < 4 * MF; ++j) {
+      const int c = lane + 64 * j, lr = c >> 4, ch = c & 15, row = RG * wm + lr;
       if (row < nrows)
         *(int4*)(p.y + (size_t)(slot0 + row) * p.H + nt * kBN + 128 * wn + 8 * ch) = *(const int4*)(stg + lr * 256 + 16 * ch);
     }
   }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs p) {
+  __shared__ __attribute__((aligned(16))) uint8_t sTA0[kStageA];
+  __shared__ __attribute__((aligned(16))) uint8_t sTB0[kStageB];
+  __shared__ __attribute__((aligned(16))) uint8_t sTA1[kStageA];
+  __shared__ __attribute__((aligned(16))) uint8_t sTB1[kStageB];
+  __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageSA];
+  __shared__ __attribute__((aligned(16))) uint8_t sA1[kStageSA];
+  __shared__ __attribute__((aligned(16))) float sR0[2 * kBM];
+  __shared__ __attribute__((aligned(16))) float sR1[2 * kBM];
+  __shared__ __attribute__((aligned(16))) float sLast[2 * kBM];
+  __shared__ int sSrc[kBM];
+  __shared__ float sRed[2][kBM];
+  __shared__ float sW[2][kMaxKB];
+  const BlkLds s{sTA0, sTB0, sTA1, sTB1, sA0, sA1, sR0, sR1, sLast, sSrc, sRed, sW};
+
+  // XCD-aware item index: workgroup b runs on XCD b % 8; XCD x takes the
+  // contiguous item range [x * per, (x + 1) * per).
+  const int NT = (KIND == 0) ? p.I / 128 : p.H / kBN;
+  const int count = p.num_tiles[0] * NT;
+  const int per = (count + 7) / 8;
+  const int jx = blockIdx.x >> 3;
+  if (jx >= per) return;
+  const int L = (blockIdx.x & 7) * per + jx;
+  if (L >= count) return;
+  const int2 sg = p.seg[L / NT];
+  const int r0 = L - NT * sg.x;
+  const int nt = r0 / sg.y;
+  const int tile = sg.x + (r0 - nt * sg.y);
+  if (tile >= p.num_tiles[0]) return;  // truncated tile list
+  const int4 td = p.tiles[tile];
+  const int e = td.x, nrows = td.z;
+  if (e < 0 || e >= p.E + p.nsh || nrows <= 0) return;
+  // Row groups sized to the tile (workgroup-uniform branch).
+  if (nrows > 192)
+    block_item<KIND, 4>(p, s, e, td.y, nrows, nt);
+  else if (nrows > 128)
+    block_item<KIND, 3>(p, s, e, td.y, nrows, nt);
+  else if (nrows > 64)
+    block_item<KIND, 2>(p, s, e, td.y, nrows, nt);
+  else
+    block_item<KIND, 1>(p, s, e, td.y, nrows, nt);
 }
 
 // ---------------------------------------------------------------------------
