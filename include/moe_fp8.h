@@ -241,6 +241,15 @@ int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E, int K, int
  * counterpart: it pins the gfx950 fp8 MFMA data layout for the tests. */
 int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, int shape, void* stream);
 
+/* For every fp32 bit pattern u in [first, first + count) (u < 2^31) whose value
+ * v has |v| <= 448: the e4m3fn codes of v and -v from the gfx950 conversion
+ * instruction against the integer round-to-nearest-even encoder. Writes
+ * out[0..blocks) = mismatch counts and out[blocks..2*blocks) = the smallest
+ * mismatching pattern per workgroup (0xffffffff if none). No reference
+ * counterpart: it pins the hardware encoder the quantizers use. */
+int moe_selftest_fp8_encode(uint32_t first, uint32_t count, uint32_t* out, int blocks,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

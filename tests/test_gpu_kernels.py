@@ -28,6 +28,15 @@ def test_mfma_fp8_fragment_layout(cuda, shape, n):
     assert np.array_equal(c, ai @ bi.T)
 
 
+def test_fp8_conversion_instruction_matches_encoder(cuda):
+    """The quantizers encode with the gfx950 conversion instruction; it equals the
+    integer round-to-nearest-even encoder (the one the oracle's encoder pins through
+    the quantizer tests) on every fp32 value in [-448, 448], both signs."""
+    say("fp8 encode exhaustive")
+    n, first_bad = ops.selftest_fp8_encode()
+    assert n == 0, (n, None if first_bad is None else hex(first_bad))
+
+
 def test_mfma_fp8_wide_range_accumulation(cuda):
     """Full-range random codes: products are exact, but the MFMA's inner sum is not an
     exact fp32 sum; it stays within 1e-3 of the largest |product| sum (measured ~1e-4)."""

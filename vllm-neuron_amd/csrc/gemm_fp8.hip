@@ -250,12 +250,11 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
           const float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
           if (sSrc[row] >= 0) {
             const long slot = slot0 + row;
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-              const int col = nt * 128 + wave * 32 + jj * 16 + r16;
-              const float yv = fminf(fmaxf(acc[ms][jj][i] / sc, -448.0f), 448.0f);
-              p.hq[(size_t)slot * p.I + col] = (uint8_t)f32_to_e4m3fn(yv);
-            }
+            const uint32_t c2 = e4m3x2(fminf(fmaxf(acc[ms][0][i] / sc, -448.0f), 448.0f),
+                                       fminf(fmaxf(acc[ms][1][i] / sc, -448.0f), 448.0f));
+            uint8_t* const hrow = p.hq + (size_t)slot * p.I + nt * 128 + wave * 32 + r16;
+            hrow[0] = (uint8_t)c2;
+            hrow[16] = (uint8_t)(c2 >> 8);
             if (wave == 0 && r16 == 0) p.hs[(size_t)slot * GI + nt] = sc;
           }
         }
@@ -416,6 +415,52 @@ extern "C" int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H,
   a.NB = NB;
   if (launch_gemm<1>(a, max_tiles, mt, (hipStream_t)stream) != MOE_OK)
     MOE_CHECK_ARG(false, "bad mt %d", mt);
+  MOE_API_END();
+}
+
+// Every fp32 bit pattern u in [first, first + count) with |value| <= 448, both
+// signs: the conversion instruction against the integer encoder. Workgroup b
+// writes its mismatch count to out[b] and its smallest mismatching pattern (or
+// 0xffffffff) to out[gridDim.x + b].
+__global__ __launch_bounds__(256) void selftest_fp8_encode_kernel(uint32_t first, uint32_t count,
+                                                                  uint32_t* out) {
+  __shared__ uint32_t s_n[256], s_min[256];
+  uint32_t n = 0, mn = 0xffffffffu;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const uint32_t u = first + i;
+    const float v = __uint_as_float(u & 0x7fffffffu);
+    if (!(v <= 448.0f)) continue;
+    const uint32_t hw = e4m3x2(v, -v);
+    const uint32_t sw = f32_to_e4m3fn(v) | (f32_to_e4m3fn(-v) << 8);
+    if (hw != sw) {
+      ++n;
+      mn = min(mn, u);
+    }
+  }
+  s_n[threadIdx.x] = n;
+  s_min[threadIdx.x] = mn;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      s_n[threadIdx.x] += s_n[threadIdx.x + o];
+      s_min[threadIdx.x] = min(s_min[threadIdx.x], s_min[threadIdx.x + o]);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[blockIdx.x] = s_n[0];
+    out[gridDim.x + blockIdx.x] = s_min[0];
+  }
+}
+
+extern "C" int moe_selftest_fp8_encode(uint32_t first, uint32_t count, uint32_t* out, int blocks,
+                                       void* stream) {
+  MOE_API_BEGIN("moe_selftest_fp8_encode");
+  MOE_CHECK_ARG(out && blocks > 0 && blocks <= 65536, "bad arguments");
+  MOE_CHECK_ARG((uint64_t)first + count <= 0x80000000ull, "range must lie in [0, 2^31)");
+  hipLaunchKernelGGL(selftest_fp8_encode_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     first, count, out);
   MOE_API_END();
 }
 

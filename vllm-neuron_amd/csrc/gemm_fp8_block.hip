@@ -362,9 +362,11 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
           const int lr = 16 * m + 4 * g + i, row = RG * wm + lr;
           const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
 #pragma unroll
-          for (int n = 0; n < 4; ++n) {
-            const float yv = fminf(fmaxf(acc[m][n][i] / sc, -448.0f), 448.0f);
-            stg[lr * 64 + 16 * n + l16] = (uint8_t)f32_to_e4m3fn(yv);
+          for (int n = 0; n < 4; n += 2) {
+            const uint32_t c2 = e4m3x2(fminf(fmaxf(acc[m][n][i] / sc, -448.0f), 448.0f),
+                                       fminf(fmaxf(acc[m][n + 1][i] / sc, -448.0f), 448.0f));
+            stg[lr * 64 + 16 * n + l16] = (uint8_t)c2;
+            stg[lr * 64 + 16 * (n + 1) + l16] = (uint8_t)(c2 >> 8);
           }
           if (wn == 0 && l16 == 0 && row < nrows && sSrc[row] >= 0)
             p.hs[(size_t)(slot0 + row) * GI + nt] = sc;

@@ -50,6 +50,14 @@ __device__ __forceinline__ uint32_t f32_to_e4m3fn(float x) {
   return code | sign;
 }
 
+// Two codes from the gfx950 conversion instruction (v_cvt_pk_fp8_f32: OCP e4m3,
+// round to nearest even): code(a) in bits 0-7, code(b) in bits 8-15. For inputs
+// in [-448, 448] it equals f32_to_e4m3fn bit for bit, which
+// moe_selftest_fp8_encode checks over every fp32 value of that range.
+__device__ __forceinline__ uint32_t e4m3x2(float a, float b) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+
 // ---------------------------------------------------------------------------
 // Deterministic fp32 exp / sigmoid built from individually rounded IEEE ops
 // (no contraction), so the host oracle reproduces them bit for bit:
@@ -120,7 +128,7 @@ __device__ __forceinline__ void quant_pair_1x128(uint32_t pair, uint8_t* q, floa
   const float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
   const float y0 = fminf(fmaxf(v0 / sc, -448.0f), 448.0f);
   const float y1 = fminf(fmaxf(v1 / sc, -448.0f), 448.0f);
-  *(uint16_t*)(q + 2 * lane) = (uint16_t)(f32_to_e4m3fn(y0) | (f32_to_e4m3fn(y1) << 8));
+  *(uint16_t*)(q + 2 * lane) = (uint16_t)e4m3x2(y0, y1);
   if (lane == 0) *s = sc;
 }
 
@@ -135,12 +143,11 @@ __device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t* q, fl
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, MOE_WAVE));
   const float sc = fmaxf(a, 0x1.b7cdfep-34f) / 448.0f;
-  uint32_t lo = 0, hi = 0;
+  float y[8];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    lo |= f32_to_e4m3fn(fminf(fmaxf(v[e] / sc, -448.0f), 448.0f)) << (8 * e);
-    hi |= f32_to_e4m3fn(fminf(fmaxf(v[e + 4] / sc, -448.0f), 448.0f)) << (8 * e);
-  }
+  for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(v[e] / sc, -448.0f), 448.0f);
+  const uint32_t lo = e4m3x2(y[0], y[1]) | (e4m3x2(y[2], y[3]) << 16);
+  const uint32_t hi = e4m3x2(y[4], y[5]) | (e4m3x2(y[6], y[7]) << 16);
   *(uint2*)q = make_uint2(lo, hi);
   if (first) *s = sc;
 }

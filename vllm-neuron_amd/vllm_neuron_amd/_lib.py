@@ -55,6 +55,7 @@ PROTOTYPES = {
     "moe_expert_down_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _p,
                                    _p]),
     "moe_selftest_mfma_fp8": (_i, [_p, _p, _p, _i, _p]),
+    "moe_selftest_fp8_encode": (_i, [ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),
 }
 
 _lock = threading.Lock()

@@ -6,6 +6,7 @@ on the current torch stream. CPU tensors are rejected: there is no CPU path.
 """
 import ctypes
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -321,6 +322,18 @@ def expert_down_block(hq, hs, w, T, NB, tiles, num_tiles, max_tiles):
               ptr(w.shared_w2_scale) if S else None, S, NB, ptr(tiles), ptr(num_tiles),
               max_tiles, ptr(y), _stream())
     return y
+
+
+def selftest_fp8_encode(first=0, count=0x43E00001, blocks=4096, device="cuda"):
+    """(mismatches, smallest mismatching fp32 pattern or None) of the hardware e4m3fn
+    encoder against the integer encoder over fp32 patterns [first, first + count),
+    both signs, values up to 448 (the default range is all of them)."""
+    out = torch.empty(2 * blocks, device=device, dtype=torch.int32)
+    _lib.call("moe_selftest_fp8_encode", first, count, ptr(out), blocks, _stream())
+    r = out.cpu().numpy().view(np.uint32)
+    n = int(r[:blocks].astype(np.int64).sum())
+    mn = int(r[blocks:].min())
+    return n, (None if mn == 0xFFFFFFFF else mn)
 
 
 def selftest_mfma(a, b, shape=0):
