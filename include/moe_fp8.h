@@ -250,6 +250,18 @@ int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, int shap
 int moe_selftest_fp8_encode(uint32_t first, uint32_t count, uint32_t* out, int blocks,
                             void* stream);
 
+/* The quantizers divide by a shared scale with one reciprocal and a correction
+ * step; this compares it with the IEEE division: equal e4m3 codes of the clamped
+ * quotients, and equal fp32 quotients wherever their magnitude is at least 2^-10
+ * (below that both encode to a signed zero). Mode 0:
+ * u in [first, first + count) (u < 2^31) is the pair (bf16 group amax u >> 16,
+ * bf16 value u & 0xffff), used when both are finite and |value| <= amax, with
+ * the quantizer's scale max(amax, 1e-10) / 448 as divisor. Mode 1: u seeds a
+ * random fp32 amax in [2^-40, 2^40) and a value of magnitude at most amax.
+ * Output as moe_selftest_fp8_encode. No reference counterpart. */
+int moe_selftest_quant_div(int mode, uint32_t first, uint32_t count, uint32_t* out, int blocks,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

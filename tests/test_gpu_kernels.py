@@ -37,6 +37,17 @@ def test_fp8_conversion_instruction_matches_encoder(cuda):
     assert n == 0, (n, None if first_bad is None else hex(first_bad))
 
 
+@pytest.mark.parametrize("mode", [0, 1])
+def test_shared_divisor_division_is_correctly_rounded(cuda, mode):
+    """The quantizers' reciprocal-and-correction quotient gives the IEEE division's
+    e4m3 code everywhere and its exact fp32 value wherever the code can be nonzero
+    (|quotient| >= 2^-10): mode 0 on every (bf16 group amax, bf16 value) pair, mode 1
+    on 2^31 random fp32 pairs spanning 80 binades."""
+    say("shared-divisor division", mode)
+    n, first_bad = ops.selftest_quant_div(mode)
+    assert n == 0, (n, None if first_bad is None else hex(first_bad))
+
+
 def test_mfma_fp8_wide_range_accumulation(cuda):
     """Full-range random codes: products are exact, but the MFMA's inner sum is not an
     exact fp32 sum; it stays within 1e-3 of the largest |product| sum (measured ~1e-4)."""

@@ -231,7 +231,8 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) {
             const float gt = acc[ms][jj][i], up = acc[ms][jj + 2][i];
-            const float h = gt / (1.0f + __expf(-gt)) * up;
+            // hardware reciprocal (about 1 ulp): h only feeds the 1x128 fp8 quantization
+            const float h = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
             acc[ms][jj][i] = h;
             m = fmaxf(m, fabsf(h));
           }
@@ -250,8 +251,9 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
           const float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
           if (sSrc[row] >= 0) {
             const long slot = slot0 + row;
-            const uint32_t c2 = e4m3x2(fminf(fmaxf(acc[ms][0][i] / sc, -448.0f), 448.0f),
-                                       fminf(fmaxf(acc[ms][1][i] / sc, -448.0f), 448.0f));
+            const float rs = 1.0f / sc;
+            const uint32_t c2 = e4m3x2(fminf(fmaxf(div_by(acc[ms][0][i], sc, rs), -448.0f), 448.0f),
+                                       fminf(fmaxf(div_by(acc[ms][1][i], sc, rs), -448.0f), 448.0f));
             uint8_t* const hrow = p.hq + (size_t)slot * p.I + nt * 128 + wave * 32 + r16;
             hrow[0] = (uint8_t)c2;
             hrow[16] = (uint8_t)(c2 >> 8);
@@ -452,6 +454,77 @@ __global__ __launch_bounds__(256) void selftest_fp8_encode_kernel(uint32_t first
     out[blockIdx.x] = s_n[0];
     out[gridDim.x + blockIdx.x] = s_min[0];
   }
+}
+
+// div_by against the IEEE division: a mismatch is a different e4m3 code of the
+// clamped quotient, or a different fp32 quotient of magnitude at least 2^-10 (the
+// smallest with a nonzero code; far below it the correction step's residual can
+// underflow, for subnormal values, and the quotient is then only within one ulp).
+// Mode 0: index u in [first, first + count)
+// (u < 2^31) is the pair (bf16 group amax m = u >> 16, bf16 value v = u & 0xffff)
+// of the 1x128 quantizer, skipped unless both are finite and |v| <= m; the
+// divisor is max(m, 1e-10) / 448. Mode 1: index u seeds a random fp32 amax in
+// [2^-40, 2^40) and a random fp32 value of magnitude at most amax. Same output
+// layout as the encoder check.
+__global__ __launch_bounds__(256) void selftest_quant_div_kernel(int mode, uint32_t first,
+                                                                 uint32_t count, uint32_t* out) {
+  __shared__ uint32_t s_n[256], s_min[256];
+  uint32_t n = 0, mn = 0xffffffffu;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const uint32_t u = first + i;
+    float v, m;
+    if (mode == 0) {
+      m = bf16_bits_to_f32((uint16_t)((u >> 16) & 0x7fffu));
+      v = bf16_bits_to_f32((uint16_t)(u & 0xffffu));
+      if (!(fabsf(v) <= m) || !(m < INFINITY)) continue;
+    } else {
+      uint32_t h = u * 0x9E3779B1u;  // integer hash of the index
+      h ^= h >> 15;
+      h *= 0x85EBCA77u;
+      h ^= h >> 13;
+      uint32_t h2 = h * 0xC2B2AE3Du;
+      h2 ^= h2 >> 16;
+      const uint32_t em = 87u + (h % 80u);  // amax exponent field: 2^-40 .. 2^39
+      m = __uint_as_float((em << 23) | (h2 & 0x7fffffu));
+      const uint32_t ev = em - (h2 >> 23) % 40u;  // value up to 39 binades below
+      v = __uint_as_float(((h >> 31) << 31) | (ev << 23) | ((h2 * 0x27d4eb2du) & 0x7fffffu));
+      if (fabsf(v) > m) v = copysignf(m, v);
+    }
+    const float sc = fmaxf(m, 0x1.b7cdfep-34f) / 448.0f;
+    const float rs = 1.0f / sc;
+    const float qi = v / sc, qf = div_by(v, sc, rs);
+    const uint32_t ci = e4m3x2(fminf(fmaxf(qi, -448.0f), 448.0f), 0.f);
+    const uint32_t cf = e4m3x2(fminf(fmaxf(qf, -448.0f), 448.0f), 0.f);
+    if (ci != cf || (fabsf(qi) >= 0x1p-10f && __float_as_uint(qi) != __float_as_uint(qf))) {
+      ++n;
+      mn = min(mn, u);
+    }
+  }
+  s_n[threadIdx.x] = n;
+  s_min[threadIdx.x] = mn;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      s_n[threadIdx.x] += s_n[threadIdx.x + o];
+      s_min[threadIdx.x] = min(s_min[threadIdx.x], s_min[threadIdx.x + o]);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[blockIdx.x] = s_n[0];
+    out[gridDim.x + blockIdx.x] = s_min[0];
+  }
+}
+
+extern "C" int moe_selftest_quant_div(int mode, uint32_t first, uint32_t count, uint32_t* out,
+                                      int blocks, void* stream) {
+  MOE_API_BEGIN("moe_selftest_quant_div");
+  MOE_CHECK_ARG(out && blocks > 0 && blocks <= 65536 && (mode == 0 || mode == 1), "bad arguments");
+  MOE_CHECK_ARG((uint64_t)first + count <= 0x80000000ull, "range must lie in [0, 2^31)");
+  hipLaunchKernelGGL(selftest_quant_div_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     mode, first, count, out);
+  MOE_API_END();
 }
 
 extern "C" int moe_selftest_fp8_encode(uint32_t first, uint32_t count, uint32_t* out, int blocks,

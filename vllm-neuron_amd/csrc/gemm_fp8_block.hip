@@ -344,7 +344,8 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           const float gt = acc[m][n][i] * sg_, up = acc[m][n + 4][i] * su;
-          const float h = gt / (1.0f + __expf(-gt)) * up;
+          // hardware reciprocal (about 1 ulp): h only feeds the 1x128 fp8 quantization
+          const float h = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
           acc[m][n][i] = h;
           mx = fmaxf(mx, fabsf(h));
         }
@@ -361,10 +362,11 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
         for (int i = 0; i < 4; ++i) {
           const int lr = 16 * m + 4 * g + i, row = RG * wm + lr;
           const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
+          const float rs = 1.0f / sc;
 #pragma unroll
           for (int n = 0; n < 4; n += 2) {
-            const uint32_t c2 = e4m3x2(fminf(fmaxf(acc[m][n][i] / sc, -448.0f), 448.0f),
-                                       fminf(fmaxf(acc[m][n + 1][i] / sc, -448.0f), 448.0f));
+            const uint32_t c2 = e4m3x2(fminf(fmaxf(div_by(acc[m][n][i], sc, rs), -448.0f), 448.0f),
+                                       fminf(fmaxf(div_by(acc[m][n + 1][i], sc, rs), -448.0f), 448.0f));
             stg[lr * 64 + 16 * n + l16] = (uint8_t)c2;
             stg[lr * 64 + 16 * (n + 1) + l16] = (uint8_t)(c2 >> 8);
           }

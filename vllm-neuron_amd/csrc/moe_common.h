@@ -58,6 +58,22 @@ __device__ __forceinline__ uint32_t e4m3x2(float a, float b) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 
+// x / d from rd = 1 / d (itself a correctly rounded IEEE division): q = x * rd
+// is within one ulp of x / d, the residual q * d - x is exact under a fused
+// multiply-add while it does not underflow, and one correction step then gives
+// the correctly rounded quotient (Markstein's theorem); zeros keep the sign of x.
+// Three instructions instead of a full division per element when many elements
+// share one divisor. For the quantizers' divisors (at least 1e-10 / 448) every
+// quotient of magnitude 2^-10 or more, the only ones with a nonzero e4m3 code, is
+// correctly rounded; moe_selftest_quant_div checks this, and equal codes, on every
+// (bf16 value, bf16 group amax) pair of the 1x128 quantizer and on random fp32
+// pairs.
+__device__ __forceinline__ float div_by(float x, float d, float rd) {
+  const float q = x * rd;
+  const float r = __builtin_fmaf(q, d, -x);
+  return __builtin_fmaf(-r, rd, q);
+}
+
 // ---------------------------------------------------------------------------
 // Deterministic fp32 exp / sigmoid built from individually rounded IEEE ops
 // (no contraction), so the host oracle reproduces them bit for bit:
@@ -120,14 +136,16 @@ __device__ __forceinline__ float group16_max_f32(float v) {
 // One 1x128 activation quantization group by one wave: lane l holds columns 2l,
 // 2l + 1 (`pair`, two bf16 bit patterns) and writes their codes to q + 2l; lane 0
 // writes the scale. s = max(amax, 1e-10) / 448 and q = RNE_e4m3fn(clamp(x / s,
-// +-448)), both IEEE fp32 divisions, so codes and scales match the oracle bit for bit.
+// +-448)), both correctly rounded fp32 divisions, so codes and scales match the oracle bit
+// for bit.
 __device__ __forceinline__ void quant_pair_1x128(uint32_t pair, uint8_t* q, float* s, int lane) {
   const float v0 = bf16_bits_to_f32((uint16_t)(pair & 0xffffu));
   const float v1 = bf16_bits_to_f32((uint16_t)(pair >> 16));
   const float amax = wave_max_f32(fmaxf(fabsf(v0), fabsf(v1)));
   const float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
-  const float y0 = fminf(fmaxf(v0 / sc, -448.0f), 448.0f);
-  const float y1 = fminf(fmaxf(v1 / sc, -448.0f), 448.0f);
+  const float rs = 1.0f / sc;
+  const float y0 = fminf(fmaxf(div_by(v0, sc, rs), -448.0f), 448.0f);
+  const float y1 = fminf(fmaxf(div_by(v1, sc, rs), -448.0f), 448.0f);
   *(uint16_t*)(q + 2 * lane) = (uint16_t)e4m3x2(y0, y1);
   if (lane == 0) *s = sc;
 }
@@ -135,7 +153,7 @@ __device__ __forceinline__ void quant_pair_1x128(uint32_t pair, uint8_t* q, floa
 // One 1x128 group held by 16 consecutive lanes (a 16-aligned lane segment): each
 // lane holds 8 consecutive values v (bf16 values widened to fp32) and writes their
 // codes as 8 bytes at q; the segment's first lane writes the scale. Same arithmetic
-// as quant_pair_1x128 (exact amax, IEEE divisions), so the codes are identical.
+// as quant_pair_1x128 (exact amax, correctly rounded divisions), so the codes are identical.
 __device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t* q, float* s, bool first) {
   float a = 0.f;
 #pragma unroll
@@ -144,8 +162,9 @@ __device__ __forceinline__ void quant8_1x128(const float (&v)[8], uint8_t* q, fl
   for (int o = 1; o < 16; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, MOE_WAVE));
   const float sc = fmaxf(a, 0x1.b7cdfep-34f) / 448.0f;
   float y[8];
+  const float rs = 1.0f / sc;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(v[e] / sc, -448.0f), 448.0f);
+  for (int e = 0; e < 8; ++e) y[e] = fminf(fmaxf(div_by(v[e], sc, rs), -448.0f), 448.0f);
   const uint32_t lo = e4m3x2(y[0], y[1]) | (e4m3x2(y[2], y[3]) << 16);
   const uint32_t hi = e4m3x2(y[4], y[5]) | (e4m3x2(y[6], y[7]) << 16);
   *(uint2*)q = make_uint2(lo, hi);

@@ -336,6 +336,18 @@ def selftest_fp8_encode(first=0, count=0x43E00001, blocks=4096, device="cuda"):
     return n, (None if mn == 0xFFFFFFFF else mn)
 
 
+def selftest_quant_div(mode, first=0, count=1 << 31, blocks=4096, device="cuda"):
+    """(mismatches, smallest mismatching index or None) of the quantizers' shared-divisor
+    division against the IEEE division: mode 0 over (bf16 amax, bf16 value) pairs,
+    mode 1 over random fp32 pairs (indices [first, first + count) of 2^31)."""
+    out = torch.empty(2 * blocks, device=device, dtype=torch.int32)
+    _lib.call("moe_selftest_quant_div", mode, first, count, ptr(out), blocks, _stream())
+    r = out.cpu().numpy().view(np.uint32)
+    n = int(r[:blocks].astype(np.int64).sum())
+    mn = int(r[blocks:].min())
+    return n, (None if mn == 0xFFFFFFFF else mn)
+
+
 def selftest_mfma(a, b, shape=0):
     """shape 0: a, b [16,128] -> c [16,16] (one 16x16x128 fp8 MFMA);
     shape 1: a, b [32,128] -> c [32,32] (two 32x32x64 fp8 MFMAs)."""
