@@ -250,6 +250,13 @@ int moe_selftest_mfma_fp8(const uint8_t* a, const uint8_t* b, float* c, int shap
 int moe_selftest_fp8_encode(uint32_t first, uint32_t count, uint32_t* out, int blocks,
                             void* stream);
 
+/* For every fp32 bit pattern in [first, first + count) (first + count <= 2^32):
+ * the bf16 conversion instruction the output stages use against the integer
+ * round-to-nearest-even encoder (a NaN has to stay a NaN). Output as
+ * moe_selftest_fp8_encode. No reference counterpart. */
+int moe_selftest_bf16_encode(uint32_t first, uint32_t count, uint32_t* out, int blocks,
+                             void* stream);
+
 /* The quantizers divide by a shared scale with one reciprocal and a correction
  * step; this compares it with the IEEE division: equal e4m3 codes of the clamped
  * quotients, and equal fp32 quotients wherever their magnitude is at least 2^-10

@@ -37,6 +37,16 @@ def test_fp8_conversion_instruction_matches_encoder(cuda):
     assert n == 0, (n, None if first_bad is None else hex(first_bad))
 
 
+@pytest.mark.parametrize("half", [0, 1])
+def test_bf16_conversion_instruction_matches_encoder(cuda, half):
+    """The output stages round to bf16 with the gfx950 conversion instruction; it
+    equals the integer round-to-nearest-even encoder on every fp32 pattern (NaNs
+    stay NaNs), checked in two halves of 2^31 patterns."""
+    say("bf16 encode exhaustive", half)
+    n, first_bad = ops.selftest_bf16_encode(first=half << 31)
+    assert n == 0, (n, None if first_bad is None else hex(first_bad))
+
+
 @pytest.mark.parametrize("mode", [0, 1])
 def test_shared_divisor_division_is_correctly_rounded(cuda, mode):
     """The quantizers' reciprocal-and-correction quotient gives the IEEE division's

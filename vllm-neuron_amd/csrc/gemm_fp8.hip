@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int col = nt * 256 + wave * 64 + j * 16 + r16;
-              p.y[(size_t)slot * p.H + col] = f32_to_bf16_bits(acc[ms][j][i]);
+              p.y[(size_t)slot * p.H + col] = (uint16_t)bf16x2(acc[ms][j][i], 0.f);
             }
           }
         }
@@ -524,6 +524,51 @@ extern "C" int moe_selftest_quant_div(int mode, uint32_t first, uint32_t count, 
   MOE_CHECK_ARG((uint64_t)first + count <= 0x80000000ull, "range must lie in [0, 2^31)");
   hipLaunchKernelGGL(selftest_quant_div_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
                      mode, first, count, out);
+  MOE_API_END();
+}
+
+// Every fp32 bit pattern u in [first, first + count): the bf16 conversion
+// instruction against the integer encoder (a NaN only has to stay a NaN). Same
+// output layout as the e4m3 check.
+__global__ __launch_bounds__(256) void selftest_bf16_encode_kernel(uint32_t first, uint32_t count,
+                                                                   uint32_t* out) {
+  __shared__ uint32_t s_n[256], s_min[256];
+  uint32_t n = 0, mn = 0xffffffffu;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const uint32_t u = first + i;
+    const float v = __uint_as_float(u);
+    const uint32_t hw = bf16x2(v, 0.f) & 0xffffu;
+    const uint32_t sw = f32_to_bf16_bits(v);
+    const bool same = (v != v) ? ((hw & 0x7fffu) > 0x7f80u) : (hw == sw);
+    if (!same) {
+      ++n;
+      mn = min(mn, u);
+    }
+  }
+  s_n[threadIdx.x] = n;
+  s_min[threadIdx.x] = mn;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) {
+      s_n[threadIdx.x] += s_n[threadIdx.x + o];
+      s_min[threadIdx.x] = min(s_min[threadIdx.x], s_min[threadIdx.x + o]);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    out[blockIdx.x] = s_n[0];
+    out[gridDim.x + blockIdx.x] = s_min[0];
+  }
+}
+
+extern "C" int moe_selftest_bf16_encode(uint32_t first, uint32_t count, uint32_t* out, int blocks,
+                                        void* stream) {
+  MOE_API_BEGIN("moe_selftest_bf16_encode");
+  MOE_CHECK_ARG(out && blocks > 0 && blocks <= 65536, "bad arguments");
+  MOE_CHECK_ARG((uint64_t)first + count <= 0x100000000ull, "range must lie in [0, 2^32)");
+  hipLaunchKernelGGL(selftest_bf16_encode_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                     first, count, out);
   MOE_API_END();
 }
 

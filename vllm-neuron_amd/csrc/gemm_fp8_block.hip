@@ -391,7 +391,11 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
         const int lr = 16 * m + 4 * g + i;
         const float sl = sLast[wn * kBM + RG * wm + lr];
 #pragma unroll
-        for (int n = 0; n < 8; ++n) stg16[lr * 128 + 16 * n + l16] = f32_to_bf16_bits(acc[m][n][i] * sl);
+        for (int n = 0; n < 8; n += 2) {
+          const uint32_t b2 = bf16x2(acc[m][n][i] * sl, acc[m][n + 1][i] * sl);
+          stg16[lr * 128 + 16 * n + l16] = (uint16_t)b2;
+          stg16[lr * 128 + 16 * (n + 1) + l16] = (uint16_t)(b2 >> 16);
+        }
       }
     wave_lds_sync();
 #pragma unroll

@@ -26,6 +26,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// Two bf16 from the gfx950 conversion instruction (v_cvt_pk_bf16_f32, round to
+// nearest even): bf16(a) in bits 0-15, bf16(b) in bits 16-31. Equal to
+// f32_to_bf16_bits on every non-NaN fp32 value (and NaN stays NaN), which
+// moe_selftest_bf16_encode checks over all 2^32 patterns.
+typedef __bf16 moe_bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16x2(float a, float b) {
+  const moe_bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // ---------------------------------------------------------------------------
 // OCP float8 e4m3fn encode, round-to-nearest-even. The caller clamps the input
 // to [-448, 448] first (max finite e4m3fn), so no NaN/overflow path is needed.

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(
       uint32_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)f32_to_bf16_bits(v[j][2 * i]) | ((uint32_t)f32_to_bf16_bits(v[j][2 * i + 1]) << 16);
+        w[i] = bf16x2(v[j][2 * i], v[j][2 * i + 1]);
       *(int4*)(res_out + base + 8 * c) = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
     }
     if (OF32) {
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(
       uint32_t w[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)f32_to_bf16_bits(y[2 * i]) | ((uint32_t)f32_to_bf16_bits(y[2 * i + 1]) << 16);
+        w[i] = bf16x2(y[2 * i], y[2 * i + 1]);
       *(int4*)((uint16_t*)out + base + 8 * c) = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
       if (QUANT) {
         float yb[8];

@@ -121,10 +121,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       }
     }
     int4 o;
-    o.x = (int)(f32_to_bf16_bits(acc[0]) | ((uint32_t)f32_to_bf16_bits(acc[1]) << 16));
-    o.y = (int)(f32_to_bf16_bits(acc[2]) | ((uint32_t)f32_to_bf16_bits(acc[3]) << 16));
-    o.z = (int)(f32_to_bf16_bits(acc[4]) | ((uint32_t)f32_to_bf16_bits(acc[5]) << 16));
-    o.w = (int)(f32_to_bf16_bits(acc[6]) | ((uint32_t)f32_to_bf16_bits(acc[7]) << 16));
+    o.x = (int)bf16x2(acc[0], acc[1]);
+    o.y = (int)bf16x2(acc[2], acc[3]);
+    o.z = (int)bf16x2(acc[4], acc[5]);
+    o.w = (int)bf16x2(acc[6], acc[7]);
     *(int4*)(out + (size_t)t * H + c * 8) = o;
   }
 }

@@ -56,6 +56,7 @@ PROTOTYPES = {
                                    _p]),
     "moe_selftest_mfma_fp8": (_i, [_p, _p, _p, _i, _p]),
     "moe_selftest_fp8_encode": (_i, [ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),
+    "moe_selftest_bf16_encode": (_i, [ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),
     "moe_selftest_quant_div": (_i, [_i, ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),
 }
 

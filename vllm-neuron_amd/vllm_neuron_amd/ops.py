@@ -336,6 +336,17 @@ def selftest_fp8_encode(first=0, count=0x43E00001, blocks=4096, device="cuda"):
     return n, (None if mn == 0xFFFFFFFF else mn)
 
 
+def selftest_bf16_encode(first=0, count=1 << 31, blocks=4096, device="cuda"):
+    """(mismatches, smallest mismatching pattern or None) of the hardware bf16 encoder
+    against the integer encoder over fp32 patterns [first, first + count)."""
+    out = torch.empty(2 * blocks, device=device, dtype=torch.int32)
+    _lib.call("moe_selftest_bf16_encode", first, count, ptr(out), blocks, _stream())
+    r = out.cpu().numpy().view(np.uint32)
+    n = int(r[:blocks].astype(np.int64).sum())
+    mn = int(r[blocks:].min())
+    return n, (None if mn == 0xFFFFFFFF else mn)
+
+
 def selftest_quant_div(mode, first=0, count=1 << 31, blocks=4096, device="cuda"):
     """(mismatches, smallest mismatching index or None) of the quantizers' shared-divisor
     division against the IEEE division: mode 0 over (bf16 amax, bf16 value) pairs,
