@@ -161,11 +161,18 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
       const int src = sSrc[row];
       off[i] = (uint32_t)((src >= 0 ? src : 0) * Kdim + swz(row, lane & 7) * 16);
     } else {
+      // Tile row -> weight row. Column tile n of a wave reads tile rows 16 n + j,
+      // and they hold output columns 4 j + n (gate_up, per 64-column wave half) or
+      // 8 j + n (down, per 128-column half): lane j then holds consecutive output
+      // columns and stores them directly (4 fp8 codes or 8 bf16 values).
       int wrow;
-      if (KIND == 0)
-        wrow = (row < 128) ? nt * 128 + row : p.I + nt * 128 + (row - 128);
-      else
-        wrow = nt * kBN + row;
+      if (KIND == 0) {
+        const int r = row & 127;
+        const int hc = (r & 64) + 4 * (r & 15) + ((r >> 4) & 3);
+        wrow = (row < 128) ? nt * 128 + hc : p.I + nt * 128 + hc;
+      } else {
+        wrow = nt * kBN + (row & 128) + 8 * (row & 15) + ((row >> 4) & 7);
+      }
       off[i] = (uint32_t)(wrow * Kdim + swz(row, lane & 7) * 16);
     }
   }
@@ -318,18 +325,9 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   (shalf ? sLast + kBM : sLast)[srow] = s_prev;
   __syncthreads();
 
-  // Accumulator layout (16x16): lane l, register i holds D[4*(l/16) + i][l%16].
-  // Each wave stages its output block in LDS (16 KB: stage array wave / 2, half
-  // wave % 2; the stages are free once every wave passed the barrier above) and
-  // writes it back in 16-byte row chunks: scattered 1- and 2-byte stores of the
-  // accumulator layout cost more than the whole K loop.
-  uint8_t* const stg = ((wave >> 1) == 0 ? sTA0 : (wave >> 1) == 1 ? sTB0 : (wave >> 1) == 2 ? sTA1 : sTB1) +
-                       (wave & 1) * 16384;
-  auto wave_lds_sync = [] {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  };
+  // Accumulator layout (16x16): lane l, register i holds D[4*(l/16) + i][l%16];
+  // with the tile's weight-row order, acc[m][n][i] of lane l is output column
+  // 4 (l % 16) + n (gate_up, n < 4) or 8 (l % 16) + n (down) of the wave's half.
   if (KIND == 0) {
     // h = SiLU(gate) * up for this wave's 64 h columns; the row amax of the 1x128
     // group combines the two column-half waves through LDS.
@@ -355,55 +353,37 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
       }
     __syncthreads();
     if (active) {
-      // codes of local row r (0..63), h column c (0..63) at stg[r * 64 + c]
 #pragma unroll
       for (int m = 0; m < MF; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int lr = 16 * m + 4 * g + i, row = RG * wm + lr;
+          const int row = RG * wm + 16 * m + 4 * g + i;
           const float sc = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), 0x1.b7cdfep-34f) / 448.0f;
           const float rs = 1.0f / sc;
+          float y[4];
 #pragma unroll
-          for (int n = 0; n < 4; n += 2) {
-            const uint32_t c2 = e4m3x2(fminf(fmaxf(div_by(acc[m][n][i], sc, rs), -448.0f), 448.0f),
-                                       fminf(fmaxf(div_by(acc[m][n + 1][i], sc, rs), -448.0f), 448.0f));
-            stg[lr * 64 + 16 * n + l16] = (uint8_t)c2;
-            stg[lr * 64 + 16 * (n + 1) + l16] = (uint8_t)(c2 >> 8);
+          for (int n = 0; n < 4; ++n) y[n] = fminf(fmaxf(div_by(acc[m][n][i], sc, rs), -448.0f), 448.0f);
+          const uint32_t c4 = e4m3x2(y[0], y[1]) | (e4m3x2(y[2], y[3]) << 16);
+          if (row < nrows && sSrc[row] >= 0) {
+            *(uint32_t*)(p.hq + (size_t)(slot0 + row) * p.I + nt * 128 + 64 * wn + 4 * l16) = c4;
+            if (wn == 0 && l16 == 0) p.hs[(size_t)(slot0 + row) * GI + nt] = sc;
           }
-          if (wn == 0 && l16 == 0 && row < nrows && sSrc[row] >= 0)
-            p.hs[(size_t)(slot0 + row) * GI + nt] = sc;
         }
-      wave_lds_sync();
-#pragma unroll
-      for (int j = 0; j < MF; ++j) {
-        const int c = lane + 64 * j, lr = c >> 2, ch = c & 3, row = RG * wm + lr;
-        if (row < nrows && sSrc[row] >= 0)
-          *(int4*)(p.hq + (size_t)(slot0 + row) * p.I + nt * 128 + 64 * wn + 16 * ch) = *(const int4*)(stg + lr * 64 + 16 * ch);
-      }
     }
   } else if (active) {
-    // bf16 of local row r (0..63), column c (0..127) at stg[(r * 128 + c) * 2]
-    uint16_t* const stg16 = (uint16_t*)stg;
 #pragma unroll
     for (int m = 0; m < MF; ++m)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int lr = 16 * m + 4 * g + i;
-        const float sl = sLast[wn * kBM + RG * wm + lr];
-#pragma unroll
-        for (int n = 0; n < 8; n += 2) {
-          const uint32_t b2 = bf16x2(acc[m][n][i] * sl, acc[m][n + 1][i] * sl);
-          stg16[lr * 128 + 16 * n + l16] = (uint16_t)b2;
-          stg16[lr * 128 + 16 * (n + 1) + l16] = (uint16_t)(b2 >> 16);
-        }
+        const int row = RG * wm + 16 * m + 4 * g + i;
+        const float sl = sLast[wn * kBM + row];
+        int4 o;
+        o.x = (int)bf16x2(acc[m][0][i] * sl, acc[m][1][i] * sl);
+        o.y = (int)bf16x2(acc[m][2][i] * sl, acc[m][3][i] * sl);
+        o.z = (int)bf16x2(acc[m][4][i] * sl, acc[m][5][i] * sl);
+        o.w = (int)bf16x2(acc[m][6][i] * sl, acc[m][7][i] * sl);
+        if (row < nrows) *(int4*)(p.y + (size_t)(slot0 + row) * p.H + nt * kBN + 128 * wn + 8 * l16) = o;
       }
-    wave_lds_sync();
-#pragma unroll
-    for (int j = 0; j < 4 * MF; ++j) {
-      const int c = lane + 64 * j, lr = c >> 4, ch = c & 15, row = RG * wm + lr;
-      if (row < nrows)
-        *(int4*)(p.y + (size_t)(slot0 + row) * p.H + nt * kBN + 128 * wn + 8 * ch) = *(const int4*)(stg + lr * 256 + 16 * ch);
-    }
   }
 }
 
