@@ -1,4 +1,6 @@
 // 1x128 fp8 activation quantization and the weighted unpermute-combine.
+#include <type_traits>
+
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -61,8 +63,8 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __re
 // one workgroup per token, 8 bf16 (16 B) per thread per step.
 // One workgroup per (token, column chunk). The token's live rows are listed in
 // slot order (ballot compaction, so the order and the fp32 sums are the same as a
-// sequential scan), then each thread sums its 8 columns over the rows, eight rows
-// of loads at a time.
+// sequential scan), then each thread sums its 8 columns over the rows, with the
+// loads of up to eight rows in flight.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const int32_t* __restrict__ inv,
                                                       const float* __restrict__ w, int S, int T,
@@ -100,26 +102,29 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-    for (int r0 = 0; r0 < n; r0 += 8) {
-      // Eight rows in flight; rows past n reload row n - 1 and are not accumulated
-      // (unconditional loads keep the compiler's wait counts exact).
-      int4 v[8];
+    // Rows r0 .. r0 + NR - 1, all NR loads in flight, then summed in row order.
+    auto rows = [&](auto nr, int r0) {
+      constexpr int NR = decltype(nr)::value;
+      int4 v[NR];
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
-        v[q] = *(const int4*)(y + (size_t)s_row[min(r0 + q, n - 1)] * H + c * 8);
+      for (int q = 0; q < NR; ++q) v[q] = *(const int4*)(y + (size_t)s_row[r0 + q] * H + c * 8);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        if (r0 + q < n) {  // workgroup-uniform
-          const float wt = s_w[r0 + q];
-          const uint32_t u[4] = {(uint32_t)v[q].x, (uint32_t)v[q].y, (uint32_t)v[q].z, (uint32_t)v[q].w};
+      for (int q = 0; q < NR; ++q) {
+        const float wt = s_w[r0 + q];
+        const uint32_t u[4] = {(uint32_t)v[q].x, (uint32_t)v[q].y, (uint32_t)v[q].z, (uint32_t)v[q].w};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc[2 * i] += wt * bf16_bits_to_f32((uint16_t)(u[i] & 0xffffu));
-            acc[2 * i + 1] += wt * bf16_bits_to_f32((uint16_t)(u[i] >> 16));
-          }
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += wt * bf16_bits_to_f32((uint16_t)(u[i] & 0xffffu));
+          acc[2 * i + 1] += wt * bf16_bits_to_f32((uint16_t)(u[i] >> 16));
         }
       }
-    }
+    };
+    // Groups of 8, then 4, 2 and 1 rows (workgroup-uniform counts, no repeated loads).
+    int r0 = 0;
+    for (; r0 + 8 <= n; r0 += 8) rows(std::integral_constant<int, 8>{}, r0);
+    if (n - r0 >= 4) { rows(std::integral_constant<int, 4>{}, r0); r0 += 4; }
+    if (n - r0 >= 2) { rows(std::integral_constant<int, 2>{}, r0); r0 += 2; }
+    if (n - r0 >= 1) rows(std::integral_constant<int, 1>{}, r0);
     int4 o;
     o.x = (int)bf16x2(acc[0], acc[1]);
     o.y = (int)bf16x2(acc[2], acc[3]);
