@@ -162,10 +162,9 @@ extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E,
     moe::set_error(_moe_fn, "%s", saved);                      \
     return rc;                                                 \
   }
-  MOE_STEP(moe_router_logits(x_bf16, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
-                             w.router_ws_bytes, stream));
-  MOE_STEP(moe_router_topk(logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
-                           renorm_eps, routed_scale, ids, wts, nullptr, stream));
+  MOE_STEP(router_logits_topk(x_bf16, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+                              w.router_ws_bytes, corr_bias, K, order, scoring, n_group, topk_group,
+                              renorm, renorm_eps, routed_scale, ids, wts, stream));
   // The mapping's scan kernel also writes the expert tile list, from the counts.
   const bool block = use_block(T, K, E);
   const int mbt = block ? moe_max_block_tiles(T, K, E, N, B, n_shared) : 0;

@@ -22,6 +22,15 @@ inline int router_logits_splits(int T, int H, int E) {
   return (int)std::max(1L, std::min(ks, kmax));
 }
 
+// moe_router_logits followed by moe_router_topk (no affinities output), with the
+// split-K reduce folded into the top-k kernel; for callers that already checked
+// the arguments of both.
+int router_logits_topk(const void* x_bf16, const void* w_bf16, const float* bias, int T, int H,
+                       int E, float* logits, void* workspace, size_t workspace_bytes,
+                       const float* corr_bias, int K, int order, int scoring, int n_group,
+                       int topk_group, int renorm, float renorm_eps, float routed_scale,
+                       int32_t* ids, float* weights, void* stream);
+
 // Rows per tile of the 256x256 expert GEMM kernels.
 constexpr int kBlockTileRows = 256;
 

@@ -228,7 +228,9 @@ template <int PM>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ corr_bias, int T, int E, int K,
     int order, int scoring, int n_group, int topk_group, int renorm, float eps, float scale,
-    int32_t* __restrict__ ids, float* __restrict__ weights, float* __restrict__ aff) {
+    int32_t* __restrict__ ids, float* __restrict__ weights, float* __restrict__ aff,
+    const float* __restrict__ part, int ksplit, const float* __restrict__ lbias,
+    float* __restrict__ logits_out) {
   __shared__ float s_act[4][PM * 64];
   __shared__ float s_key[4][PM * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -240,10 +242,45 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   const bool need_act = order != MOE_ORDER_TOPK_ACT;
 
   float lg[PM];
+  if (part == nullptr) {
 #pragma unroll
-  for (int j = 0; j < PM; ++j) {
-    int e = lane + 64 * j;
-    lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
+    for (int j = 0; j < PM; ++j) {
+      int e = lane + 64 * j;
+      lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
+    }
+  } else {
+    // Split-K partials [ksplit, T, E] summed here, in split order and then + bias,
+    // exactly as router_logits_reduce does; the sums are also written to logits_out.
+    constexpr int Q = (PM >= 8) ? 2 : 8;
+    const size_t TE = (size_t)T * E;
+    float sum[PM];
+#pragma unroll
+    for (int j = 0; j < PM; ++j) sum[j] = 0.f;
+    for (int k0 = 0; k0 < ksplit; k0 += Q) {
+      float v[Q][PM];
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int j = 0; j < PM; ++j) {
+          const int e = lane + 64 * j;
+          v[q][j] = (j < P && e < E) ? part[(size_t)min(k0 + q, ksplit - 1) * TE + (size_t)t * E + e] : 0.f;
+        }
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+        if (k0 + q < ksplit)
+#pragma unroll
+          for (int j = 0; j < PM; ++j) sum[j] += v[q][j];
+    }
+#pragma unroll
+    for (int j = 0; j < PM; ++j) {
+      const int e = lane + 64 * j;
+      if (j < P && e < E) {
+        lg[j] = (lbias != nullptr) ? sum[j] + lbias[e] : sum[j];
+        if (logits_out != nullptr) logits_out[(size_t)t * E + e] = lg[j];
+      } else {
+        lg[j] = NEG_INF;
+      }
+    }
   }
 
   if (need_act) {
@@ -502,7 +539,7 @@ extern "C" int moe_router_topk(const float* logits, const float* corr_bias, int 
 #define MOE_TOPK_LAUNCH(PMV)                                                                   \
   hipLaunchKernelGGL(router_topk_kernel<PMV>, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, \
                      logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,     \
-                     renorm_eps, routed_scale, ids, weights, affinities)
+                     renorm_eps, routed_scale, ids, weights, affinities, nullptr, 0, nullptr, nullptr)
   if (P <= 1)
     MOE_TOPK_LAUNCH(1);
   else if (P <= 2)
@@ -514,5 +551,67 @@ extern "C" int moe_router_topk(const float* logits, const float* corr_bias, int 
   else
     MOE_TOPK_LAUNCH(kTopkMaxP);
 #undef MOE_TOPK_LAUNCH
+  MOE_API_END();
+}
+
+// Router logits and top-k for the layer: with a split-K logits product the top-k
+// kernel sums the partials itself (same order and values as router_logits_reduce,
+// written to logits), one launch fewer than moe_router_logits + moe_router_topk.
+// Arguments are those of the two entry points, already checked by the caller.
+int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float* bias, int T, int H,
+                            int E, float* logits, void* workspace, size_t workspace_bytes,
+                            const float* corr_bias, int K, int order, int scoring, int n_group,
+                            int topk_group, int renorm, float renorm_eps, float routed_scale,
+                            int32_t* ids, float* weights, void* stream) {
+  int ks = router_logits_splits(T, H, E);
+  const int kchunk = ((H / 64 + ks - 1) / ks) * 64;
+  ks = (H + kchunk - 1) / kchunk;
+  if (ks == 1 || T == 0 || E > kTopkMaxE || workspace == nullptr ||
+      workspace_bytes < (size_t)ks * T * E * sizeof(float)) {
+    int rc = moe_router_logits(x_bf16, w_bf16, bias, T, H, E, logits, workspace, workspace_bytes,
+                               stream);
+    if (rc != MOE_OK) return rc;
+    return moe_router_topk(logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
+                           renorm_eps, routed_scale, ids, weights, nullptr, stream);
+  }
+  MOE_API_BEGIN("moe_layer_forward (router)");
+  // The checks of moe_router_logits and moe_router_topk.
+  MOE_CHECK_ARG(x_bf16 && w_bf16 && logits && ids && weights, "null pointer argument");
+  MOE_CHECK_ARG(T > 0 && H > 0 && H % 64 == 0 && E > 0, "bad sizes T=%d H=%d E=%d", T, H, E);
+  MOE_CHECK_ARG(((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)w_bf16 & 15) == 0,
+                "x and w must be 16-byte aligned");
+  MOE_CHECK_ARG(K >= 1 && K <= E && K <= 64, "top_k must be in [1, min(E, 64)], got %d", K);
+  MOE_CHECK_ARG(order >= MOE_ORDER_TOPK_ACT && order <= MOE_ORDER_GROUPED, "bad order %d", order);
+  MOE_CHECK_ARG(scoring == MOE_SCORING_SOFTMAX || scoring == MOE_SCORING_SIGMOID,
+                "bad scoring %d", scoring);
+  if (order == MOE_ORDER_GROUPED) {
+    MOE_CHECK_ARG(n_group >= 1 && n_group <= 64 && E % n_group == 0,
+                  "n_group must divide E and be <= 64 (E=%d, n_group=%d)", E, n_group);
+    MOE_CHECK_ARG(topk_group >= 1 && topk_group <= n_group, "bad topk_group %d", topk_group);
+    MOE_CHECK_ARG((long)topk_group * (E / n_group) >= K,
+                  "topk_group * group size must be >= top_k");
+  }
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  const long tiles = (long)((T + 63) / 64) * ((E + 63) / 64) * ks;
+  hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)(((tiles + 7) / 8) * 8)), dim3(256), 0, st,
+                     (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E, kchunk, ks,
+                     part);
+  const int P = (E + 63) / 64;
+#define MOE_TOPK_FUSED(PMV)                                                                       \
+  hipLaunchKernelGGL(router_topk_kernel<PMV>, dim3((T + 3) / 4), dim3(256), 0, st, nullptr, corr_bias, \
+                     T, E, K, order, scoring, n_group, topk_group, renorm, renorm_eps,             \
+                     routed_scale, ids, weights, nullptr, part, ks, bias, logits)
+  if (P <= 1)
+    MOE_TOPK_FUSED(1);
+  else if (P <= 2)
+    MOE_TOPK_FUSED(2);
+  else if (P <= 4)
+    MOE_TOPK_FUSED(4);
+  else if (P <= 8)
+    MOE_TOPK_FUSED(8);
+  else
+    MOE_TOPK_FUSED(kTopkMaxP);
+#undef MOE_TOPK_FUSED
   MOE_API_END();
 }
