@@ -103,7 +103,9 @@ def test_act_quant_bit_exact(cuda, R_, C, offset):
     assert np.array_equal(np_f32(s), os_)
 
 
-@pytest.mark.parametrize("T,H,E", [(64, 1024, 8), (64, 7168, 256), (300, 5120, 160), (1, 7168, 384)])
+@pytest.mark.parametrize("T,H,E", [(64, 1024, 8), (64, 7168, 256), (300, 5120, 160), (1, 7168, 384),
+                                   # wide tiles (T >= 2048, 128 <= E <= 256), ragged last tile
+                                   (2100, 1024, 128), (4096, 7168, 256), (2048, 5120, 160)])
 def test_router_logits_close(cuda, T, H, E):
     say("router_logits", T, H, E)
     g = torch.Generator().manual_seed(T + H + E)

@@ -131,6 +131,142 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-T form: one workgroup holds 128 tokens x all E experts, so x is read
+// once per (token tile, K chunk) instead of once per 64-expert tile, and the
+// router rows once per 128 tokens. E / (16 EF) waves; wave w owns experts
+// [16 EF w, +16 EF) for the 128 tokens (8 x EF MFMA tiles). K advances 128 per
+// iteration (four 32-long sub-steps) in ascending order for every accumulator;
+// same lane layout as router_logits_kernel. Partials [ks, T, E] as there.
+// ---------------------------------------------------------------------------
+template <int EF>
+__global__ __launch_bounds__(1024) void router_logits_wide_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const float* __restrict__ bias, int T, int H, int E, int kchunk, int ks,
+    float* __restrict__ out) {
+  constexpr int KW = 128, LDX = KW + 8;
+  __shared__ __attribute__((aligned(16))) uint16_t sx[128][LDX];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nthreads = blockDim.x;
+  // Tiles numbered token tile fastest within a K chunk; XCD x runs the contiguous
+  // range [x per, (x + 1) per), so its workgroups share the K chunk's router rows.
+  const int nrt = (T + 127) / 128;
+  const long total = (long)nrt * ks;
+  const long per = (total + 7) / 8;
+  const long L = (long)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (L >= total) return;  // whole workgroup
+  const int kz = (int)(L / nrt), rt = (int)(L % nrt);
+  const int t0 = rt * 128;
+  const int k_begin = kz * kchunk, k_end = min(H, k_begin + kchunk);
+  const int g = lane >> 4, r16 = lane & 15;
+
+  const uint16_t* wrow[EF];
+#pragma unroll
+  for (int n = 0; n < EF; ++n) wrow[n] = w + (size_t)(wave * 16 * EF + n * 16 + r16) * H;
+
+  v4f acc[8][EF];
+#pragma unroll
+  for (int m = 0; m < 8; ++m)
+#pragma unroll
+    for (int n = 0; n < EF; ++n) acc[m][n] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  for (int k0 = k_begin; k0 < k_end; k0 += KW) {
+    // x tile: 128 rows x 128 columns = 2048 16-byte chunks (at least 512 threads).
+    int4 xv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = tid + c * nthreads;
+      const int row = idx >> 4, col = (idx & 15) * 8;
+      const int tr = min(t0 + row, T - 1);  // rows past T load row T-1 and are zeroed
+      xv[c] = (idx < 2048) ? *(const int4*)(x + (size_t)tr * H + k0 + col) : make_int4(0, 0, 0, 0);
+      if (t0 + row >= T) xv[c] = make_int4(0, 0, 0, 0);
+    }
+    v8bf b[EF][4];
+#pragma unroll
+    for (int n = 0; n < EF; ++n)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) b[n][q] = *(const v8bf*)(wrow[n] + k0 + q * 32 + g * 8);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = tid + c * nthreads;
+      if (idx < 2048) *(int4*)&sx[idx >> 4][(idx & 15) * 8] = xv[c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const v8bf a = *(const v8bf*)&sx[m * 16 + r16][q * 32 + g * 8];
+#pragma unroll
+        for (int n = 0; n < EF; ++n)
+          acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[n][q], acc[m][n], 0, 0, 0);
+      }
+    __syncthreads();
+  }
+  float* o = out + (size_t)kz * T * E;
+#pragma unroll
+  for (int n = 0; n < EF; ++n) {
+    const int e = wave * 16 * EF + n * 16 + r16;
+    const float bv = (bias != nullptr && ks == 1) ? bias[e] : 0.f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + m * 16 + g * 4 + i;
+        if (t < T) o[(size_t)t * E + e] = acc[m][n][i] + bv;
+      }
+  }
+}
+
+// Launch plan of the logits product: the wide form for many tokens (E a multiple
+// of 16 in [128, 256], one wave per 16 experts; H a multiple of 128), else 64 x 64
+// tiles. ks K chunks give at least about 256 wide (or 1024 small) workgroups.
+struct RouterPlan {
+  bool wide;
+  int ef;  // experts per wave / 16 (wide form)
+  int ks;
+  int kchunk;
+};
+
+static RouterPlan router_plan(int T, int H, int E) {
+  RouterPlan pl{};
+  const int ef = 1;  // waves of 16 experts: 8 to 16 waves (128 registers per lane at 16)
+  pl.wide = T >= 2048 && H % 128 == 0 && E % 16 == 0 && E >= 128 && E <= 256;
+  if (pl.wide) {
+    pl.ef = ef;
+    const int nrt = (T + 127) / 128;
+    const int ks = std::max(1, std::min((256 + nrt - 1) / nrt, H / 512));
+    pl.kchunk = ((H / 128 + ks - 1) / ks) * 128;
+  } else {
+    const int ks = router_logits_splits(T, H, E);
+    pl.kchunk = ((H / 64 + ks - 1) / ks) * 64;
+  }
+  pl.ks = (H + pl.kchunk - 1) / pl.kchunk;
+  return pl;
+}
+
+// The logits product into out (ks == 1: the logits with bias) or into the
+// partials [ks, T, E].
+static void launch_router_logits(const RouterPlan& pl, const void* x_bf16, const void* w_bf16,
+                                 const float* bias, int T, int H, int E, float* out,
+                                 hipStream_t st) {
+  if (pl.wide) {
+    const long tiles = (long)((T + 127) / 128) * pl.ks;
+    const dim3 grid((unsigned)(((tiles + 7) / 8) * 8));
+    const dim3 block((unsigned)(64 * (E / (16 * pl.ef))));
+#define MOE_WIDE(EFV)                                                                              \
+  hipLaunchKernelGGL(router_logits_wide_kernel<EFV>, grid, block, 0, st, (const uint16_t*)x_bf16, \
+                     (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk, pl.ks, out)
+    MOE_WIDE(1);
+#undef MOE_WIDE
+  } else {
+    const long tiles = (long)((T + 63) / 64) * ((E + 63) / 64) * pl.ks;
+    hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)(((tiles + 7) / 8) * 8)), dim3(256), 0,
+                       st, (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E,
+                       pl.kchunk, pl.ks, out);
+  }
+}
+
 __global__ void router_logits_reduce(const float* __restrict__ part, const float* __restrict__ bias,
                                      int T, int E, int ksplit, float* __restrict__ out) {
   size_t n = (size_t)T * E;
@@ -483,24 +619,18 @@ extern "C" int moe_router_logits(const void* x_bf16, const void* w_bf16, const f
                 "x and w must be 16-byte aligned");
   if (T == 0) return MOE_OK;
   hipStream_t st = (hipStream_t)stream;
-  int ks = router_logits_splits(T, H, E);
-  int kchunk = ((H / 64 + ks - 1) / ks) * 64;
-  ks = (H + kchunk - 1) / kchunk;
-  const long tiles = (long)((T + 63) / 64) * ((E + 63) / 64) * ks;
-  const dim3 grid((unsigned)(((tiles + 7) / 8) * 8));
-  if (ks == 1) {
-    hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, st, (const uint16_t*)x_bf16,
-                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, ks, logits);
+  const RouterPlan pl = router_plan(T, H, E);
+  if (pl.ks == 1) {
+    launch_router_logits(pl, x_bf16, w_bf16, bias, T, H, E, logits, st);
   } else {
-    size_t need = (size_t)ks * T * E * sizeof(float);
+    size_t need = (size_t)pl.ks * T * E * sizeof(float);
     MOE_CHECK_ARG(workspace != nullptr && workspace_bytes >= need,
                   "workspace too small: need %zu bytes", need);
     float* part = (float*)workspace;
-    hipLaunchKernelGGL(router_logits_kernel, grid, dim3(256), 0, st, (const uint16_t*)x_bf16,
-                       (const uint16_t*)w_bf16, bias, T, H, E, kchunk, ks, part);
+    launch_router_logits(pl, x_bf16, w_bf16, bias, T, H, E, part, st);
     size_t n = (size_t)T * E;
     int blocks = (int)std::min<size_t>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(router_logits_reduce, dim3(blocks), dim3(256), 0, st, part, bias, T, E, ks,
+    hipLaunchKernelGGL(router_logits_reduce, dim3(blocks), dim3(256), 0, st, part, bias, T, E, pl.ks,
                        logits);
   }
   MOE_API_END();
@@ -508,10 +638,13 @@ extern "C" int moe_router_logits(const void* x_bf16, const void* w_bf16, const f
 
 extern "C" size_t moe_router_logits_workspace_bytes(int T, int H, int E) {
   if (T <= 0 || H <= 0 || E <= 0 || H % 64) return 0;
-  int ks = router_logits_splits(T, H, E);
-  int kchunk = ((H / 64 + ks - 1) / ks) * 64;
-  ks = (H + kchunk - 1) / kchunk;
-  return ks > 1 ? (size_t)ks * T * E * sizeof(float) : 0;
+  // Covers both products: the bf16 one (this plan) and the fp32 one (64 x 64 tiles).
+  const RouterPlan pl = router_plan(T, H, E);
+  int ks32 = router_logits_splits(T, H, E);
+  const int kc32 = ((H / 64 + ks32 - 1) / ks32) * 64;
+  ks32 = (H + kc32 - 1) / kc32;
+  const int ks = std::max(pl.ks > 1 ? pl.ks : 0, ks32 > 1 ? ks32 : 0);
+  return (size_t)ks * T * E * sizeof(float);
 }
 
 extern "C" int moe_router_topk(const float* logits, const float* corr_bias, int T, int E, int K,
@@ -563,9 +696,8 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
                             const float* corr_bias, int K, int order, int scoring, int n_group,
                             int topk_group, int renorm, float renorm_eps, float routed_scale,
                             int32_t* ids, float* weights, void* stream) {
-  int ks = router_logits_splits(T, H, E);
-  const int kchunk = ((H / 64 + ks - 1) / ks) * 64;
-  ks = (H + kchunk - 1) / kchunk;
+  const RouterPlan pl = router_plan(T, H, E);
+  const int ks = pl.ks;
   if (ks == 1 || T == 0 || E > kTopkMaxE || workspace == nullptr ||
       workspace_bytes < (size_t)ks * T * E * sizeof(float)) {
     int rc = moe_router_logits(x_bf16, w_bf16, bias, T, H, E, logits, workspace, workspace_bytes,
@@ -593,10 +725,7 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
   }
   hipStream_t st = (hipStream_t)stream;
   float* part = (float*)workspace;
-  const long tiles = (long)((T + 63) / 64) * ((E + 63) / 64) * ks;
-  hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)(((tiles + 7) / 8) * 8)), dim3(256), 0, st,
-                     (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E, kchunk, ks,
-                     part);
+  launch_router_logits(pl, x_bf16, w_bf16, bias, T, H, E, part, st);
   const int P = (E + 63) / 64;
 #define MOE_TOPK_FUSED(PMV)                                                                       \
   hipLaunchKernelGGL(router_topk_kernel<PMV>, dim3((T + 3) / 4), dim3(256), 0, st, nullptr, corr_bias, \
