@@ -121,6 +121,23 @@ def test_layer_row_tile_heights_agree(cuda):
     assert rel_l2(np_f32(ref), np_f32(outs[0])) < 5e-3
 
 
+@pytest.mark.parametrize("T,E", [(64, 64), (4096, 128)])
+def test_layer_router_matches_op_path(cuda, T, E):
+    """Inside the layer the top-k kernel sums the router's split-K partials itself (28
+    partials at 64 tokens; 8 from the 128-token wide tiles at 4096). Logits, ids and
+    weights equal, bit for bit, those of ops.router_logits (reduce kernel) followed by
+    ops.router_topk."""
+    cfg = PRESETS["dsv3"].with_(n_experts=E, intermediate=128, n_group=8, topk_group=4)
+    say("layer router vs op path", T, E)
+    w = synthetic.make_weights(cfg, 30 + E, device=cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, 30 + E).to(cuda)
+    _, ids, wts, lg = ops.layer_forward(x, w, cfg, return_routing=True)
+    lg2 = ops.router_logits(x, w.router_w, w.router_bias)
+    ids2, wts2 = ops.router_topk(lg2, cfg.top_k, ops.ORDER_GROUPED, cfg.scoring, cfg.n_group,
+                                 cfg.topk_group, w.corr_bias, cfg.renorm, 1e-20, cfg.routed_scaling)
+    assert torch.equal(lg, lg2) and torch.equal(ids, ids2) and torch.equal(wts, wts2)
+
+
 def test_layer_deterministic_and_module_api(cuda):
     cfg = PRESETS["small"]
     say("layer determinism")
