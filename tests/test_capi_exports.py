@@ -44,6 +44,39 @@ def test_block_formula_and_sizes_match_oracle():
     assert lib.moe_max_tiles(64, 8, 256, 257, 256, 1, 16) >= 64 * 8 // 16
 
 
+def _splits_small(T, H, E):
+    """Split count of the 64 x 64-tile products (bf16 below the wide-tile sizes, and
+    always the fp32 product): about 1024 workgroups, at least 256 columns per chunk."""
+    base = -(-T // 64) * -(-E // 64)
+    ks = max(1, min(-(-1024 // base), max(1, H // 256)))
+    kchunk = -(-(H // 64) // ks) * 64
+    return -(-H // kchunk)
+
+
+def _splits_wide(T, H):
+    """Split count of the 128-token wide tiles: about 256 workgroups, K chunks of at
+    least 512 columns in steps of 128."""
+    nrt = -(-T // 128)
+    ks = max(1, min(-(-256 // nrt), H // 512))
+    kchunk = -(-(H // 128) // ks) * 128
+    return -(-H // kchunk)
+
+
+@pytest.mark.parametrize("T,H,E", [(64, 7168, 256), (8192, 7168, 256), (2048, 7168, 128),
+                                   (4096, 5120, 160), (16384, 7168, 384), (2100, 1024, 128)])
+def test_router_workspace_covers_both_products(T, H, E):
+    """moe_router_logits_workspace_bytes sizes the split-K partials of whichever
+    product runs: the bf16 one (wide tiles from 2048 tokens for 128 <= E <= 256) and
+    the fp32 one (always 64 x 64 tiles), which share the query."""
+    from vllm_neuron_amd import _lib
+    lib = _lib.load()
+    wide = T >= 2048 and H % 128 == 0 and E % 16 == 0 and 128 <= E <= 256
+    ks_bf16 = _splits_wide(T, H) if wide else _splits_small(T, H, E)
+    ks_f32 = _splits_small(T, H, E)
+    need = max(k for k in (ks_bf16, ks_f32, 0) if k != 1) * T * E * 4
+    assert lib.moe_router_logits_workspace_bytes(T, H, E) == need
+
+
 def test_argument_errors_raise_reference_exception_types():
     from vllm_neuron_amd import _lib
     lib = _lib.load()
