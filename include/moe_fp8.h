@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MOE_FP8_ABI_VERSION 1
+#define MOE_FP8_ABI_VERSION 2
 
 /* status codes */
 #define MOE_OK 0
@@ -147,9 +147,12 @@ int moe_act_quant_1x128(const void* x_bf16, int rows, int cols, uint8_t* q, floa
 
 /* ---- expert row tiles ---------------------------------------------------- */
 
-/* A tile is {expert, first slot, rows, 0} (int32 x4): at most `mt` consecutive
- * slots of one block of token_position_to_id; shared experts j < n_shared get
- * tiles over slots [N*B + j*T, N*B + (j+1)*T) with expert id E + j. */
+/* A tile is {expert, first slot, rows, first row} (int32 x4): at most `mt`
+ * consecutive slots of one block of token_position_to_id; shared experts
+ * j < n_shared get tiles over slots [N*B + j*T, N*B + (j+1)*T) with expert id
+ * E + j. "first row" is the row of hq / hs / y the tile's first slot uses; the
+ * tile builders here set it to the slot itself, so these buffers have
+ * N*B + n_shared*T rows. */
 int moe_max_tiles(int T, int K, int E, int N, int B, int n_shared, int mt);
 int moe_build_tiles(const int32_t* token_position_to_id, const int32_t* block_to_expert, int N,
                     int B, int T, int E, int n_shared, int mt, int32_t* tiles, int max_tiles,
@@ -178,7 +181,7 @@ int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int
                     void* stream);
 
 /* Prefill-sized variants ("block" kernels): one workgroup computes 256 slots
- * of one expert x 256 weight rows with 32x32x64 fp8 MFMA tiles, both operands
+ * of one expert x 256 weight rows with 16x16x128 fp8 MFMA tiles, both operands
  * staged through LDS. Their tile list holds up to 256 consecutive slots of one
  * expert per tile: `tiles` is max_tiles * 24 bytes (int32x4 tiles followed by
  * int32x2 {first tile, tile count} of each tile's expert), built by
@@ -215,22 +218,36 @@ int moe_combine(const void* y_bf16, const int32_t* inv, const float* w, int S, i
 
 /* ---- whole layer --------------------------------------------------------- */
 
-/* router -> top-k -> mapping -> act quant -> gate_up -> down -> combine.
+/* [residual add ->] [RMSNorm ->] router -> top-k -> mapping -> act quant ->
+ * gate_up -> down -> combine, on one stream.
+ *   gamma [H] fp32 (NULL: no norm, x is already normalized): the layer's own
+ *     pre-MoE RMSNorm over the first hidden_actual columns (<= 0: all H), as
+ *     moe_rms_norm; the router and the experts read the normalized bf16 rows.
+ *     GptOssExperts.forward_prefill normalizes first (model_bf16.py:1359) and
+ *     forward_decode passes the norm weight as gamma to moe_block_tkg
+ *     (model_bf16.py:1276, moe_block_tkg.py:135-151).
+ *   residual [T,H] bf16 (optional, needs gamma) is added first; the bf16 sum
+ *     goes to residual_out [T,H], the (out, residual_sum) form of the MXFP4
+ *     layer (model_mxfp4.py:1362-1377, :1584-1609).
  * ids/weights/logits outputs are optional (NULL to skip). The layer forward of
  * the reference MoE block (GptOssExperts.forward, model_bf16.py:1221-1232 ->
  * forward_prefill :1347-1484 / forward_decode :1309-1345; fused decode
- * moe_block_tkg.py:306-591) with DeepSeek-style fp8-blockwise experts. */
-size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, int n_shared, int B);
-int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E, int K, int n_shared,
-                      const void* router_w_bf16, const float* router_bias,
+ * moe_block_tkg.py:306-591) with DeepSeek-style fp8-blockwise experts.
+ * The workspace holds the expert rows compacted: T*min(K,E) routed rows plus
+ * n_shared*T shared rows of h and y (norm != 0 adds T*H*2 bytes of normalized
+ * rows). */
+size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, int n_shared, int B, int norm);
+int moe_layer_forward(const void* x_bf16, const void* residual_bf16, const float* gamma,
+                      float eps, int hidden_actual, int T, int H, int I, int E, int K,
+                      int n_shared, const void* router_w_bf16, const float* router_bias,
                       const float* corr_bias, int order, int scoring, int n_group,
                       int topk_group, int renorm, float renorm_eps, float routed_scale,
                       const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
                       const float* w2_scale, const uint8_t* w13_shared,
                       const float* w13_shared_scale, const uint8_t* w2_shared,
-                      const float* w2_shared_scale, int B, void* out_bf16, int32_t* ids_out,
-                      float* weights_out, float* logits_out, void* workspace,
-                      size_t workspace_bytes, void* stream);
+                      const float* w2_shared_scale, int B, void* out_bf16,
+                      void* residual_out_bf16, int32_t* ids_out, float* weights_out,
+                      float* logits_out, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- diagnostics ----------------------------------------------------------- */
 

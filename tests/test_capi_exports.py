@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.moe_abi_version() == 1
+    assert lib.moe_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_block_formula_and_sizes_match_oracle():
@@ -40,7 +40,11 @@ def test_block_formula_and_sizes_match_oracle():
                        (16384, 8, 384, 256), (4096, 8, 160, 256), (5, 1, 6, 1), (3, 4, 2, 7)]:
         assert lib.moe_num_blocks(T, K, E, B) == num_blocks(T, K, E, B)
     assert lib.moe_mapping_workspace_bytes(64, 256) > 0
-    assert lib.moe_layer_workspace_bytes(64, 7168, 2048, 256, 8, 1, 256) > 0
+    # hq / y hold only the routed and shared rows: DeepSeek-V3 decode 64 needs
+    # 64 * 8 + 64 rows, about 12 MB in all (the padded slot space would need ~1 GB)
+    ws = lib.moe_layer_workspace_bytes(64, 7168, 2048, 256, 8, 1, 256, 0)
+    assert 0 < ws < 16 << 20, ws
+    assert lib.moe_layer_workspace_bytes(64, 7168, 2048, 256, 8, 1, 256, 1) >= ws + 64 * 7168 * 2
     assert lib.moe_max_tiles(64, 8, 256, 257, 256, 1, 16) >= 64 * 8 // 16
 
 
@@ -98,9 +102,19 @@ def test_argument_errors_raise_reference_exception_types():
     assert rc == _lib.MOE_ERR_ARG and b"257" in lib.moe_last_error()
     rc = lib.moe_expert_gate_up(p, p, 4, 100, 256, 4, p, p, None, None, 0, p, 0, p, p, 1, 16, p, p, None)
     assert rc == _lib.MOE_ERR_ARG and b"multiples of 128" in lib.moe_last_error()
-    rc = lib.moe_layer_forward(p, 4, 7168, 2048, 256, 8, 1, p, None, None, 2, 1, 8, 4, 1, 1e-20,
-                               2.5, p, p, p, p, p, p, p, p, 256, p, None, None, None, p, 1, None)
+    rc = lib.moe_layer_forward(p, None, None, 1e-6, 0, 4, 7168, 2048, 256, 8, 1, p, None, None, 2,
+                               1, 8, 4, 1, 1e-20, 2.5, p, p, p, p, p, p, p, p, 256, p, None, None,
+                               None, None, p, 1, None)
     assert rc == _lib.MOE_ERR_ARG and b"workspace too small" in lib.moe_last_error()
+    # the residual add lives in the norm: a residual without gamma is refused
+    rc = lib.moe_layer_forward(p, p, None, 1e-6, 0, 4, 7168, 2048, 256, 8, 1, p, None, None, 2,
+                               1, 8, 4, 1, 1e-20, 2.5, p, p, p, p, p, p, p, p, 256, p, p, None,
+                               None, None, p, 1 << 30, None)
+    assert rc == _lib.MOE_ERR_ARG and b"residual needs gamma" in lib.moe_last_error()
+    # activation operands beyond 32-bit byte offsets are refused by the block kernels
+    rc = lib.moe_expert_down_block(p, p, 4, 7168, 2048, 256, p, p, None, None, 0, 1 << 21, p, p,
+                                   1, p, None)
+    assert rc == _lib.MOE_ERR_UNSUPPORTED and b"exceeds 4 GiB" in lib.moe_last_error()
 
 
 def test_ops_reject_cpu_tensors():

@@ -99,3 +99,33 @@ def test_moe_block_tkg_unsupported_options():
         M.moe_block_tkg(x, g, wr, gu, dn, hidden_act_fn=M.ActFnType.Swish)
     with pytest.raises(NotImplementedError):   # 2 local experts of 4 routed
         M.moe_block_tkg(x, g, torch.zeros(256, 4, dtype=torch.bfloat16), gu, dn)
+
+
+def test_converted_weight_cache_follows_its_sources():
+    """The reference-layout conversion is cached per source tensor; when the source is
+    freed the entry goes with it, so new weights of the same shape (possibly at the same
+    address) are converted afresh instead of hitting another tensor's entry."""
+    import gc
+
+    from vllm_neuron_amd.functional.moe import _experts
+    _experts._CACHE.clear()
+    E, H, I = 2, 256, 128
+
+    def make(seed):
+        gg = torch.Generator().manual_seed(seed)
+        gu = (torch.randn(E, H, 2, I, generator=gg) * 20).to(FP8)
+        dn = (torch.randn(E, I, H, generator=gg) * 20).to(FP8)
+        return gu, dn
+
+    for seed in range(4):
+        gu, dn = make(seed)
+        w13, _, w2, _ = _experts.routed_weights(gu, dn)
+        ref13 = gu.view(torch.uint8).permute(0, 2, 3, 1).reshape(E, 2 * I, H)
+        assert torch.equal(w13.view(torch.uint8), ref13)
+        assert torch.equal(w2.view(torch.uint8), dn.view(torch.uint8).transpose(1, 2))
+        assert len(_experts._CACHE) == 1
+        # a second call with the same live tensors is a cache hit
+        assert _experts.routed_weights(gu, dn)[0] is w13
+        del gu, dn, w13, w2
+        gc.collect()
+        assert len(_experts._CACHE) == 0

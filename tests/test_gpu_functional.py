@@ -180,6 +180,35 @@ def test_router_bf16_computation(cuda):
     assert np.array_equal(np_f32(aff), bf16_round(R.scatter_dense(ids, wts, E)))
 
 
+@pytest.mark.parametrize("with_gamma", [False, True])
+def test_router_fp16_computation(cuda, with_gamma):
+    """computation_dtype float16: hidden states, the RMSNorm output and the bf16 router
+    weights are rounded to fp16 before the fp32-accumulated product (router.py:236,
+    :419-424, :681-688); logits and affinities come back in fp16, and the selection
+    made from the returned logits is the oracle's."""
+    say("router fp16 computation dtype", with_gamma)
+    g = torch.Generator().manual_seed(6)
+    T, H, E, K = 64, 512, 32, 4
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(cuda)
+    w_param = (0.05 * torch.randn(E, H, generator=g)).to(torch.bfloat16).to(cuda)
+    bias = (0.1 * torch.randn(E, generator=g)).to(cuda)
+    gamma = (1 + 0.1 * torch.randn(H, generator=g)).to(cuda) if with_gamma else None
+    aff, lg = M.router(x, w_param.t(), K, router_bias=bias, return_logits=True, gamma=gamma,
+                       computation_dtype=torch.float16)
+    assert aff.dtype == torch.float16 and lg.dtype == torch.float16
+    xs = np_f32(x.half())
+    if with_gamma:
+        xs = np_f32(torch.from_numpy(R.rms_norm(xs, np_f32(gamma), 1e-6)).half())
+    w16 = np_f32(w_param.half())
+    ref_lg = np_f32(torch.from_numpy(R.router_logits(xs, w16, np_f32(bias.half()))).half())
+    lgf = np_f32(lg)
+    # fp16 output rounding dominates the fp32 summation-order differences
+    assert np.allclose(lgf, ref_lg, rtol=2 ** -10, atol=2 ** -14)
+    ids, wts = R.route_topk_act(lgf, K, R.SOFTMAX)
+    ref_aff = np_f32(torch.from_numpy(R.scatter_dense(ids, wts, E)).half())
+    assert np.array_equal(np_f32(aff), ref_aff)
+
+
 # ---------------------------------------------------------------- mapping / experts
 
 def test_build_blockwise_mapping_api(cuda):

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import np_f32, oracle_shared, oracle_weights, rel_l2, say
+from _util import np_f32, np_u8, oracle_shared, oracle_weights, rel_l2, say
 from oracle import router as R
 from oracle.moe import bf16_round, moe_sparse_fp8
 from vllm_neuron_amd import FP8BlockMoE, MoEConfig, PRESETS, ops, synthetic
@@ -151,8 +151,10 @@ def test_layer_deterministic_and_module_api(cuda):
     pos[50:] = 0                                    # padding after the last real position
     c = layer(x, positions=pos, is_decode=False)
     assert torch.equal(c[:50], a[:50]) and torch.all(c[50:] == 0)
+    # rank (the tensor-parallel rank) does not change the result with every expert local
+    assert torch.equal(layer(x, None, True, torch.tensor([1])), a)
     with pytest.raises(NotImplementedError):
-        layer(x, None, False, torch.tensor([1]))
+        layer(x, None, False, None, rsag_dispatch=True)
 
 
 def _big_weights(cfg, idx, cuda):
@@ -163,13 +165,92 @@ def _big_weights(cfg, idx, cuda):
 def test_layer_dsv3_full_size(cuda, T, idx, tokens):
     """DeepSeek-V3 layer (256 experts + 1 shared): decode 64 and prefill 8192 tokens.
     Outputs are per token, so the oracle checks a token subset (only their experts are
-    dequantized on the host); routing is checked bit-exact for every token."""
+    dequantized on the host), plus the tokens in the last slot of experts whose last
+    256-row tiles cover every 64-row band; routing is checked bit-exact for every token."""
     cfg = PRESETS["dsv3"]
     say("layer dsv3 full", T)
     w = _big_weights(cfg, idx, cuda)
     x = synthetic.hidden_states(T, cfg.hidden, idx).to(cuda)
+    ids = ops.layer_forward(x, w, cfg, return_routing=True)[1].cpu().numpy()
+    tokens, experts = _tile_tokens(ids, cfg.n_experts, extra=tokens)
+    say("dsv3 tokens", tokens, "experts", experts)
     _check_layer(cfg, w, x, tokens=tokens, tag=f"dsv3 T={T}")
     del w
+    torch.cuda.empty_cache()
+
+
+def test_dsv3_prefill_every_row_of_chosen_experts(cuda):
+    """DeepSeek-V3 prefill (8192 tokens) through the block kernels: every slot row of y
+    (the unweighted expert outputs) of several whole experts against the oracle's expert
+    MLP on the same fp8 operands: experts whose second 256-row tile is partial (1-64 and
+    65-128 rows), the most loaded one, one below 256 rows, and the shared expert's last
+    two tiles. The same routing through the row-tile kernels (128-row tiles) agrees
+    with the block kernels on the whole layer output."""
+    from oracle.fp8 import dequant_act_1x128, dequant_weight_128x128, quant_act_1x128
+    from oracle.moe import expert_mlp
+    cfg = PRESETS["dsv3"]
+    T, E, K, B = 8192, cfg.n_experts, cfg.top_k, cfg.block_size
+    say("dsv3 prefill every row", T)
+    w = _big_weights(cfg, 2, cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, 2).to(cuda)
+    lg = ops.router_logits(x, w.router_w, w.router_bias)
+    ids, wts = ops.router_topk(lg, K, ops.ORDER_GROUPED, cfg.scoring, cfg.n_group, cfg.topk_group,
+                               w.corr_bias, cfg.renorm, 1e-20, cfg.routed_scaling)
+    m = ops.blockwise_mapping(ids=ids, n_experts=E, block_size=B)
+    tpid, b2e = m["token_position_to_id"], m["block_to_expert"]
+    NB = tpid.numel()
+    xq, xs = ops.act_quant(x)
+    tiles, num, mbt = ops.build_block_tiles(tpid, b2e, B, T, K, E, 1)
+    hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mbt)
+    y = ops.expert_down_block(hq, hs, w, T, NB, tiles, num, mbt)
+    out_blk = ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, 1)
+    counts = m["expert_counts"].cpu().numpy()
+    tp = tpid.cpu().numpy()
+    b2 = b2e.cpu().numpy()
+    picks = []
+    for lo, hi in ((256, 320), (320, 384)):
+        band = np.nonzero((counts > lo) & (counts <= hi))[0]
+        if band.size:
+            picks.append(int(band[0]))
+    picks.append(int(np.argmax(counts)))
+    small = np.nonzero((counts > 0) & (counts < 256))[0]
+    if small.size:
+        picks.append(int(small[0]))
+    picks = list(dict.fromkeys(picks))
+    assert len(picks) >= 3, counts
+    say("experts", picks, "counts", counts[picks].tolist())
+    xhat = dequant_act_1x128(*quant_act_1x128(np_f32(x)))
+    for e in picks:
+        first = int(np.nonzero(b2 == e)[0][0]) * B
+        slots = np.arange(first, first + counts[e])
+        toks = tp[slots]
+        assert np.all(toks >= 0) and np.all(np.diff(toks) > 0)
+        w13 = dequant_weight_128x128(np_u8(w.w13[e]), np_f32(w.w13_scale[e]))
+        w2 = dequant_weight_128x128(np_u8(w.w2[e]), np_f32(w.w2_scale[e]))
+        ref = expert_mlp(xhat[toks], w13, w2)
+        got = np_f32(y[torch.from_numpy(slots).to(cuda)])
+        err = rel_l2(got, ref)
+        say("expert", e, "rows", counts[e], "rel_l2", err)
+        assert err <= TOL_REL_L2, (e, err)
+    # shared expert: slots NB + t; its last two 256-row tiles
+    sh = np.arange(T - 512, T)
+    w13 = dequant_weight_128x128(np_u8(w.shared_w13[0]), np_f32(w.shared_w13_scale[0]))
+    w2 = dequant_weight_128x128(np_u8(w.shared_w2[0]), np_f32(w.shared_w2_scale[0]))
+    ref = expert_mlp(xhat[sh], w13, w2)
+    got = np_f32(y[NB + T - 512:NB + T])
+    err = rel_l2(got, ref)
+    say("shared expert last tiles rel_l2", err)
+    assert err <= TOL_REL_L2, err
+    # row-tile kernels on the same routing and operands
+    tiles, num, mx = ops.build_tiles(tpid, b2e, B, T, K, E, 1, 128)
+    hq2, hs2 = ops.expert_gate_up(xq, xs, w, tpid, NB, tiles, num, mx, 128)
+    y2 = ops.expert_down(hq2, hs2, w, T, NB, tiles, num, mx, 128)
+    out_row = ops.combine(y2, m["inv_pos"], wts, T, cfg.hidden, NB, 1)
+    err = rel_l2(np_f32(out_row), np_f32(out_blk))
+    say("row tiles vs block kernels rel_l2", err)
+    assert err < 5e-3, err
+    assert torch.equal(out_blk, ops.layer_forward(x, w, cfg))
+    del w, y, y2, hq, hq2
     torch.cuda.empty_cache()
 
 
@@ -181,14 +262,40 @@ def kimi_weights(cuda):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("T,tokens", [(1, [0]), (256, [0, 131, 255]), (16384, [0, 9001, 16383])])
-def test_layer_kimi_k2_full_size(cuda, kimi_weights, T, tokens):
-    """Kimi-K2 layer (384 experts + 1 shared, sigmoid top-8 over one group, x2.827) at the
-    ends and middle of its token sweep: 1 token (row tiles), 256, and 16384 (block
-    kernels, ~341 rows per expert)."""
+def _tile_tokens(ids, E, extra=(), n_experts=6):
+    """Tokens that put the oracle on the last (partial) 256-row tile of several experts.
+
+    Slots hold an expert's tokens in ascending order, so the expert's largest token id
+    sits in its last slot, on its last tile. The experts are picked by count mod 256
+    (one per 64-row band of the last tile's height, then the most and least loaded)."""
+    ids = np.asarray(ids)
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    live = np.nonzero(counts)[0]
+    rem = (counts[live] - 1) % 256 + 1                    # rows of each expert's last tile
+    picks = []
+    for lo in (0, 64, 128, 192):
+        band = live[(rem > lo) & (rem <= lo + 64)]
+        if band.size:
+            picks.append(int(band[np.argmax(counts[band])]))
+    picks += [int(live[np.argmax(counts[live])]), int(live[np.argmin(counts[live])])]
+    picks = list(dict.fromkeys(picks))[:n_experts]
+    toks = {int(np.nonzero((ids == e).any(axis=1))[0].max()) for e in picks}
+    return sorted(toks | set(extra)), picks
+
+
+@pytest.mark.parametrize("T", [1, 16, 256, 2048, 16384])
+def test_layer_kimi_k2_full_size(cuda, kimi_weights, T):
+    """Kimi-K2 layer (384 experts + 1 shared, sigmoid top-8 over one group, x2.827) over
+    its whole token sweep: 1 and 16 tokens (16-row tiles), 256 (32-row tiles), 2048
+    (block kernels on mostly one partial tile per expert, ~43 rows) and 16384 (block
+    kernels, ~341 rows per expert). The oracle checks the first and last token and the
+    tokens in the last slot of experts whose last tiles cover every 64-row band."""
     cfg = PRESETS["kimi_k2"]
     say("layer kimi-k2 full", T)
     x = synthetic.hidden_states(T, cfg.hidden, 3).to(cuda)
+    ids = ops.layer_forward(x, kimi_weights, cfg, return_routing=True)[1].cpu().numpy()
+    tokens, experts = _tile_tokens(ids, cfg.n_experts, extra=(0, T - 1))
+    say("kimi tokens", tokens, "experts", experts)
     _check_layer(cfg, kimi_weights, x, tokens=tokens, tag=f"kimi T={T}")
 
 
@@ -268,3 +375,100 @@ def test_block_kernels_every_tile_height(cuda):
     err = rel_l2(np_f32(out), ref)
     say("tile heights rel_l2", err)
     assert err <= TOL_REL_L2, err
+
+
+# ---------------------------------------------------------------- the layer's own norm
+
+def _check_layer_norm(cfg, w, x, gamma, residual=None, hidden_actual=None, tokens=None, tag=""):
+    """Layer with its pre-MoE RMSNorm (and the fused residual add) against the oracle
+    composition: v = bf16(x + residual) -> xn = bf16(RMSNorm(v)) -> router on xn ->
+    selection -> experts on xn. The normalized rows come from the same fused kernel
+    (ops.rms_norm_quant); the kernel itself is pinned against the oracle's norm in
+    test_rms_norm_quant_fused."""
+    r = ops.layer_forward(x, w, cfg, return_routing=True, gamma=gamma, eps=1e-6,
+                          hidden_actual=hidden_actual, residual=residual)
+    if residual is not None:
+        out, rsum, ids, wts, lg = r
+        assert np.array_equal(np_f32(rsum), bf16_round(np_f32(x) + np_f32(residual))), tag
+    else:
+        out, ids, wts, lg = r
+    xn, _, _, _ = ops.rms_norm_quant(x, gamma, 1e-6, hidden_actual, residual)
+    v = np_f32(x) if residual is None else np_f32(rsum)
+    ref_xn = R.rms_norm_padded(v, np_f32(gamma), 1e-6, hidden_actual)
+    assert np.allclose(np_f32(xn), bf16_round(ref_xn), rtol=2 ** -7, atol=0), tag
+    xs = np_f32(xn)
+    lg, ids, wts = lg.cpu().numpy(), ids.cpu().numpy(), wts.cpu().numpy()
+    ref_lg = R.router_logits(xs, np_f32(w.router_w), None if w.router_bias is None else np_f32(w.router_bias))
+    assert np.allclose(lg, ref_lg, rtol=1e-5, atol=2e-5), tag
+    oi, ow = _route_oracle(cfg, lg, w)
+    assert np.array_equal(ids, oi) and np.array_equal(wts, ow), tag
+    sel = np.arange(x.shape[0]) if tokens is None else np.asarray(tokens)
+    experts = set(np.unique(ids[sel]).tolist())
+    q13, s13, q2, s2 = oracle_weights(w, experts if tokens is not None else None)
+    ref = moe_sparse_fp8(xs[sel], ids[sel], wts[sel], q13, s13, q2, s2, shared=oracle_shared(w),
+                         experts=experts)
+    err = rel_l2(np_f32(out)[sel], ref)
+    say(tag, "rel_l2", err)
+    assert err <= TOL_REL_L2, (tag, err)
+    # without the norm the same layer differs (the norm is applied, not skipped)
+    return out
+
+
+def _gamma(H, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    return (1 + 0.2 * torch.randn(H, generator=g)).to(torch.bfloat16).float().to(device)
+
+
+@pytest.mark.parametrize("residual, hidden_actual", [(False, None), (True, None), (True, 1000)])
+def test_layer_norm_small(cuda, residual, hidden_actual):
+    """Small layer (64 tokens, H 1024) with the layer's own RMSNorm, the residual add
+    and a padded hidden size."""
+    cfg = PRESETS["small"]
+    say("layer norm small", residual, hidden_actual)
+    w = synthetic.make_weights(cfg, 0, device=cuda)
+    x = (3 * synthetic.hidden_states(64, cfg.hidden, 0)).to(torch.bfloat16).to(cuda)
+    r = synthetic.hidden_states(64, cfg.hidden, 7).to(cuda) if residual else None
+    gamma = _gamma(cfg.hidden, 1, cuda)
+    out = _check_layer_norm(cfg, w, x, gamma, r, hidden_actual, tag=f"norm small {residual}")
+    assert not torch.equal(out, ops.layer_forward(x, w, cfg))
+
+
+@pytest.mark.parametrize("T,idx,tokens", [(64, 1, None), (8192, 2, [0, 3001, 8191])])
+def test_layer_norm_dsv3_full_size(cuda, T, idx, tokens):
+    """DeepSeek-V3 decode 64 and prefill 8192 with the layer's RMSNorm and residual add."""
+    cfg = PRESETS["dsv3"]
+    say("layer norm dsv3", T)
+    w = _big_weights(cfg, idx, cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, idx).to(cuda)
+    r = synthetic.hidden_states(T, cfg.hidden, idx + 50).to(cuda)
+    gamma = _gamma(cfg.hidden, idx, cuda)
+    if tokens is None:
+        tokens = [0, 17, 40, 63]
+    _check_layer_norm(cfg, w, x, gamma, r, tokens=tokens, tag=f"norm dsv3 T={T}")
+    del w
+    torch.cuda.empty_cache()
+
+
+def test_layer_module_norm_and_residual(cuda):
+    """FP8BlockMoE with a norm weight: prefill with a residual returns (out, x +
+    residual) and equals the functional layer; decode applies the same norm and returns
+    one tensor; padding rows after the last real position are zero."""
+    cfg = PRESETS["small"]
+    say("layer module norm")
+    w = synthetic.make_weights(cfg, 0, device=cuda)
+    x = synthetic.hidden_states(64, cfg.hidden, 0).to(cuda)
+    r = synthetic.hidden_states(64, cfg.hidden, 9).to(cuda)
+    gamma = _gamma(cfg.hidden, 2, cuda)
+    layer = FP8BlockMoE(cfg, w, norm_weight=gamma.to(torch.bfloat16), eps=1e-6)
+    out, rsum = layer(x, positions=None, is_decode=False, rank=None, residual=r)
+    ref_out, ref_sum = ops.layer_forward(x, w, cfg, gamma=gamma, eps=1e-6, residual=r)
+    assert torch.equal(out, ref_out) and torch.equal(rsum, ref_sum)
+    dec = layer(rsum, None, True, None)
+    assert torch.equal(dec, ops.layer_forward(rsum, w, cfg, gamma=gamma, eps=1e-6))
+    assert torch.equal(dec, out)  # norm(x + r) either way
+    pos = torch.arange(64, device=cuda)
+    pos[40:] = 0
+    pad, _ = layer(x, positions=pos, is_decode=False, residual=r)
+    assert torch.equal(pad[:40], out[:40]) and torch.all(pad[40:] == 0)
+    with pytest.raises(ValueError):
+        FP8BlockMoE(cfg, w)(x, None, False, None, residual=r)

@@ -94,3 +94,24 @@ def test_weight_quant_blocks():
     tq, ts = quant_weight_blocks(torch.from_numpy(w))
     assert np.array_equal(tq.view(torch.uint8).numpy(), q)
     assert np.array_equal(ts.numpy(), s)
+
+
+def test_bf16_round_matches_torch_bfloat16_cast():
+    """oracle.moe.bf16_round equals torch's float32 -> bfloat16 cast (round to nearest
+    even) on every exponent, on halfway cases of both parities, and on signed zeros and
+    subnormals."""
+    import torch
+
+    from oracle.moe import bf16_round
+    rng = np.random.default_rng(5)
+    u = rng.integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    exp_all = ((np.arange(256, dtype=np.uint32) << 23)[:, None] | np.arange(0, 1 << 16, 97, dtype=np.uint32)[None, :]).reshape(-1)
+    halfway = (rng.integers(0, 2 ** 16, size=4096, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000
+    special = np.array([0, 0x80000000, 1, 0x8000, 0x7F7FFFFF, 0x00800000, 0x3F808000, 0x3F818000],
+                       dtype=np.uint32)
+    bits = np.concatenate([u, exp_all, exp_all | 0x80000000, halfway, special])
+    x = bits.view(np.float32)
+    x = x[np.isfinite(x) & (np.abs(x.astype(np.float64)) < 3.3e38)]  # stay below bf16 overflow
+    got = bf16_round(x)
+    ref = torch.from_numpy(x.copy()).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))

@@ -29,6 +29,7 @@ struct MapWs {
   int32_t* chunk_counts;  // [nchunks, E]
   int32_t* chunk_base;    // [nchunks, E]
   int32_t* block_off;     // [E]
+  int32_t* count_off;     // [E] exclusive prefix of the counts (compact rows)
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -44,12 +45,14 @@ static inline MapWs carve_map_ws(void* ws, int T, int E) {
   m.chunk_base = (int32_t*)p;
   p += align256((size_t)nch * E * 4);
   m.block_off = (int32_t*)p;
+  p += align256((size_t)E * 4);
+  m.count_off = (int32_t*)p;
   return m;
 }
 
 static inline size_t map_ws_bytes(int T, int E) {
   int nch = (T + kChunk - 1) / kChunk;
-  return 256 + 2 * align256((size_t)nch * E * 4) + align256((size_t)E * 4);
+  return 256 + 2 * align256((size_t)nch * E * 4) + 2 * align256((size_t)E * 4);
 }
 
 __device__ __forceinline__ void build_chunk_mask(uint32_t (*bm)[8], const int32_t* ids,
@@ -130,11 +133,13 @@ __device__ __forceinline__ int block_inclusive_sum(int v, int* s_wave) {
 // Everything after the per-expert counts: block offsets (exclusive scan of
 // ceil(count/B)), expert_counts, block_to_expert, conditions and the optional tile
 // list. Thread tid < E holds run = count of expert tid. Leaves the inclusive
-// block scan in s_blk and the counts in s_cnt; 1024 threads.
+// block scan in s_blk, the counts in s_cnt and, for compact rows, the exclusive
+// count scan in s_cex (and count_off); 1024 threads.
 __device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __restrict__ expert_counts,
                                int32_t* __restrict__ block_to_expert, int32_t* __restrict__ conditions,
-                               int32_t* __restrict__ block_off, const TileOut& to, int* s_blk, int* s_cnt,
-                               int* s_tile, int* s_wave) {
+                               int32_t* __restrict__ block_off, int32_t* __restrict__ count_off,
+                               const TileOut& to, int* s_blk, int* s_cnt, int* s_cex, int* s_tile,
+                               int* s_wave) {
   const int tid = threadIdx.x;
   int blk = 0;
   if (tid < E) {
@@ -146,6 +151,13 @@ __device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __r
     if (block_off != nullptr) block_off[tid] = cum - blk;  // exclusive
     s_blk[tid] = cum;                                      // inclusive cumulative blocks
     s_cnt[tid] = run;
+  }
+  if (to.compact) {  // workgroup-uniform
+    const int ccum = block_inclusive_sum(run, s_wave);
+    if (tid < E) {
+      s_cex[tid] = ccum - run;
+      if (count_off != nullptr) count_off[tid] = ccum - run;
+    }
   }
   __syncthreads();
   const int total = s_blk[E - 1];
@@ -184,20 +196,26 @@ __device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __r
     const int c = s_cnt[e];
     const long base = (long)(s_blk[e] - (c + B - 1) / B) * B;
     if (to.span) {
-      to.tiles[i] = make_int4(e, (int)(base + (long)loc * mt), min(mt, c - loc * mt), 0);
+      const long in_e = (long)loc * mt;  // first slot of the tile, relative to the expert
+      const long row = to.compact ? s_cex[e] + in_e : base + in_e;
+      to.tiles[i] = make_int4(e, (int)(base + in_e), min(mt, c - loc * mt), (int)row);
       to.seg[i] = make_int2(first, s_tile[e] - first);
     } else {
       const int j = loc / tpb, m = loc - j * tpb;
       const int rows = min(B, c - j * B);
-      to.tiles[i] = make_int4(e, (int)(base + (long)j * B + m * mt), min(mt, rows - m * mt), 0);
+      const long in_e = (long)j * B + m * mt;
+      const long row = to.compact ? s_cex[e] + in_e : base + in_e;
+      to.tiles[i] = make_int4(e, (int)(base + in_e), min(mt, rows - m * mt), (int)row);
     }
   }
   const int per = (T + mt - 1) / mt;
   const long nb_total = (long)N * B;
+  const long row_sh = to.compact ? to.row_shared : nb_total;
   for (int i = tid; i < to.n_shared * per; i += blockDim.x) {
     const int j = i / per, m = i - j * per, idx = ntiles + i;
     if (idx < to.max_tiles) {
-      to.tiles[idx] = make_int4(E + j, (int)(nb_total + (long)j * T + (long)m * mt), min(mt, T - m * mt), 0);
+      const long in_sh = (long)j * T + (long)m * mt;
+      to.tiles[idx] = make_int4(E + j, (int)(nb_total + in_sh), min(mt, T - m * mt), (int)(row_sh + in_sh));
       if (to.span) to.seg[idx] = make_int2(ntiles + j * per, per);
     }
   }
@@ -211,6 +229,7 @@ __global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int
                                                         MapWs ws, TileOut to) {
   __shared__ int s_blk[kMapMaxE];
   __shared__ int s_cnt[kMapMaxE];
+  __shared__ int s_cex[kMapMaxE];
   __shared__ int s_tile[kMapMaxE];
   __shared__ int s_wave[16];
   const int tid = threadIdx.x;
@@ -222,8 +241,8 @@ __global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int
       run += v;
     }
   }
-  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off, to,
-                 s_blk, s_cnt, s_tile, s_wave);
+  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off,
+                 ws.count_off, to, s_blk, s_cnt, s_cex, s_tile, s_wave);
 }
 
 // The whole mapping in one workgroup, for ids and at most one 256-token chunk
@@ -237,6 +256,7 @@ __global__ __launch_bounds__(1024) void map_small_kernel(
   __shared__ uint32_t bm[kMapMaxE][8];
   __shared__ int s_blk[kMapMaxE];
   __shared__ int s_cnt[kMapMaxE];
+  __shared__ int s_cex[kMapMaxE];
   __shared__ int s_tile[kMapMaxE];
   __shared__ int s_wave[16];
   const int tid = threadIdx.x;
@@ -255,8 +275,8 @@ __global__ __launch_bounds__(1024) void map_small_kernel(
 #pragma unroll
     for (int w = 0; w < 8; ++w) run += __popc(bm[tid][w]);
   }
-  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off, to,
-                 s_blk, s_cnt, s_tile, s_wave);
+  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off,
+                 nullptr, to, s_blk, s_cnt, s_cex, s_tile, s_wave);
   for (int i = tid; i < T * K; i += blockDim.x) {
     const int t = i / K;
     const int e = ids[i];
@@ -269,7 +289,7 @@ __global__ __launch_bounds__(1024) void map_small_kernel(
       const long slot = (long)(s_blk[e] - (s_cnt[e] + B - 1) / B) * B + rank;
       if (slot < nb_total) {
         tpid[slot] = t;
-        out = (int)slot;
+        out = to.compact ? s_cex[e] + rank : (int)slot;
       } else {
         atomicAdd(ws.status, 1);
       }
@@ -278,19 +298,24 @@ __global__ __launch_bounds__(1024) void map_small_kernel(
   }
 }
 
+// inv_rows: inv_pos receives compact rows (count_off[e] + rank in the expert)
+// instead of slots.
 __global__ __launch_bounds__(256) void map_scatter_kernel(
     const int32_t* __restrict__ ids, const float* __restrict__ aff, int T, int K, int E, int B,
-    long nb_total, int32_t* __restrict__ tpid, int32_t* __restrict__ inv_pos, MapWs ws) {
+    long nb_total, int32_t* __restrict__ tpid, int32_t* __restrict__ inv_pos, int inv_rows,
+    MapWs ws) {
   __shared__ uint32_t bm[kMapMaxE][8];
   const int chunk = blockIdx.x, t0 = chunk * kChunk;
   build_chunk_mask(bm, ids, aff, T, K, E, t0, ws.status);
-  auto slot_of = [&](int e, int tl) -> long {
+  // rank of token t0 + tl among the tokens of expert e (all chunks)
+  auto rank_of = [&](int e, int tl) -> int {
     int rank = 0;
     const int wq = tl >> 5;
     for (int w = 0; w < wq; ++w) rank += __popc(bm[e][w]);
     rank += __popc(bm[e][wq] & ((1u << (tl & 31)) - 1u));
-    return (long)ws.block_off[e] * B + ws.chunk_base[(size_t)chunk * E + e] + rank;
+    return ws.chunk_base[(size_t)chunk * E + e] + rank;
   };
+  auto slot_of = [&](int e, int tl) -> long { return (long)ws.block_off[e] * B + rank_of(e, tl); };
   if (ids != nullptr) {
     for (int i = threadIdx.x; i < kChunk * K; i += blockDim.x) {
       int tl = i / K, t = t0 + tl;
@@ -302,7 +327,7 @@ __global__ __launch_bounds__(256) void map_scatter_kernel(
         long s = slot_of(e, tl);
         if (s < nb_total) {
           tpid[s] = t;
-          out = (int)s;
+          out = inv_rows ? ws.count_off[e] + rank_of(e, tl) : (int)s;
         } else {
           atomicAdd(ws.status, 1);
         }
@@ -396,7 +421,7 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(
         for (int j = 0; j < loc[q]; ++j) {
           int idx = base + run + j;
           if (idx < max_tiles)
-            tiles[idx] = make_int4(e, b * B + j * mt, min(mt, s_vlen[i] - j * mt), 0);
+            tiles[idx] = make_int4(e, b * B + j * mt, min(mt, s_vlen[i] - j * mt), b * B + j * mt);
         }
         run += loc[q];
       }
@@ -409,8 +434,10 @@ __global__ __launch_bounds__(1024) void build_tiles_kernel(
   for (int i = tid; i < n_shared * per; i += blockDim.x) {
     int j = i / per, m = i - j * per;
     int idx = base + i;
-    if (idx < max_tiles)
-      tiles[idx] = make_int4(E + j, (int)(nb_total + (long)j * T + (long)m * mt), min(mt, T - m * mt), 0);
+    if (idx < max_tiles) {
+      const int s0 = (int)(nb_total + (long)j * T + (long)m * mt);
+      tiles[idx] = make_int4(E + j, s0, min(mt, T - m * mt), s0);
+    }
   }
   if (tid == 0) num_tiles[0] = min(base + n_shared * per, max_tiles);
 }
@@ -444,6 +471,8 @@ int moe::blockwise_mapping(const int32_t* ids, const float* affinities,
   MOE_CHECK_ARG(to.tiles == nullptr || (to.num_tiles && to.mt > 0 && to.max_tiles > 0 &&
                                         to.n_shared >= 0 && (!to.span || to.seg)),
                 "bad tile output");
+  MOE_CHECK_ARG(!to.compact || (to.tiles != nullptr && ids != nullptr && to.row_shared >= 0),
+                "compact rows need ids and a tile list");
   MOE_CHECK_ARG((ids != nullptr) != (affinities != nullptr),
                 "exactly one of ids / affinities must be given");
   MOE_CHECK_ARG(token_position_to_id && block_to_expert && workspace, "null pointer argument");
@@ -470,7 +499,7 @@ int moe::blockwise_mapping(const int32_t* ids, const float* affinities,
   hipLaunchKernelGGL(map_scan_kernel, dim3(1), dim3(1024), 0, st, T, E, B, N, nch, expert_counts,
                      block_to_expert, conditions, ws, to);
   hipLaunchKernelGGL(map_scatter_kernel, dim3(nch), dim3(256), 0, st, ids, affinities, T, K, E, B,
-                     nbt, token_position_to_id, inv_pos, ws);
+                     nbt, token_position_to_id, inv_pos, to.compact, ws);
   MOE_API_END();
 }
 

@@ -32,6 +32,7 @@ static int choose_mt(int T, int K, int E) {
 }
 
 struct LayerWs {
+  uint16_t* xn;  // normalized rows (bf16), when the layer normalizes
   float* logits;
   void* router_ws;
   size_t router_ws_bytes;
@@ -67,12 +68,16 @@ static bool use_block(int T, int K, int E) {
 
 static inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Routed rows held by the layer's hq / y buffers: every routed (token, expert)
+// pair has a row (packed expert by expert), then n_shared * T shared rows.
+static inline long routed_rows(int T, int K, int E) { return (long)T * std::min(K, E); }
+
 // Carves the workspace (base may be null to size it).
-static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, int B) {
+static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, int B, bool norm) {
   LayerWs w{};
   const int N = moe_num_blocks(T, K, E, B);
   const long NB = (long)N * B;
-  const long P = NB + (long)n_sh * T;
+  const long P = routed_rows(T, K, E) + (long)n_sh * T;
   const int mt = choose_mt(T, K, E);
   const int max_tiles = moe_max_tiles(T, K, E, N, B, n_sh, mt);
   size_t off = 0;
@@ -81,6 +86,7 @@ static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, in
     off += al(bytes);
     return p;
   };
+  if (norm) w.xn = (uint16_t*)take((size_t)T * H * 2);
   w.logits = (float*)take((size_t)T * E * 4);
   w.router_ws_bytes = moe_router_logits_workspace_bytes(T, H, E);
   w.router_ws = take(w.router_ws_bytes);
@@ -117,35 +123,43 @@ extern "C" int moe_abi_version(void) { return MOE_FP8_ABI_VERSION; }
 
 extern "C" const char* moe_last_error(void) { return g_err; }
 
-extern "C" size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, int n_shared, int B) {
+extern "C" size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, int n_shared, int B,
+                                            int norm) {
   if (T <= 0 || H <= 0 || I <= 0 || E <= 0 || K <= 0 || n_shared < 0 || B <= 0) return 0;
-  return carve(nullptr, T, H, I, E, K, n_shared, B).bytes;
+  return carve(nullptr, T, H, I, E, K, n_shared, B, norm != 0).bytes;
 }
 
-extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E, int K,
-                                 int n_shared, const void* router_w_bf16,
+extern "C" int moe_layer_forward(const void* x_bf16, const void* residual_bf16,
+                                 const float* gamma, float eps, int hidden_actual, int T, int H,
+                                 int I, int E, int K, int n_shared, const void* router_w_bf16,
                                  const float* router_bias, const float* corr_bias, int order,
                                  int scoring, int n_group, int topk_group, int renorm,
                                  float renorm_eps, float routed_scale, const uint8_t* w13,
                                  const float* w13_scale, const uint8_t* w2, const float* w2_scale,
                                  const uint8_t* w13_shared, const float* w13_shared_scale,
                                  const uint8_t* w2_shared, const float* w2_shared_scale, int B,
-                                 void* out_bf16, int32_t* ids_out, float* weights_out,
-                                 float* logits_out, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+                                 void* out_bf16, void* residual_out_bf16, int32_t* ids_out,
+                                 float* weights_out, float* logits_out, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   MOE_API_BEGIN("moe_layer_forward");
   MOE_CHECK_ARG(x_bf16 && router_w_bf16 && w13 && w13_scale && w2 && w2_scale && out_bf16 && workspace,
                 "null pointer argument");
   MOE_CHECK_ARG(T > 0 && E > 0 && K > 0 && K <= E && B > 0 && n_shared >= 0,
                 "bad sizes T=%d E=%d K=%d B=%d", T, E, K, B);
   MOE_CHECK_ARG(H % 256 == 0 && I % 128 == 0, "H must be a multiple of 256 and I of 128");
-  const size_t need = moe_layer_workspace_bytes(T, H, I, E, K, n_shared, B);
+  MOE_CHECK_ARG((residual_bf16 == nullptr) == (residual_out_bf16 == nullptr),
+                "residual and residual_out must be given together");
+  MOE_CHECK_ARG(gamma != nullptr || residual_bf16 == nullptr,
+                "the residual add is fused into the norm: residual needs gamma");
+  const bool norm = gamma != nullptr;
+  const size_t need = moe_layer_workspace_bytes(T, H, I, E, K, n_shared, B, norm);
   MOE_CHECK_ARG(workspace_bytes >= need, "workspace too small: need %zu bytes, got %zu", need,
                 workspace_bytes);
   MOE_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
-  LayerWs w = carve((char*)workspace, T, H, I, E, K, n_shared, B);
+  LayerWs w = carve((char*)workspace, T, H, I, E, K, n_shared, B, norm);
   const int N = moe_num_blocks(T, K, E, B);
   const long NB = (long)N * B;
+  const long R = routed_rows(T, K, E);
   MOE_CHECK_SUPPORTED(NB + (long)n_shared * T < (1L << 31), "too many slots");
   const int mt = choose_mt(T, K, E);
   const int max_tiles = moe_max_tiles(T, K, E, N, B, n_shared, mt);
@@ -162,7 +176,16 @@ extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E,
     moe::set_error(_moe_fn, "%s", saved);                      \
     return rc;                                                 \
   }
-  MOE_STEP(router_logits_topk(x_bf16, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+  // Pre-MoE RMSNorm (with the residual add) and the 1x128 quantization of the
+  // normalized rows in one pass; the router reads the normalized bf16 rows.
+  const void* xr = x_bf16;
+  if (norm) {
+    MOE_STEP(moe_rms_norm_quant(x_bf16, residual_bf16, gamma, T, H,
+                                hidden_actual > 0 ? hidden_actual : H, eps, w.xn,
+                                residual_out_bf16, w.xq, w.xs, stream));
+    xr = w.xn;
+  }
+  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
                               w.router_ws_bytes, corr_bias, K, order, scoring, n_group, topk_group,
                               renorm, renorm_eps, routed_scale, ids, wts, stream));
   // The mapping's scan kernel also writes the expert tile list, from the counts.
@@ -183,9 +206,11 @@ extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E,
     to.mt = mt;
   }
   to.n_shared = n_shared;
+  to.compact = 1;  // hq / y hold only the routed and shared rows
+  to.row_shared = R;
   MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
                              w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
-  MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
+  if (!norm) MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
   if (block) {
     MOE_STEP(moe_expert_gate_up_block(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
                                       w13_shared_scale, n_shared, w.tpid, (int)NB, w.btiles,
@@ -201,7 +226,7 @@ extern "C" int moe_layer_forward(const void* x_bf16, int T, int H, int I, int E,
                              n_shared, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y,
                              stream));
   }
-  MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)NB, n_shared, out_bf16, stream));
+  MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)R, n_shared, out_bf16, stream));
 #undef MOE_STEP
   return MOE_OK;
 }

@@ -10,7 +10,9 @@
 // 128x128 block-scale dequantization is DeepSeek-V3's checkpoint format.
 //
 // Work decomposition: a work item is (row tile, N tile). A row tile holds up
-// to MT consecutive slots of one expert (moe_build_tiles). Each workgroup
+// to MT consecutive slots of one expert (moe_build_tiles) and names the first
+// row of hq / y its slots use (the slot itself, or a compacted row in the
+// layer, whose buffers hold only the routed rows). Each workgroup
 // (4 waves) owns 256 weight rows: for gate_up, 128 gate rows and the matching
 // 128 up rows (so one workgroup sees a whole 128-column quantization group of
 // h); for down, 256 output columns. Wave w owns four 16-row MFMA column tiles.
@@ -88,6 +90,7 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
     const int4 td = p.tiles[tile];
     const int e = td.x, nrows = td.z;
     const long slot0 = td.y;
+    const long row0 = td.w;  // first hq / y row of the tile
     if (e < 0 || e >= p.E + p.nsh) continue;  // workgroup-uniform: malformed tile
     const bool is_sh = e >= p.E;
     const int ej = is_sh ? e - p.E : e;
@@ -100,7 +103,7 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
           src = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
           if (src >= p.T) src = -1;  // token ids outside [0, T) are treated as padding
         } else {
-          src = slot;
+          src = row0 + tid;
         }
       }
       sSrc[tid] = src;
@@ -250,14 +253,14 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
           const float amax = fmaxf(fmaxf(sRed[0][row], sRed[1][row]), fmaxf(sRed[2][row], sRed[3][row]));
           const float sc = fmaxf(amax, 0x1.b7cdfep-34f) / 448.0f;
           if (sSrc[row] >= 0) {
-            const long slot = slot0 + row;
+            const long hrow_i = row0 + row;
             const float rs = 1.0f / sc;
             const uint32_t c2 = e4m3x2(fminf(fmaxf(div_by(acc[ms][0][i], sc, rs), -448.0f), 448.0f),
                                        fminf(fmaxf(div_by(acc[ms][1][i], sc, rs), -448.0f), 448.0f));
-            uint8_t* const hrow = p.hq + (size_t)slot * p.I + nt * 128 + wave * 32 + r16;
+            uint8_t* const hrow = p.hq + (size_t)hrow_i * p.I + nt * 128 + wave * 32 + r16;
             hrow[0] = (uint8_t)c2;
             hrow[16] = (uint8_t)(c2 >> 8);
-            if (wave == 0 && r16 == 0) p.hs[(size_t)slot * GI + nt] = sc;
+            if (wave == 0 && r16 == 0) p.hs[(size_t)hrow_i * GI + nt] = sc;
           }
         }
       }
@@ -268,11 +271,11 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
         for (int i = 0; i < 4; ++i) {
           const int row = ms * 16 + 4 * g + i;
           if (row < nrows) {
-            const long slot = slot0 + row;
+            const long yrow = row0 + row;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int col = nt * 256 + wave * 64 + j * 16 + r16;
-              p.y[(size_t)slot * p.H + col] = (uint16_t)bf16x2(acc[ms][j][i], 0.f);
+              p.y[(size_t)yrow * p.H + col] = (uint16_t)bf16x2(acc[ms][j][i], 0.f);
             }
           }
         }

@@ -52,7 +52,7 @@ struct BlkArgs {
   const uint8_t* wsh;
   const float* wssh;
   const int32_t* tpid;
-  const int4* tiles;   // {expert, first slot, rows, 0}
+  const int4* tiles;   // {expert, first slot, rows, first hq / y row}
   const int2* seg;     // {first tile of the expert, tiles of the expert}
   const int32_t* num_tiles;
   uint8_t* hq;
@@ -96,12 +96,13 @@ struct BlkLds {
 };
 
 // One work item: tile rows [slot0, slot0 + nrows) of expert e against column
-// tile nt. MF is the number of 16-row fragments per wave: the four row groups
+// tile nt; they use hq / y rows [rbase, rbase + nrows). MF is the number of 16-row fragments per wave: the four row groups
 // hold 16 * MF rows each, so a tile of up to 64 * MF rows keeps all eight waves
 // (two per SIMD) busy and its MFMA, ratio and fragment-read work scales with MF.
 template <int KIND, int MF>
 __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, const int e,
-                                           const long slot0, const int nrows, const int nt) {
+                                           const long slot0, const long rbase, const int nrows,
+                                           const int nt) {
   uint8_t* const sTA0 = s.ta0;
   uint8_t* const sTB0 = s.tb0;
   uint8_t* const sTA1 = s.ta1;
@@ -134,7 +135,7 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
         long sv = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
         src = (sv >= 0 && sv < p.T) ? (int)sv : -1;
       } else {
-        src = (int)slot;
+        src = (int)(rbase + r);
       }
     }
     sSrc[r] = src;
@@ -159,7 +160,7 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
     const int row = 8 * (4 * wave + (i & 3)) + (lane >> 3);
     if (i < 4) {
       const int src = sSrc[row];
-      off[i] = (uint32_t)((src >= 0 ? src : 0) * Kdim + swz(row, lane & 7) * 16);
+      off[i] = (uint32_t)(src >= 0 ? src : 0) * (uint32_t)Kdim + (uint32_t)(swz(row, lane & 7) * 16);
     } else {
       // Tile row -> weight row. Column tile n of a wave reads tile rows 16 n + j,
       // and they hold output columns 4 j + n (gate_up, per 64-column wave half) or
@@ -188,7 +189,8 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // own wave's scale load fills, so its own vmcnt wait covers them.
   const int srow = 64 * wm + lane, shalf = wn;
   const bool svalid = sSrc[srow] >= 0;
-  const uint32_t off_sa = (uint32_t)((sSrc[64 * wm + lane] >= 0 ? sSrc[64 * wm + lane] : 0) * KB * 4);
+  // Byte offsets of operand rows fit 32 bits: the entry points reject larger operands.
+  const uint32_t off_sa = (uint32_t)(sSrc[64 * wm + lane] >= 0 ? sSrc[64 * wm + lane] : 0) * (uint32_t)(KB * 4);
   const int sa_dst = (wn * kBM + 64 * wm) * 4;
   for (int i = tid; i < 2 * KB; i += kBlkThreads) {
     const int hf = i / KB, kb = i - hf * KB;
@@ -365,8 +367,8 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
           for (int n = 0; n < 4; ++n) y[n] = fminf(fmaxf(div_by(acc[m][n][i], sc, rs), -448.0f), 448.0f);
           const uint32_t c4 = e4m3x2(y[0], y[1]) | (e4m3x2(y[2], y[3]) << 16);
           if (row < nrows && sSrc[row] >= 0) {
-            *(uint32_t*)(p.hq + (size_t)(slot0 + row) * p.I + nt * 128 + 64 * wn + 4 * l16) = c4;
-            if (wn == 0 && l16 == 0) p.hs[(size_t)(slot0 + row) * GI + nt] = sc;
+            *(uint32_t*)(p.hq + (size_t)(rbase + row) * p.I + nt * 128 + 64 * wn + 4 * l16) = c4;
+            if (wn == 0 && l16 == 0) p.hs[(size_t)(rbase + row) * GI + nt] = sc;
           }
         }
     }
@@ -382,7 +384,7 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
         o.y = (int)bf16x2(acc[m][2][i] * sl, acc[m][3][i] * sl);
         o.z = (int)bf16x2(acc[m][4][i] * sl, acc[m][5][i] * sl);
         o.w = (int)bf16x2(acc[m][6][i] * sl, acc[m][7][i] * sl);
-        if (row < nrows) *(int4*)(p.y + (size_t)(slot0 + row) * p.H + nt * kBN + 128 * wn + 8 * l16) = o;
+        if (row < nrows) *(int4*)(p.y + (size_t)(rbase + row) * p.H + nt * kBN + 128 * wn + 8 * l16) = o;
       }
   }
 }
@@ -422,13 +424,13 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   if (e < 0 || e >= p.E + p.nsh || nrows <= 0) return;
   // Row groups sized to the tile (workgroup-uniform branch).
   if (nrows > 192)
-    block_item<KIND, 4>(p, s, e, td.y, nrows, nt);
+    block_item<KIND, 4>(p, s, e, td.y, td.w, nrows, nt);
   else if (nrows > 128)
-    block_item<KIND, 3>(p, s, e, td.y, nrows, nt);
+    block_item<KIND, 3>(p, s, e, td.y, td.w, nrows, nt);
   else if (nrows > 64)
-    block_item<KIND, 2>(p, s, e, td.y, nrows, nt);
+    block_item<KIND, 2>(p, s, e, td.y, td.w, nrows, nt);
   else
-    block_item<KIND, 1>(p, s, e, td.y, nrows, nt);
+    block_item<KIND, 1>(p, s, e, td.y, td.w, nrows, nt);
 }
 
 // ---------------------------------------------------------------------------
@@ -493,7 +495,8 @@ __global__ __launch_bounds__(1024) void build_block_tiles_kernel(
       for (int c = 0; c < v; ++c) {
         const int idx = off + c;
         if (idx < max_tiles) {
-          tiles[idx] = make_int4(b2e[b], (int)(s0 + (long)c * kBM), (int)min((long)kBM, s1 - s0 - (long)c * kBM), 0);
+          tiles[idx] = make_int4(b2e[b], (int)(s0 + (long)c * kBM), (int)min((long)kBM, s1 - s0 - (long)c * kBM),
+                                 (int)(s0 + (long)c * kBM));
           seg[idx] = make_int2(off, v);
         }
       }
@@ -507,7 +510,8 @@ __global__ __launch_bounds__(1024) void build_block_tiles_kernel(
     const int jj = i / per, m = i - jj * per;
     const int idx = base + i;
     if (idx < max_tiles) {
-      tiles[idx] = make_int4(E + jj, (int)(NB + (long)jj * T + (long)m * kBM), min(kBM, T - m * kBM), 0);
+      const int s0 = (int)(NB + (long)jj * T + (long)m * kBM);
+      tiles[idx] = make_int4(E + jj, s0, min(kBM, T - m * kBM), s0);
       seg[idx] = make_int2(base + jj * per, per);
     }
   }
@@ -557,13 +561,17 @@ extern "C" int moe_build_block_tiles(const int32_t* token_position_to_id,
   MOE_API_END();
 }
 
+// a_rows x a_cols: the gathered operand (x for gate_up, h for down), addressed with
+// 32-bit byte offsets inside the kernel.
 static int block_gemm_common_checks(const char* _moe_fn, int T, int H, int I, int E, int NB,
-                                    int max_tiles) {
+                                    int max_tiles, long a_rows, int a_cols) {
   MOE_CHECK_ARG(T > 0 && E > 0 && NB >= 0 && max_tiles > 0, "bad sizes");
   MOE_CHECK_ARG(H > 0 && H % 256 == 0 && I > 0 && I % 128 == 0,
                 "H must be a multiple of 256 and I of 128 (H=%d I=%d)", H, I);
   MOE_CHECK_SUPPORTED(H / 128 <= kMaxKB && I / 128 <= kMaxKB,
                       "H and I must be at most %d (H=%d I=%d)", 128 * kMaxKB, H, I);
+  MOE_CHECK_SUPPORTED((unsigned long)a_rows * (unsigned long)a_cols < (1UL << 32),
+                      "activation operand of %ld rows x %d bytes exceeds 4 GiB", a_rows, a_cols);
   return MOE_OK;
 }
 
@@ -576,7 +584,7 @@ extern "C" int moe_expert_gate_up_block(const uint8_t* xq, const float* xs, int 
   MOE_API_BEGIN("moe_expert_gate_up_block");
   MOE_CHECK_ARG(xq && xs && w13 && w13_scale && token_position_to_id && tiles && num_tiles && hq && hs,
                 "null pointer argument");
-  int rc = block_gemm_common_checks(_moe_fn, T, H, I, E, NB, max_tiles);
+  int rc = block_gemm_common_checks(_moe_fn, T, H, I, E, NB, max_tiles, T, H);
   if (rc != MOE_OK) return rc;
   MOE_CHECK_ARG(n_shared == 0 || (w13_shared && w13_shared_scale), "shared weights missing");
   MOE_CHECK_ARG(((uintptr_t)xq & 15) == 0 && ((uintptr_t)w13 & 15) == 0 && ((uintptr_t)hq & 15) == 0,
@@ -612,7 +620,8 @@ extern "C" int moe_expert_down_block(const uint8_t* hq, const float* hs, int T, 
                                      void* stream) {
   MOE_API_BEGIN("moe_expert_down_block");
   MOE_CHECK_ARG(hq && hs && w2 && w2_scale && tiles && num_tiles && y_bf16, "null pointer argument");
-  int rc = block_gemm_common_checks(_moe_fn, T, H, I, E, NB, max_tiles);
+  int rc = block_gemm_common_checks(_moe_fn, T, H, I, E, NB, max_tiles,
+                                    (long)NB + (long)n_shared * T, I);
   if (rc != MOE_OK) return rc;
   MOE_CHECK_ARG(n_shared == 0 || (w2_shared && w2_shared_scale), "shared weights missing");
   MOE_CHECK_ARG(((uintptr_t)hq & 15) == 0 && ((uintptr_t)w2 & 15) == 0 && ((uintptr_t)y_bf16 & 15) == 0,

@@ -38,6 +38,11 @@ constexpr int kBlockTileRows = 256;
 // (tiles == nullptr: none). Row tiles stay inside one block; block tiles
 // (span = 1) run across an expert's blocks and carry seg = (first tile of the
 // expert, its tile count). Shared-expert tiles follow the routed ones.
+// A tile is {expert, first slot, rows, first hq / y row}. With compact = 0 the
+// rows are the slots themselves; with compact = 1 the routed rows are packed
+// expert after expert (expert e's i-th slot is row sum_{e' < e} count_e' + i),
+// the shared expert j's token t is row row_shared + j * T + t, and inv_pos
+// receives these rows instead of slots.
 struct TileOut {
   int4* tiles;
   int2* seg;
@@ -46,6 +51,8 @@ struct TileOut {
   int mt;
   int span;
   int n_shared;
+  int compact;
+  long row_shared;
 };
 
 // moe_blockwise_mapping plus an optional tile list (same checks and errors).

@@ -7,7 +7,12 @@ kernels read the DeepSeek-V3 checkpoint stacking (w13 [E, 2I, H], w2 [E, H, I],
 reference layout is converted once per weight tensor and the result cached,
 keyed by the tensors' storage, version and shape (a second copy of the experts
 while the caller keeps the originals: pass the stacked layout to avoid it).
+An entry lives only as long as every source tensor object: a finalizer on each
+source drops it, so a later tensor allocated at a freed address never hits a
+stale entry.
 """
+import weakref
+
 import torch
 
 from ... import ops
@@ -22,13 +27,22 @@ def _key(*ts):
                  for t in ts)
 
 
-def _cached(key, build):
+def _drop(key):
+    _CACHE.pop(key, None)
+
+
+def _cached(key, build, sources):
+    """build() once per key; the entry is dropped when any tensor of ``sources``
+    is garbage-collected (before its memory can be handed to another tensor)."""
     hit = _CACHE.get(key)
     if hit is None:
         if len(_CACHE) >= _CACHE_MAX:
             _CACHE.pop(next(iter(_CACHE)))
         hit = build()
         _CACHE[key] = hit
+        for t in sources:
+            if t is not None:
+                weakref.finalize(t, _drop, key)
     return hit
 
 
@@ -41,6 +55,20 @@ def _need_fp8(t, name):
 
 def _ones_scale(E, O, I, device):
     return torch.ones(E, O // 128, I // 128, device=device, dtype=torch.float32)
+
+
+def weight_dims(gate_up, down):
+    """(E, H, I) of routed expert weights in either layout, from shapes alone: stacked
+    gate_up [E, 2I, H] / down [E, H, I], or reference gate_up [E, H, 2, I] / down
+    [E, I, H]."""
+    if gate_up.dim() == 3:
+        E, I2, H = gate_up.shape
+        return E, H, I2 // 2
+    if gate_up.dim() != 4 or gate_up.shape[2] != 2:
+        raise ValueError(f"gate_up_proj_weight must be [E, H, 2, I] or [E, 2I, H], got "
+                         f"{tuple(gate_up.shape)}")
+    E, H, _, I = gate_up.shape
+    return E, H, I
 
 
 def routed_weights(gate_up, down, gate_up_scale=None, down_scale=None):
@@ -97,7 +125,8 @@ def routed_weights(gate_up, down, gate_up_scale=None, down_scale=None):
         s2 = _ones_scale(E, H, I, dev) if down_scale is None else down_scale.transpose(1, 2)
         return w13, s13.float().contiguous(), w2, s2.float().contiguous()
 
-    return _cached(("nf",) + _key(gate_up, down, gate_up_scale, down_scale), build)
+    srcs = (gate_up, down, gate_up_scale, down_scale)
+    return _cached(("nf",) + _key(*srcs), build, srcs)
 
 
 def shared_weights(gate_w, up_w, down_w, I):
@@ -136,7 +165,8 @@ def shared_weights(gate_w, up_w, down_w, I):
         return (w13s.contiguous(), s13s.float().contiguous(), w2s.contiguous(),
                 s2s.float().contiguous())
 
-    return _cached(("shared", I) + _key(gate_w, up_w, down_w), build)
+    srcs = (gate_w, up_w, down_w)
+    return _cached(("shared", I) + _key(*srcs), build, srcs)
 
 
 def make_weights(w13, s13, w2, s2, shared=None):

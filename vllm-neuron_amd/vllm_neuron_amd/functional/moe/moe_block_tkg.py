@@ -23,7 +23,8 @@ mapping -> fp8 experts -> combine. Routed experts are float8_e4m3fn with
 128x128 block scales (expert_gate_up_weights_scale / expert_down_weights_scale
 in the block-scale shapes); floating-point shared-expert weights are quantized
 once to the same format. router_mm_dtype is accepted for signature
-compatibility; the logits are always accumulated in fp32.
+compatibility; the logits are always accumulated in fp32. The GPU work is one
+torch.library operator (moe_fp8::moe_block_tkg), an opaque node under torch.compile.
 """
 from typing import Optional, Tuple
 
@@ -110,37 +111,62 @@ def moe_block_tkg(
         raise ValueError(f"router_weights must be [H, E] with H={H}, got "
                          f"{tuple(router_weights.shape)}")
     E_global = router_weights.shape[1]
-    w13, s13, w2, s2 = _experts.routed_weights(expert_gate_up_weights, expert_down_weights,
-                                                expert_gate_up_weights_scale,
-                                                expert_down_weights_scale)
-    E_L, I = w13.shape[0], w13.shape[1] // 2
-    if w13.shape[2] != H:
-        raise ValueError(f"expert weights have H={w13.shape[2]}, inp H={H}")
+    E_L, H_w, _ = _experts.weight_dims(expert_gate_up_weights, expert_down_weights)
+    if H_w != H:
+        raise ValueError(f"expert weights have H={H_w}, inp H={H}")
     if E_L != E_global:
         raise NotImplementedError(
             f"{E_L} local of {E_global} experts: expert-parallel slicing needs several GPUs; "
             "this build keeps every expert on one")
-    if rank_id is not None and int(torch.as_tensor(rank_id).reshape(-1)[0]) != 0:
+    if rank_id is not None and not torch.compiler.is_compiling() and \
+            int(torch.as_tensor(rank_id).reshape(-1)[0]) != 0:
         raise NotImplementedError("rank_id != 0: one GPU holds every expert")
     if not 1 <= top_k <= E_global:
         raise ValueError(f"top_k must be between 1 and {E_global}, got {top_k}")
     if x.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError(f"inp must be bfloat16 or float32, got {x.dtype}")
+    r = None
+    if residual is not None:
+        r = residual.reshape(-1, residual.shape[-1]) if residual.dim() == 3 else residual
+        if tuple(r.shape) != (T, H) or r.dtype != torch.bfloat16:
+            raise ValueError(f"residual must be bfloat16 [T, H] = [{T}, {H}], got "
+                             f"{r.dtype} {tuple(residual.shape)}")
+    out, logits, res_out = _block_tkg_op(
+        x, gamma, router_weights, expert_gate_up_weights, expert_down_weights,
+        expert_gate_up_weights_scale, expert_down_weights_scale, shared_expert_gate_w,
+        shared_expert_up_w, shared_expert_down_w, router_bias, r, int(top_k), float(eps),
+        0 if router_act_fn == RouterActFnType.SOFTMAX else 1, bool(router_pre_norm),
+        bool(norm_topk_prob), expert_affinities_scaling_mode == ExpertAffinityScaleMode.POST_SCALE,
+        0 if hidden_actual is None else int(hidden_actual))
+    # (output, router_logits[, residual_out]) as the reference's kernel path (:480)
+    res = (out,) if skip_router_logits else (out, logits)
+    if residual is not None:
+        res = res + (res_out.reshape(inp.shape),)
+    return res[0] if len(res) == 1 else res
 
+
+@torch.library.custom_op("moe_fp8::moe_block_tkg", mutates_args=())
+def _block_tkg_op(x: Tensor, gamma: Tensor, router_weights: Tensor, gate_up: Tensor,
+                  down: Tensor, gate_up_scale: Optional[Tensor], down_scale: Optional[Tensor],
+                  shared_gate: Optional[Tensor], shared_up: Optional[Tensor],
+                  shared_down: Optional[Tensor], router_bias: Optional[Tensor],
+                  residual: Optional[Tensor], top_k: int, eps: float, scoring: int,
+                  pre_norm: bool, norm_topk_prob: bool, post_scale: bool,
+                  hidden_actual: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """Opaque graph node of moe_block_tkg (arguments checked by moe_block_tkg).
+    Returns (out [T, H], logits [T, E] fp32, residual_out [T, H] or [0, H])."""
+    T, H = x.shape
+    ha = None if hidden_actual <= 0 else hidden_actual
+    w13, s13, w2, s2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
+    I = w13.shape[1] // 2
     # 1. (residual add, :341, :421-428) RMSNorm, cast back to the input dtype (:135-151).
     # bf16 input: one fused pass that also quantizes the normalized rows for the experts.
     xq = xs = res_out = None
     if x.dtype == torch.bfloat16:
-        r = None
-        if residual is not None:
-            r = residual.reshape(-1, residual.shape[-1]) if residual.dim() == 3 else residual
-            if tuple(r.shape) != (T, H) or r.dtype != torch.bfloat16:
-                raise ValueError(f"residual must be bfloat16 [T, H] = [{T}, {H}], got "
-                                 f"{r.dtype} {tuple(residual.shape)}")
-            r = r.contiguous()
-        xn, xq, xs, res_out = ops.rms_norm_quant(x.contiguous(), gamma, eps, hidden_actual, r)
+        r = None if residual is None else residual.contiguous()
+        xn, xq, xs, res_out = ops.rms_norm_quant(x.contiguous(), gamma, eps, ha, r)
     else:
-        xn = ops.rms_norm(x.contiguous(), gamma, eps, hidden_actual, out_dtype=x.dtype)
+        xn = ops.rms_norm(x.contiguous(), gamma, eps, ha, out_dtype=x.dtype)
     # 2. fp32 router matmul on the normalized values (:153-163)
     wt = router_weights.t()
     wt = wt if wt.is_contiguous() else wt.contiguous()
@@ -152,23 +178,30 @@ def moe_block_tkg(
             wt = wt.float().contiguous()
         logits = ops.router_logits_f32(xn.float().contiguous(), wt, bias)
     # 3. selection (:165-205)
-    order = ops.ORDER_ACT_TOPK if router_pre_norm else ops.ORDER_TOPK_ACT
-    scoring = "softmax" if router_act_fn == RouterActFnType.SOFTMAX else "sigmoid"
+    order = ops.ORDER_ACT_TOPK if pre_norm else ops.ORDER_TOPK_ACT
     ids, wts = ops.router_topk(logits, top_k, order, scoring, renorm=norm_topk_prob, eps=1e-20,
                                scale=1.0)
-    if expert_affinities_scaling_mode == ExpertAffinityScaleMode.NO_SCALE:
+    if not post_scale:
         wts = torch.ones_like(wts)
     # 4./5. routed experts (+ shared expert) on the normalized values
     shared = None
-    if shared_expert_gate_w is not None:
-        shared = _experts.shared_weights(shared_expert_gate_w, shared_expert_up_w,
-                                         shared_expert_down_w, I)
+    if shared_gate is not None:
+        shared = _experts.shared_weights(shared_gate, shared_up, shared_down, I)
     w = _experts.make_weights(w13, s13, w2, s2, shared)
     out = _experts.routed_forward(_experts.as_bf16(xn), ids, wts, w, xq=xq, xs=xs)
     if x.dtype != torch.bfloat16:
         out = out.to(x.dtype)
-    # (output, router_logits[, residual_out]) as the reference's kernel path (:480)
-    res = (out,) if skip_router_logits else (out, logits)
-    if res_out is not None:
-        res = res + (res_out.reshape(inp.shape),)
-    return res[0] if len(res) == 1 else res
+    if res_out is None:
+        res_out = x.new_empty(0, H, dtype=torch.bfloat16)
+    return out, logits, res_out
+
+
+@_block_tkg_op.register_fake
+def _block_tkg_fake(x, gamma, router_weights, gate_up, down, gate_up_scale, down_scale,
+                    shared_gate, shared_up, shared_down, router_bias, residual, top_k, eps,
+                    scoring, pre_norm, norm_topk_prob, post_scale, hidden_actual):
+    T, H = x.shape
+    E = router_weights.shape[1]
+    nres = 0 if residual is None or x.dtype != torch.bfloat16 else T
+    return (x.new_empty(T, H), x.new_empty(T, E, dtype=torch.float32),
+            x.new_empty(nres, H, dtype=torch.bfloat16))

@@ -4,7 +4,8 @@ Reference: vllm_neuron/functional/moe/moe_cte.py:35-437 (API and dispatch),
 :465-612 (_torch_moe_impl, the math):
     out[t] = sum_e affinity[t, e] * ( act(x_t W_g,e) * (x_t W_u,e) ) W_d,e
 summed in expert order, accumulated in fp32 (POST_SCALE), cast to the input
-dtype; T = expert_affinities_masked.shape[0] // E (:533-536).
+dtype; T = expert_affinities_masked.shape[0] // E (:533-536). The GPU work is one
+torch.library operator (moe_fp8::moe_cte), an opaque node under torch.compile.
 
 Compute path (all HIP): 1x128 fp8 activation quant -> row tiles of the given
 token_position_to_id / block_to_expert -> fp8 gate_up with SiLU * up and the
@@ -105,9 +106,7 @@ def moe_cte(
     if hidden_states.dim() != 2:
         raise ValueError(f"hidden_states must be [T, H] or [T+1, H], got {tuple(hidden_states.shape)}")
 
-    w13, s13, w2, s2 = _experts.routed_weights(gate_up_proj_weight, down_proj_weight,
-                                                gate_up_proj_scale, down_proj_scale)
-    E, H = w13.shape[0], w13.shape[2]
+    E, H, _ = _experts.weight_dims(gate_up_proj_weight, down_proj_weight)
     if hidden_states.shape[1] != H:
         raise ValueError(f"hidden_states has H={hidden_states.shape[1]}, weights H={H}")
     if expert_affinities_masked.numel() % E:
@@ -125,8 +124,26 @@ def moe_cte(
                          f"{N} blocks of {B}")
     if tpid.dtype != torch.int32 or b2e.dtype != torch.int32:
         raise ValueError("token_position_to_id and block_to_expert must be int32")
-    tpid, b2e = tpid.contiguous(), b2e.contiguous()
+    no_scale = expert_affinities_scaling_mode == ExpertAffinityScaleMode.NO_SCALE
+    return _moe_cte_op(hidden_states, expert_affinities_masked, gate_up_proj_weight,
+                       down_proj_weight, gate_up_proj_scale, down_proj_scale, tpid, b2e, B,
+                       no_scale)
 
+
+@torch.library.custom_op("moe_fp8::moe_cte", mutates_args=())
+def _moe_cte_op(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up: Tensor,
+                down: Tensor, gate_up_scale: Optional[Tensor], down_scale: Optional[Tensor],
+                token_position_to_id: Tensor, block_to_expert: Tensor, block_size: int,
+                no_scale: bool) -> Tensor:
+    """Opaque graph node of moe_cte (arguments checked by moe_cte): the experts of a
+    mapping, combined per token with the dense affinities in expert order."""
+    w13, s13, w2, s2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
+    E, H = w13.shape[0], w13.shape[2]
+    T = expert_affinities_masked.numel() // E
+    B = block_size
+    tpid = token_position_to_id.contiguous()
+    b2e = block_to_expert.contiguous()
+    N = b2e.numel()
     x = _experts.as_bf16(hidden_states[:T]).contiguous()
     w = _experts.make_weights(w13, s13, w2, s2)
     # Expected routed rows per token from the mapping size (N ~ T*K/B + E - 1);
@@ -135,7 +152,15 @@ def moe_cte(
     y, NB = _experts.run_experts(x, tpid, b2e, B, k_rows, E, w)
     inv = ops.invert_mapping(tpid, b2e, B, T, E)  # [T, E] slot of (t, e) or -1
     aff = expert_affinities_masked.reshape(T, E).float()
-    if expert_affinities_scaling_mode == ExpertAffinityScaleMode.NO_SCALE:
+    if no_scale:
         aff = (aff != 0).float()  # moe_block_tkg.py:280-289 binary weights
     out = ops.combine(y, inv, aff.contiguous(), T, H, NB, 0)
     return out if hidden_states.dtype == torch.bfloat16 else out.to(hidden_states.dtype)
+
+
+@_moe_cte_op.register_fake
+def _moe_cte_fake(hidden_states, expert_affinities_masked, gate_up, down, gate_up_scale,
+                  down_scale, token_position_to_id, block_to_expert, block_size, no_scale):
+    E, H, _ = _experts.weight_dims(gate_up, down)
+    T = expert_affinities_masked.numel() // E
+    return hidden_states.new_empty(T, H)

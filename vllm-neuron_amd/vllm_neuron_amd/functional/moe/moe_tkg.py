@@ -72,20 +72,18 @@ def moe_tkg(
         raise NotImplementedError(f"moe_tkg: {', '.join(bad)} not supported by this build")
     if hidden_input.dim() != 2:
         raise ValueError(f"hidden_input must be [T, H], got {tuple(hidden_input.shape)}")
-    w13, s13, w2, s2 = _experts.routed_weights(expert_gate_up_weights, expert_down_weights,
-                                                expert_gate_up_weights_scale,
-                                                expert_down_weights_scale)
-    E_L = w13.shape[0]
+    E_L, H_w, _ = _experts.weight_dims(expert_gate_up_weights, expert_down_weights)
     T, H = hidden_input.shape
-    if H != w13.shape[2]:
-        raise ValueError(f"hidden_input has H={H}, weights H={w13.shape[2]}")
+    if H != H_w:
+        raise ValueError(f"hidden_input has H={H}, weights H={H_w}")
     if expert_affinities.dim() != 2 or expert_affinities.shape[0] != T:
         raise ValueError(f"expert_affinities must be [T, E], got {tuple(expert_affinities.shape)}")
     if expert_affinities.shape[1] != E_L:
         raise NotImplementedError(
             f"expert_affinities has {expert_affinities.shape[1]} experts, the weights {E_L}: "
             "expert-parallel slicing needs several GPUs; this build keeps every expert on one")
-    if rank_id is not None and int(torch.as_tensor(rank_id).reshape(-1)[0]) != 0:
+    if rank_id is not None and not torch.compiler.is_compiling() and \
+            int(torch.as_tensor(rank_id).reshape(-1)[0]) != 0:
         raise NotImplementedError("rank_id != 0: one GPU holds every expert")
     aff = expert_affinities.float()
     post = expert_affinities_scaling_mode == ExpertAffinityScaleMode.POST_SCALE
@@ -103,8 +101,26 @@ def moe_tkg(
             raise ValueError(f"expert_index must be [T, K], got {tuple(expert_index.shape)}")
         ids = expert_index.to(torch.int32)
         wts = aff.gather(1, ids.long()) if post else torch.ones(ids.shape, device=aff.device)
+    od = output_dtype if output_dtype is not None else hidden_input.dtype
+    return _moe_tkg_op(hidden_input, expert_gate_up_weights, expert_down_weights,
+                       expert_gate_up_weights_scale, expert_down_weights_scale,
+                       ids.contiguous(), wts.float().contiguous(), od)
+
+
+@torch.library.custom_op("moe_fp8::moe_tkg", mutates_args=())
+def _moe_tkg_op(hidden_input: Tensor, gate_up: Tensor, down: Tensor,
+                gate_up_scale: Optional[Tensor], down_scale: Optional[Tensor], ids: Tensor,
+                wts: Tensor, output_dtype: torch.dtype) -> Tensor:
+    """Opaque graph node of moe_tkg (arguments checked by moe_tkg): experts ids [T, K]
+    weighted by wts [T, K], combined per token in k order."""
+    w13, s13, w2, s2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
     x = _experts.as_bf16(hidden_input).contiguous()
     w = _experts.make_weights(w13, s13, w2, s2)
-    out = _experts.routed_forward(x, ids.contiguous(), wts.float().contiguous(), w)
-    od = output_dtype if output_dtype is not None else hidden_input.dtype
-    return out if od == torch.bfloat16 else out.to(od)
+    out = _experts.routed_forward(x, ids, wts, w)
+    return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
+
+
+@_moe_tkg_op.register_fake
+def _moe_tkg_fake(hidden_input, gate_up, down, gate_up_scale, down_scale, ids, wts,
+                  output_dtype):
+    return hidden_input.new_empty(hidden_input.shape, dtype=output_dtype)

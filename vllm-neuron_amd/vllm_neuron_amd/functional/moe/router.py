@@ -106,8 +106,10 @@ def router_logits(hidden_states, router_weights, router_bias=None, gamma=None, e
     x = hidden_states.to(computation_dtype)
     if gamma is not None:
         if x.dtype == torch.float16:
-            x = x.float()
-        x = ops.rms_norm(x.contiguous(), gamma, eps)  # output in x's dtype (router.py:681-688)
+            # fp32 norm, then the fp16 rounding _torch_rms_norm's cast back applies
+            x = ops.rms_norm(x.float().contiguous(), gamma, eps).half()
+        else:
+            x = ops.rms_norm(x.contiguous(), gamma, eps)  # output in x's dtype (router.py:681-688)
     wt = router_weights.t()
     if not wt.is_contiguous():
         wt = wt.contiguous()
@@ -115,14 +117,39 @@ def router_logits(hidden_states, router_weights, router_bias=None, gamma=None, e
     if x.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16:
         logits = ops.router_logits(x.contiguous(), wt, bias)
     else:
+        if computation_dtype != torch.float32 and wt.dtype != computation_dtype:
+            # F.linear's operands are router_weights.to(computation_dtype) (router.py:419-424)
+            wt = wt.to(computation_dtype)
         if wt.dtype not in (torch.float32, torch.bfloat16):
-            wt = wt.to(torch.float32)
-        if computation_dtype != torch.float32 and wt.dtype == torch.float32:
-            wt = wt.to(computation_dtype).float()  # operands rounded to the computation dtype
+            wt = wt.to(torch.float32)  # exact: fp16 values are fp32 values
         logits = ops.router_logits_f32(x.float().contiguous(), wt.contiguous(), bias)
     if computation_dtype != torch.float32:
         logits = logits.to(computation_dtype).float()  # F.linear's output rounding
     return logits
+
+
+@torch.library.custom_op("moe_fp8::router", mutates_args=())
+def _router_op(hidden_states: Tensor, router_weights: Tensor, top_k: int,
+               router_bias: Optional[Tensor], scoring: int, gamma: Optional[Tensor], eps: float,
+               computation_dtype: torch.dtype, order: int, renorm: bool) -> Tuple[Tensor, Tensor]:
+    """Opaque graph node of router(): logits -> top-k -> dense affinities on the GPU.
+    hidden_states [T, H] (already un-transposed), router_weights [H, E]."""
+    logits = router_logits(hidden_states, router_weights, router_bias, gamma, eps,
+                           computation_dtype)
+    _, _, aff = ops.router_topk(logits, top_k, order, scoring, renorm=renorm, eps=0.0, scale=1.0,
+                                dense=True)
+    if computation_dtype != torch.float32:
+        aff = aff.to(computation_dtype)
+        logits = logits.to(computation_dtype)
+    return aff, logits
+
+
+@_router_op.register_fake
+def _router_fake(hidden_states, router_weights, top_k, router_bias, scoring, gamma, eps,
+                 computation_dtype, order, renorm):
+    T, E = hidden_states.shape[0], router_weights.shape[1]
+    return (hidden_states.new_empty(T, E, dtype=computation_dtype),
+            hidden_states.new_empty(T, E, dtype=computation_dtype))
 
 
 def router(
@@ -145,13 +172,13 @@ def router(
 ) -> Union[Tensor, Tuple[Tensor, Tensor]]:
     """Expert affinities [T, E] (zeros for unselected experts), and the raw logits
     [T, E] when return_logits. Same arguments as router.py:72-89; see the module
-    docstring for the compute path."""
+    docstring for the compute path. The GPU work is one torch.library operator
+    (moe_fp8::router), an opaque node under torch.compile."""
     _validate_router_inputs(hidden_states, router_weights, top_k, router_bias, gamma,
                             computation_dtype, router_computation_order,
                             transposed_hidden_states)
     scoring = _scoring(activation)
     x = hidden_states.t() if transposed_hidden_states else hidden_states
-    logits = router_logits(x, router_weights, router_bias, gamma, eps, computation_dtype)
     O = RouterComputationOrder
     if router_computation_order == O.PRENORM_LINEAR_ACT_TOPK_RENORM_SCATTER:
         order, renorm = ops.ORDER_ACT_TOPK, True
@@ -160,11 +187,8 @@ def router(
         # softmax of the k values, and sigmoid(-inf) = 0, so it selects and weighs
         # as TOPK_ACT does (router.py:507-566 vs :384-441).
         order, renorm = ops.ORDER_TOPK_ACT, False
-    _, _, aff = ops.router_topk(logits, top_k, order, scoring, renorm=renorm, eps=0.0, scale=1.0,
-                                dense=True)
-    if computation_dtype != torch.float32:
-        aff = aff.to(computation_dtype)
-        logits = logits.to(computation_dtype)
+    aff, logits = _router_op(x.contiguous(), router_weights, int(top_k), router_bias, scoring,
+                             gamma, float(eps), computation_dtype, order, renorm)
     if return_logits:
         return aff, logits
     return aff
