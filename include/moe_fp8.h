@@ -249,6 +249,29 @@ int moe_layer_forward(const void* x_bf16, const void* residual_bf16, const float
                       void* residual_out_bf16, int32_t* ids_out, float* weights_out,
                       float* logits_out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* moe_layer_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid allocation). No counterpart in the reference. Its workspace is a static
+ * device array of MOE_NOALLOC_SCRATCH_BYTES, one per GPU, held from the first
+ * call on that GPU until the process ends; the call allocates nothing. Calls
+ * whose moe_layer_workspace_bytes exceeds it return MOE_ERR_UNSUPPORTED (64 MiB
+ * covers the DeepSeek-V3 / Kimi-K2 layers up to about 320 tokens). All calls on
+ * one GPU share the array: calls that overlap on one GPU (unordered streams,
+ * host threads) race and must be serialized by the caller. The device current
+ * on the calling thread must be the stream's device. */
+#define MOE_NOALLOC_SCRATCH_BYTES (64 << 20)
+int moe_layer_forward_noalloc(const void* x_bf16, const void* residual_bf16, const float* gamma,
+                              float eps, int hidden_actual, int T, int H, int I, int E, int K,
+                              int n_shared, const void* router_w_bf16, const float* router_bias,
+                              const float* corr_bias, int order, int scoring, int n_group,
+                              int topk_group, int renorm, float renorm_eps, float routed_scale,
+                              const uint8_t* w13, const float* w13_scale, const uint8_t* w2,
+                              const float* w2_scale, const uint8_t* w13_shared,
+                              const float* w13_shared_scale, const uint8_t* w2_shared,
+                              const float* w2_shared_scale, int B, void* out_bf16,
+                              void* residual_out_bf16, int32_t* ids_out, float* weights_out,
+                              float* logits_out, void* stream);
+
 /* ---- diagnostics ----------------------------------------------------------- */
 
 /* shape 0: c[16,16] = decode(a[16,128]) . decode(b[16,128])^T through one

@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -129,19 +131,20 @@ extern "C" size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, i
   return carve(nullptr, T, H, I, E, K, n_shared, B, norm != 0).bytes;
 }
 
-extern "C" int moe_layer_forward(const void* x_bf16, const void* residual_bf16,
-                                 const float* gamma, float eps, int hidden_actual, int T, int H,
-                                 int I, int E, int K, int n_shared, const void* router_w_bf16,
-                                 const float* router_bias, const float* corr_bias, int order,
-                                 int scoring, int n_group, int topk_group, int renorm,
-                                 float renorm_eps, float routed_scale, const uint8_t* w13,
-                                 const float* w13_scale, const uint8_t* w2, const float* w2_scale,
-                                 const uint8_t* w13_shared, const float* w13_shared_scale,
-                                 const uint8_t* w2_shared, const float* w2_shared_scale, int B,
-                                 void* out_bf16, void* residual_out_bf16, int32_t* ids_out,
-                                 float* weights_out, float* logits_out, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
-  MOE_API_BEGIN("moe_layer_forward");
+// The layer forward of both entry points: `workspace` is the caller's buffer or
+// this device's static scratch. _moe_fn names the entry point in error messages.
+static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const void* residual_bf16,
+                              const float* gamma, float eps, int hidden_actual, int T, int H,
+                              int I, int E, int K, int n_shared, const void* router_w_bf16,
+                              const float* router_bias, const float* corr_bias, int order,
+                              int scoring, int n_group, int topk_group, int renorm,
+                              float renorm_eps, float routed_scale, const uint8_t* w13,
+                              const float* w13_scale, const uint8_t* w2, const float* w2_scale,
+                              const uint8_t* w13_shared, const float* w13_shared_scale,
+                              const uint8_t* w2_shared, const float* w2_shared_scale, int B,
+                              void* out_bf16, void* residual_out_bf16, int32_t* ids_out,
+                              float* weights_out, float* logits_out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   MOE_CHECK_ARG(x_bf16 && router_w_bf16 && w13 && w13_scale && w2 && w2_scale && out_bf16 && workspace,
                 "null pointer argument");
   MOE_CHECK_ARG(T > 0 && E > 0 && K > 0 && K <= E && B > 0 && n_shared >= 0,
@@ -229,4 +232,90 @@ extern "C" int moe_layer_forward(const void* x_bf16, const void* residual_bf16,
   MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)R, n_shared, out_bf16, stream));
 #undef MOE_STEP
   return MOE_OK;
+}
+
+extern "C" int moe_layer_forward(const void* x_bf16, const void* residual_bf16,
+                                 const float* gamma, float eps, int hidden_actual, int T, int H,
+                                 int I, int E, int K, int n_shared, const void* router_w_bf16,
+                                 const float* router_bias, const float* corr_bias, int order,
+                                 int scoring, int n_group, int topk_group, int renorm,
+                                 float renorm_eps, float routed_scale, const uint8_t* w13,
+                                 const float* w13_scale, const uint8_t* w2, const float* w2_scale,
+                                 const uint8_t* w13_shared, const float* w13_shared_scale,
+                                 const uint8_t* w2_shared, const float* w2_shared_scale, int B,
+                                 void* out_bf16, void* residual_out_bf16, int32_t* ids_out,
+                                 float* weights_out, float* logits_out, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  MOE_API_BEGIN("moe_layer_forward");
+  return layer_forward_impl(_moe_fn, x_bf16, residual_bf16, gamma, eps, hidden_actual, T, H, I, E,
+                            K, n_shared, router_w_bf16, router_bias, corr_bias, order, scoring,
+                            n_group, topk_group, renorm, renorm_eps, routed_scale, w13, w13_scale,
+                            w2, w2_scale, w13_shared, w13_shared_scale, w2_shared,
+                            w2_shared_scale, B, out_bf16, residual_out_bf16, ids_out, weights_out,
+                            logits_out, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free layer forward. Its workspace is `scratch`, one static array per
+// GPU that the code object's loader places in device memory and that lives until
+// the process ends. In host code `scratch` names a host-side shadow, not device
+// memory, so its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and only that address is handed
+// to kernels. Calls on one GPU share the array: they must not overlap (same
+// stream or otherwise ordered), and nothing in it has to start at zero (every
+// kernel of the layer writes what it later reads; the mapping clears its own
+// status word).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+namespace moe {
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices];
+
+// Device address of this device's `scratch` (looked up on the first call per device).
+static int scratch_address(const char* _moe_fn, void** out) {
+  int dev = -1;
+  MOE_CHECK_HIP(hipGetDevice(&dev));
+  MOE_CHECK_SUPPORTED(dev >= 0 && dev < kMaxDevices, "device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    MOE_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    MOE_CHECK_ARG(p != nullptr && ((uintptr_t)p & 255) == 0, "bad scratch address");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return MOE_OK;
+}
+
+}  // namespace moe
+
+extern "C" int moe_layer_forward_noalloc(
+    const void* x_bf16, const void* residual_bf16, const float* gamma, float eps,
+    int hidden_actual, int T, int H, int I, int E, int K, int n_shared, const void* router_w_bf16,
+    const float* router_bias, const float* corr_bias, int order, int scoring, int n_group,
+    int topk_group, int renorm, float renorm_eps, float routed_scale, const uint8_t* w13,
+    const float* w13_scale, const uint8_t* w2, const float* w2_scale, const uint8_t* w13_shared,
+    const float* w13_shared_scale, const uint8_t* w2_shared, const float* w2_shared_scale, int B,
+    void* out_bf16, void* residual_out_bf16, int32_t* ids_out, float* weights_out,
+    float* logits_out, void* stream) {
+  MOE_API_BEGIN("moe_layer_forward_noalloc");
+  MOE_CHECK_ARG(T > 0 && H > 0 && I > 0 && E > 0 && K > 0 && B > 0 && n_shared >= 0,
+                "bad sizes T=%d H=%d I=%d E=%d K=%d B=%d", T, H, I, E, K, B);
+  const size_t need = moe_layer_workspace_bytes(T, H, I, E, K, n_shared, B, gamma != nullptr);
+  MOE_CHECK_SUPPORTED(need <= (size_t)MOE_NOALLOC_SCRATCH_BYTES,
+                      "this layer call needs %zu bytes of scratch; the static scratch holds %zu "
+                      "(use moe_layer_forward with a workspace)",
+                      need, (size_t)MOE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_address(_moe_fn, &ws);
+  if (rc != MOE_OK) return rc;
+  return layer_forward_impl(_moe_fn, x_bf16, residual_bf16, gamma, eps, hidden_actual, T, H, I, E,
+                            K, n_shared, router_w_bf16, router_bias, corr_bias, order, scoring,
+                            n_group, topk_group, renorm, renorm_eps, routed_scale, w13, w13_scale,
+                            w2, w2_scale, w13_shared, w13_shared_scale, w2_shared,
+                            w2_shared_scale, B, out_bf16, residual_out_bf16, ids_out, weights_out,
+                            logits_out, ws, (size_t)MOE_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -12,6 +12,7 @@ import threading
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libmoe_fp8.so")
 ABI_VERSION = 2
+NOALLOC_SCRATCH_BYTES = 64 << 20  # MOE_NOALLOC_SCRATCH_BYTES
 
 MOE_OK, MOE_ERR_ARG, MOE_ERR_UNSUPPORTED, MOE_ERR_HIP = 0, -1, -2, -3
 
@@ -48,6 +49,9 @@ PROTOTYPES = {
     "moe_layer_forward": (_i, [_p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _i, _i,
                                _i, _i, _f, _f, _p, _p, _p, _p, _p, _p, _p, _p, _i, _p, _p, _p, _p,
                                _p, _p, _sz, _p]),
+    "moe_layer_forward_noalloc": (_i, [_p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _i,
+                                       _i, _i, _i, _i, _f, _f, _p, _p, _p, _p, _p, _p, _p, _p, _i,
+                                       _p, _p, _p, _p, _p, _p]),
     "moe_max_block_tiles": (_i, [_i, _i, _i, _i, _i, _i]),
     "moe_block_tiles_workspace_bytes": (_sz, [_i, _i]),
     "moe_build_block_tiles": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _i, _p, _p, _sz, _p]),

@@ -418,3 +418,41 @@ def layer_forward(x, w, cfg, return_routing=False, gamma=None, eps=1e-6, hidden_
     if return_routing:
         res = res + (ids, wts, lg)
     return res[0] if len(res) == 1 else res
+
+
+def layer_forward_noalloc(x, w, cfg, return_routing=False, gamma=None, eps=1e-6,
+                          hidden_actual=None, residual=None):
+    """layer_forward through moe_layer_forward_noalloc: the library's static per-GPU
+    scratch replaces the workspace, so only the outputs are allocated here (by the
+    caller, in code that must not allocate). Same arguments and results."""
+    _need_cuda(x, w.w13, gamma, residual)
+    T, H = x.shape
+    _need(x, torch.bfloat16, (T, H), "hidden_states")
+    if residual is not None:
+        _need(residual, torch.bfloat16, (T, H), "residual")
+    g = None
+    if gamma is not None:
+        g = gamma.reshape(-1).to(torch.float32).contiguous()
+        if g.numel() != H:
+            raise ValueError(f"gamma must hold H={H} values, got shape {tuple(gamma.shape)}")
+    E, I = w.n_experts, w.intermediate
+    K, S, B = cfg.top_k, w.n_shared, cfg.block_size
+    out = torch.empty(T, H, device=x.device, dtype=torch.bfloat16)
+    rsum = torch.empty_like(x) if residual is not None else None
+    ids = torch.empty(T, K, device=x.device, dtype=torch.int32) if return_routing else None
+    wts = torch.empty(T, K, device=x.device, dtype=torch.float32) if return_routing else None
+    lg = torch.empty(T, E, device=x.device, dtype=torch.float32) if return_routing else None
+    order = ORDER_GROUPED if cfg.grouped else ORDER_TOPK_ACT
+    ha = 0 if hidden_actual is None else int(hidden_actual)
+    _lib.call("moe_layer_forward_noalloc", ptr(x), ptr(residual), ptr(g), float(eps), ha, T, H, I,
+              E, K, S, ptr(w.router_w), ptr(w.router_bias), ptr(w.corr_bias), order,
+              SCORING[cfg.scoring], cfg.n_group, cfg.topk_group, int(cfg.renorm), 1e-20,
+              float(cfg.routed_scaling), ptr(_u8(w.w13)), ptr(w.w13_scale), ptr(_u8(w.w2)),
+              ptr(w.w2_scale), ptr(_u8(w.shared_w13)) if S else None,
+              ptr(w.shared_w13_scale) if S else None, ptr(_u8(w.shared_w2)) if S else None,
+              ptr(w.shared_w2_scale) if S else None, B, ptr(out), ptr(rsum), ptr(ids), ptr(wts),
+              ptr(lg), _stream())
+    res = (out,) if residual is None else (out, rsum)
+    if return_routing:
+        res = res + (ids, wts, lg)
+    return res[0] if len(res) == 1 else res
