@@ -272,6 +272,54 @@ int moe_layer_forward_noalloc(const void* x_bf16, const void* residual_bf16, con
                               void* residual_out_bf16, int32_t* ids_out, float* weights_out,
                               float* logits_out, void* stream);
 
+/* ---- MX (microscaling) experts ------------------------------------------- */
+
+/* OCP MX formats (MX v1.0): 32 consecutive values along K share one E8M0 scale
+ * byte (2^(b - 127)). Expert weights are MXFP4 (E2M1, two codes per byte, the low
+ * nibble first: the HF GPT-OSS packing) or MXFP8 (E4M3); activations are MXFP8.
+ * Layouts: w13 [E, 2I, H/2] (fp4) or [E, 2I, H] (fp8), gate rows [0, I) then up
+ * rows; w13_scale [E, 2I, H/32]; w2 [E, H, I/2] or [E, H, I]; w2_scale
+ * [E, H, I/32]; biases fp32 b13 [E, 2I], b2 [E, H] (optional). The reference holds
+ * GPT-OSS's MXFP4 experts in a Trainium tiling (moe_cte.py:122-130, :178-191;
+ * model/gpt_oss/weight_loaders_mxfp4.py:301-560), converted from the same HF
+ * checkpoint tensors this layout stacks. */
+#define MOE_MX_FP8 0
+#define MOE_MX_FP4 1
+#define MOE_ACT_SILU 0
+#define MOE_ACT_SWISH 1 /* g * sigmoid(1.702 g), moe_cte.py:459-461 */
+
+/* MXFP8 quantization of bf16 rows [rows, cols] (cols % 32 == 0): e =
+ * max(floor(log2(amax)) - 8, -127) per 32-value block, scale byte e + 127,
+ * codes RNE_e4m3(clamp(x * 2^-e, +-448)). The activation quantization of the MX
+ * path (the reference quantizes hidden rows to MX inside its fused prefill
+ * kernel, model_mxfp4.py:1584-1605). */
+int moe_act_quant_mx(const void* x_bf16, int rows, int cols, uint8_t* q, uint8_t* scales,
+                     void* stream);
+
+/* MX gate_up over row tiles (tiles as moe_build_tiles): gate = clamp(x W_g^T + b_g,
+ * gate_lo, gate_hi), up = clamp(x W_u^T + b_u, up_lo, up_hi) (NaN limit = none),
+ * h = act(gate) * up, written MXFP8-quantized per 32 columns (hq [rows, I] codes,
+ * hs [rows, I/32] scale bytes). Replaces the gate/up half of nkilib's
+ * shard_on_block_mx moe_cte (moe_cte.py:356-421) with the math of _torch_moe_impl
+ * (moe_cte.py:557-575: biases :562-564, clamps :567-571, Swish :459-461). */
+int moe_expert_gate_up_mx(const uint8_t* xq, const uint8_t* xs, int T, int H, int I, int E,
+                          int wfmt, const uint8_t* w13, const uint8_t* w13_scale,
+                          const float* b13, const uint8_t* w13_shared,
+                          const uint8_t* w13_shared_scale, const float* b13_shared, int n_shared,
+                          const int32_t* token_position_to_id, int NB, const int32_t* tiles,
+                          const int32_t* num_tiles, int max_tiles, int mt, int act, float gate_lo,
+                          float gate_hi, float up_lo, float up_hi, uint8_t* hq, uint8_t* hs,
+                          void* stream);
+
+/* MX down: y[row, :H] = bf16(h W_d^T + b_d) per tile row (unweighted). Replaces the
+ * down projection and its bias of moe_cte (moe_cte.py:585-591). */
+int moe_expert_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E, int wfmt,
+                       const uint8_t* w2, const uint8_t* w2_scale, const float* b2,
+                       const uint8_t* w2_shared, const uint8_t* w2_shared_scale,
+                       const float* b2_shared, int n_shared, int NB, const int32_t* tiles,
+                       const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
+                       void* stream);
+
 /* ---- diagnostics ----------------------------------------------------------- */
 
 /* shape 0: c[16,16] = decode(a[16,128]) . decode(b[16,128])^T through one
@@ -306,6 +354,13 @@ int moe_selftest_bf16_encode(uint32_t first, uint32_t count, uint32_t* out, int 
  * the quantizer's scale max(amax, 1e-10) / 448 as divisor. Mode 1: u seeds a
  * random fp32 amax in [2^-40, 2^40) and a value of magnitude at most amax.
  * Output as moe_selftest_fp8_encode. No reference counterpart. */
+/* One scaled MFMA with the MX GEMMs' lane mapping: c[16,16] = A . B^T with A
+ * [16,128] fp8 codes and scale bytes sa [16,4], B [16,128] values as fp4 (packed
+ * [16,64] bytes) or fp8 ([16,128]) with sb [16,4]. No reference counterpart: it
+ * pins the gfx950 scaled-MFMA data and scale layout for the tests. */
+int moe_selftest_mfma_mx(const uint8_t* a, const uint8_t* sa, const uint8_t* b, const uint8_t* sb,
+                         int wfmt, float* c, void* stream);
+
 int moe_selftest_quant_div(int mode, uint32_t first, uint32_t count, uint32_t* out, int blocks,
                            void* stream);
 

@@ -1,0 +1,152 @@
+"""GPU parity of the MX (microscaling) expert path: MXFP4 / MXFP8 weights, MXFP8
+activations and E8M0 scales applied by gfx950's scaled MFMA, with GPT-OSS's Swish,
+clamps and biases (moe_cte.py:440-612), against the oracle (oracle/mx.py).
+
+Gates: MXFP8 activation codes and scale bytes bit-exact; one scaled MFMA within fp32
+summation rounding of the float64 product; expert and layer outputs rel-L2 <= 1e-2
+against the oracle on the same MX operands."""
+import numpy as np
+import pytest
+import torch
+
+from _util import np_f32, rel_l2, say
+from oracle import mx as OX
+from oracle.fp8 import e4m3fn_decode
+from vllm_neuron_amd import ops
+from vllm_neuron_amd.weights_mx import MxMoEWeights, quant_mx_weight
+
+pytestmark = pytest.mark.gpu
+TOL_REL_L2 = 1e-2
+LIMIT = 7.0  # GPT-OSS swiglu_limit (model/gpt_oss/config.py:62)
+
+
+def _np_u8(t):
+    return t.view(torch.uint8).cpu().numpy() if t.dtype == torch.float8_e4m3fn else t.cpu().numpy()
+
+
+def _rand_fp8_codes(g, shape):
+    c = torch.randint(0, 256, shape, generator=g, dtype=torch.int32)
+    c[(c & 0x7F) == 0x7F] = 0x3F  # no NaN codes
+    return c.to(torch.uint8)
+
+
+def _scaled_mfma_case(cuda, fmt, g, a, sa, sb, small):
+    if fmt == "fp4":
+        bc = torch.randint(0, 16, (16, 128), generator=g, dtype=torch.int32).to(torch.uint8)
+        b = (bc[:, 0::2] | (bc[:, 1::2] << 4)).contiguous()
+        bval = OX.fp4_decode(bc.numpy())
+    elif small:
+        bv = torch.randint(-8, 9, (16, 128), generator=g).float()
+        b = bv.to(torch.float8_e4m3fn).view(torch.uint8)
+        bval = bv.numpy()
+    else:
+        b = _rand_fp8_codes(g, (16, 128))
+        bval = e4m3fn_decode(b.numpy())
+    c = ops.selftest_mfma_mx(a.to(cuda), sa.to(cuda), b.to(cuda), sb.to(cuda), fmt).cpu().numpy()
+    A = OX.dequant_mx(e4m3fn_decode(a.numpy()), sa.numpy())
+    B = OX.dequant_mx(bval, sb.numpy())
+    return c, A @ B.T, np.abs(A) @ np.abs(B).T
+
+
+@pytest.mark.parametrize("fmt", ["fp4", "fp8"])
+def test_scaled_mfma_layout(cuda, fmt):
+    """One v_mfma_scale_f32_16x16x128_f8f6f4 with the GEMMs' lane mapping against the
+    float64 product of the dequantized operands: pins the fp8 and fp4 operand layouts,
+    the fp4 nibble order, the scale lanes and E8M0. Small integers and scales 2^-1..2^1
+    keep every partial sum exact, so that case is bit for bit; over the full fp8 range
+    the MFMA's internal accumulation is compared as in the unscaled fp8 test."""
+    say("scaled mfma", fmt)
+    g = torch.Generator().manual_seed(1 if fmt == "fp4" else 2)
+    av = torch.randint(-8, 9, (16, 128), generator=g).float()
+    a = av.to(torch.float8_e4m3fn).view(torch.uint8)
+    sa = torch.randint(126, 129, (16, 4), generator=g, dtype=torch.int32).to(torch.uint8)
+    sb = torch.randint(126, 129, (16, 4), generator=g, dtype=torch.int32).to(torch.uint8)
+    c, ref, _ = _scaled_mfma_case(cuda, fmt, g, a, sa, sb, small=True)
+    assert np.array_equal(c, ref)
+    a = _rand_fp8_codes(g, (16, 128))
+    sa = torch.randint(110, 145, (16, 4), generator=g, dtype=torch.int32).to(torch.uint8)
+    sb = torch.randint(110, 145, (16, 4), generator=g, dtype=torch.int32).to(torch.uint8)
+    c, ref, bound = _scaled_mfma_case(cuda, fmt, g, a, sa, sb, small=False)
+    err = np.abs(c - ref) / (bound + 1e-30)
+    say("scaled mfma wide-range max error / sum|products|", float(err.max()))
+    assert err.max() < 1e-3
+
+
+@pytest.mark.parametrize("R,C", [(1, 32), (37, 512), (300, 3072)])
+def test_act_quant_mx_bit_exact(cuda, R, C):
+    """MXFP8 codes and E8M0 bytes equal the oracle's OCP quantizer, including all-zero
+    blocks and blocks spanning many binades."""
+    say("act quant mx", R, C)
+    g = torch.Generator().manual_seed(R + C)
+    x = torch.randn(R, C, generator=g) * torch.exp2(torch.randint(-20, 20, (R, 1), generator=g).float())
+    x[0, :32] = 0.0
+    if C >= 64:
+        x[-1, 32:64] = torch.exp2(torch.arange(32).float() - 16)  # 32 binades in one block
+    xb = x.to(torch.bfloat16)
+    q, s = ops.act_quant_mx(xb.to(cuda))
+    oq, os_ = OX.quant_mxfp8(np_f32(xb))
+    assert np.array_equal(_np_u8(q), oq)
+    assert np.array_equal(s.cpu().numpy(), os_)
+
+
+def make_mx_weights(E, H, I, seed, device, fmt="fp4", bias=True):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    w13 = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(device)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.02).to(device)
+    q13, s13 = quant_mx_weight(w13, fmt)
+    q2, s2 = quant_mx_weight(w2, fmt)
+    b13 = b2 = None
+    if bias:
+        b13 = (torch.randn(E, 2 * I, generator=g) * 0.1).to(device)
+        b13[:, I:] += 1.0  # the +1 the reference's loaders fold into the up bias
+        b2 = (torch.randn(E, H, generator=g) * 0.1).to(device)
+    rw = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(device)
+    rb = (torch.randn(E, generator=g) * 0.1).to(device)
+    return MxMoEWeights(router_w=rw, w13=q13, w13_scale=s13, w2=q2, w2_scale=s2, b13=b13, b2=b2,
+                        router_bias=rb, fmt=fmt).validate()
+
+
+def oracle_mx_weights(w):
+    """numpy operands of the oracle: packed fp4 (or fp8 codes), scales, biases."""
+    cv = _np_u8
+    return (cv(w.w13), cv(w.w13_scale), None if w.b13 is None else np_f32(w.b13), cv(w.w2),
+            cv(w.w2_scale), None if w.b2 is None else np_f32(w.b2))
+
+
+def oracle_layer(x, ids, wts, w, act, gl, ul, experts=None):
+    q13, s13, b13, q2, s2, b2 = oracle_mx_weights(w)
+    if w.fmt == "fp4":
+        return OX.moe_sparse_mx(np_f32(x), ids, wts, q13, s13, b13, q2, s2, b2, act, gl, ul, experts)
+    # fp8 weights: dequantize the codes with the same helper path
+    xhat = OX.dequant_mxfp8(*OX.quant_mxfp8(np_f32(x)))
+    out = np.zeros(x.shape, np.float32)
+    for e in (range(w.n_experts) if experts is None else sorted(experts)):
+        sel = ids == e
+        rows = np.nonzero(sel.any(axis=1))[0]
+        if rows.size == 0:
+            continue
+        wt = (wts * sel).sum(axis=1)[rows].astype(np.float32)
+        y = OX.expert_mlp_mx(xhat[rows], OX.dequant_mxfp8(q13[e], s13[e]), b13[e],
+                             OX.dequant_mxfp8(q2[e], s2[e]), b2[e], act, gl, ul)
+        out[rows] += y * wt[:, None]
+    return out
+
+
+@pytest.mark.parametrize("fmt,act,T,E,K", [("fp4", "swish", 64, 8, 2), ("fp4", "silu", 200, 16, 4),
+                                           ("fp8", "swish", 64, 8, 2), ("fp4", "swish", 1, 8, 4)])
+def test_mx_experts_match_oracle(cuda, fmt, act, T, E, K):
+    """The op pipeline (mapping -> MXFP8 quant -> MX gate_up with bias, clamps and
+    activation -> MX down with bias -> combine) against the oracle."""
+    H, I = 512, 256
+    say("mx experts", fmt, act, T, E, K)
+    w = make_mx_weights(E, H, I, 5 + T, cuda, fmt)
+    g = torch.Generator().manual_seed(T)
+    x = (torch.randn(T, H, generator=g) * 2).to(torch.bfloat16).to(cuda)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    wts = torch.rand(T, K, generator=g)
+    gl, ul = ((None, LIMIT), (1 - LIMIT, 1 + LIMIT)) if act == "swish" else ((None, None), (None, None))
+    out = ops.mx_experts(x, ids.to(cuda), wts.to(cuda), w, act, gl, ul)
+    ref = oracle_layer(x, ids.numpy(), wts.numpy(), w, act, gl, ul)
+    err = rel_l2(np_f32(out), ref)
+    say("rel_l2", err)
+    assert err <= TOL_REL_L2, err

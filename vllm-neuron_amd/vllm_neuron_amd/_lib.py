@@ -59,6 +59,12 @@ PROTOTYPES = {
                                       _i, _p, _p, _p]),
     "moe_expert_down_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _p,
                                    _p]),
+    "moe_act_quant_mx": (_i, [_p, _i, _i, _p, _p, _p]),
+    "moe_expert_gate_up_mx": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p, _i,
+                                   _p, _p, _i, _i, _i, _f, _f, _f, _f, _p, _p, _p]),
+    "moe_expert_down_mx": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p, _p,
+                                _i, _i, _p, _p]),
+    "moe_selftest_mfma_mx": (_i, [_p, _p, _p, _p, _i, _p, _p]),
     "moe_selftest_mfma_fp8": (_i, [_p, _p, _p, _i, _p]),
     "moe_selftest_fp8_encode": (_i, [ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),
     "moe_selftest_bf16_encode": (_i, [ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),

@@ -456,3 +456,78 @@ def layer_forward_noalloc(x, w, cfg, return_routing=False, gamma=None, eps=1e-6,
     if return_routing:
         res = res + (ids, wts, lg)
     return res[0] if len(res) == 1 else res
+
+
+# ---------------------------------------------------------------- MX experts
+
+MX_FMT = {"fp8": 0, "fp4": 1}
+ACT = {"silu": 0, "swish": 1}
+NAN = float("nan")
+
+
+def _lim(v):
+    return NAN if v is None else float(v)
+
+
+def act_quant_mx(x):
+    """x [R, C] bf16 -> (MXFP8 codes [R, C] e4m3fn, E8M0 scale bytes [R, C/32] uint8)."""
+    _need_cuda(x)
+    R, C = x.shape
+    _need(x, torch.bfloat16, (R, C), "activations")
+    q = torch.empty(R, C, device=x.device, dtype=FP8)
+    s = torch.empty(R, C // 32, device=x.device, dtype=torch.uint8)
+    _lib.call("moe_act_quant_mx", ptr(x), R, C, ptr(_u8(q)), ptr(s), _stream())
+    return q, s
+
+
+def expert_gate_up_mx(xq, xs, w, tpid, NB, tiles, num_tiles, max_tiles, mt, rows, act="swish",
+                      gate_limits=(None, None), up_limits=(None, None)):
+    """MX gate_up over row tiles; returns (hq [rows, I] e4m3fn, hs [rows, I/32] uint8)."""
+    T, H = xq.shape
+    E, I = w.n_experts, w.intermediate
+    hq = torch.empty(rows, I, device=xq.device, dtype=FP8)
+    hs = torch.empty(rows, I // 32, device=xq.device, dtype=torch.uint8)
+    _lib.call("moe_expert_gate_up_mx", ptr(_u8(xq)), ptr(xs), T, H, I, E, MX_FMT[w.fmt],
+              ptr(_u8(w.w13)), ptr(w.w13_scale), ptr(w.b13), None, None, None, 0, ptr(tpid), NB,
+              ptr(tiles), ptr(num_tiles), max_tiles, mt, ACT[act], _lim(gate_limits[0]),
+              _lim(gate_limits[1]), _lim(up_limits[0]), _lim(up_limits[1]), ptr(_u8(hq)), ptr(hs),
+              _stream())
+    return hq, hs
+
+
+def expert_down_mx(hq, hs, w, T, NB, tiles, num_tiles, max_tiles, mt):
+    E, H, I = w.n_experts, w.hidden, w.intermediate
+    y = torch.empty(hq.shape[0], H, device=hq.device, dtype=torch.bfloat16)
+    _lib.call("moe_expert_down_mx", ptr(_u8(hq)), ptr(hs), T, H, I, E, MX_FMT[w.fmt],
+              ptr(_u8(w.w2)), ptr(w.w2_scale), ptr(w.b2), None, None, None, 0, NB, ptr(tiles),
+              ptr(num_tiles), max_tiles, mt, ptr(y), _stream())
+    return y
+
+
+def selftest_mfma_mx(a, sa, b, sb, fmt="fp4"):
+    """c[16,16] = (a[16,128] fp8 with scale bytes sa[16,4]) . (b with sb[16,4])^T through
+    one scaled MFMA; b is packed fp4 [16,64] uint8 or fp8 [16,128]."""
+    _need_cuda(a, sa, b, sb)
+    c = torch.empty(16, 16, device=a.device, dtype=torch.float32)
+    _lib.call("moe_selftest_mfma_mx", ptr(_u8(a.contiguous())), ptr(sa.contiguous()),
+              ptr(_u8(b.contiguous())), ptr(sb.contiguous()), MX_FMT[fmt], ptr(c), _stream())
+    return c
+
+
+def mx_experts(x, ids, wts, w, act="swish", gate_limits=(None, None), up_limits=(None, None),
+               block_size=256, xq=None, xs=None):
+    """Experts of ids [T, K] weighted by wts [T, K] with MX weights: [T, H] bf16.
+    Routed rows are compacted per expert (the mapping's inv holds rows, not slots)."""
+    T, K = ids.shape
+    E, H = w.n_experts, w.hidden
+    m = blockwise_mapping(ids=ids.contiguous(), n_experts=E, top_k=K, block_size=block_size)
+    tpid, b2e = m["token_position_to_id"], m["block_to_expert"]
+    NB = tpid.numel()
+    if xq is None:
+        xq, xs = act_quant_mx(x)
+    mt = choose_mt(T, K, E)
+    tiles, num, max_tiles = build_tiles(tpid, b2e, block_size, T, K, E, 0, mt)
+    hq, hs = expert_gate_up_mx(xq, xs, w, tpid, NB, tiles, num, max_tiles, mt, NB, act,
+                               gate_limits, up_limits)
+    y = expert_down_mx(hq, hs, w, T, NB, tiles, num, max_tiles, mt)
+    return combine(y, m["inv_pos"], wts.contiguous(), T, H, NB, 0)
