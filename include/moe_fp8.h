@@ -320,6 +320,27 @@ int moe_expert_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I
                        const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
                        void* stream);
 
+/* The MoE layer with MX experts (GPT-OSS: MXFP4 experts with biases, Swish and
+ * clamps): [residual add ->] [RMSNorm (gamma) ->] router logits (+ router_bias) ->
+ * top-k (orders TOPK_ACT / ACT_TOPK) -> mapping -> MXFP8 activations -> MX gate_up
+ * -> MX down -> weighted combine. Arguments as moe_layer_forward and
+ * moe_expert_gate_up_mx; no shared experts. Workspace:
+ * moe_layer_workspace_bytes(T, H, I, E, K, 0, B, gamma != NULL). Replaces
+ * GptOssExperts.forward of the MXFP4 model (model_mxfp4.py:1362-1377: prefill
+ * :1584-1769 fused norm + router + shard_on_block_mx moe_cte; decode
+ * moe_block_tkg with the same activation, clamps and biases, model_bf16.py:
+ * 1274-1307). */
+int moe_layer_forward_mx(const void* x_bf16, const void* residual_bf16, const float* gamma,
+                         float eps, int hidden_actual, int T, int H, int I, int E, int K,
+                         const void* router_w_bf16, const float* router_bias, int order,
+                         int scoring, int renorm, float renorm_eps, float routed_scale, int wfmt,
+                         const uint8_t* w13, const uint8_t* w13_scale, const float* b13,
+                         const uint8_t* w2, const uint8_t* w2_scale, const float* b2, int act,
+                         float gate_lo, float gate_hi, float up_lo, float up_hi, int B,
+                         void* out_bf16, void* residual_out_bf16, int32_t* ids_out,
+                         float* weights_out, float* logits_out, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* ---- diagnostics ----------------------------------------------------------- */
 
 /* shape 0: c[16,16] = decode(a[16,128]) . decode(b[16,128])^T through one

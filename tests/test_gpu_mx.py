@@ -150,3 +150,72 @@ def test_mx_experts_match_oracle(cuda, fmt, act, T, E, K):
     err = rel_l2(np_f32(out), ref)
     say("rel_l2", err)
     assert err <= TOL_REL_L2, err
+
+
+# ---------------------------------------------------------------- GPT-OSS-120B layer
+
+GPT_OSS = dict(E=128, H=3072, I=3072, h_real=2880, i_real=2880, K=4)   # hidden 2880 padded to 3072
+
+
+@pytest.fixture(scope="module")
+def gpt_oss_weights(cuda):
+    from vllm_neuron_amd import synthetic
+    c = GPT_OSS
+    w = synthetic.make_mx_weights(c["E"], c["H"], c["I"], 7, device=cuda, h_real=c["h_real"],
+                                  i_real=c["i_real"])
+    yield w
+    del w
+    torch.cuda.empty_cache()
+
+
+def _padded_hidden(T, seed, cuda):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.zeros(T, GPT_OSS["H"])
+    x[:, :GPT_OSS["h_real"]] = torch.randn(T, GPT_OSS["h_real"], generator=g)
+    return x.to(torch.bfloat16).to(cuda)
+
+
+@pytest.mark.parametrize("T,tokens", [(1, [0]), (64, [0, 9, 31, 63]), (2048, [0, 700, 2047])])
+def test_gpt_oss_120b_layer(cuda, gpt_oss_weights, T, tokens):
+    """GPT-OSS-120B expert shapes (128 MXFP4 experts, hidden and intermediate 2880
+    padded to 3072, top-4 softmax with a router bias, Swish with gate <= 7 and
+    -6 <= up <= 8, biases) through MXFP4MoE with the layer's RMSNorm and residual add:
+    routing bit-exact from the GPU's logits, output rel-L2 <= 1e-2 on a token subset."""
+    from oracle import router as R
+    from oracle.moe import bf16_round
+    from vllm_neuron_amd import MXFP4MoE
+    c = GPT_OSS
+    w = gpt_oss_weights
+    say("gpt-oss-120b layer", T)
+    x = _padded_hidden(T, 100 + T, cuda)
+    r = _padded_hidden(T, 200 + T, cuda)
+    g = torch.Generator().manual_seed(T)
+    gamma = torch.zeros(c["H"])
+    gamma[:c["h_real"]] = 1 + 0.1 * torch.randn(c["h_real"], generator=g)
+    gamma = gamma.to(torch.bfloat16).float().to(cuda)
+    layer = MXFP4MoE(w, c["K"], norm_weight=gamma, eps=1e-5, hidden_actual=c["h_real"])
+    out, rsum = layer(x, None, False, None, residual=r)
+    out2, rsum2, ids, wts, lg = ops.layer_forward_mx(
+        x, w, c["K"], "swish", (None, LIMIT), (1 - LIMIT, 1 + LIMIT), return_routing=True,
+        gamma=gamma, eps=1e-5, hidden_actual=c["h_real"], residual=r)
+    assert torch.equal(out, out2) and torch.equal(rsum, rsum2)
+    assert np.array_equal(np_f32(rsum), bf16_round(np_f32(x) + np_f32(r)))
+    dec = layer(rsum, None, True, None)   # decode: the same norm, one tensor
+    assert torch.equal(dec, out)
+    xn = ops.rms_norm_quant(x, gamma, 1e-5, c["h_real"], r)[0]
+    ref_xn = R.rms_norm_padded(np_f32(rsum), np_f32(gamma), 1e-5, c["h_real"])
+    assert np.allclose(np_f32(xn), bf16_round(ref_xn), rtol=2 ** -7, atol=0)
+    xs = np_f32(xn)
+    lg, ids, wts = lg.cpu().numpy(), ids.cpu().numpy(), wts.cpu().numpy()
+    ref_lg = R.router_logits(xs, np_f32(w.router_w), np_f32(w.router_bias))
+    assert np.allclose(lg, ref_lg, rtol=1e-5, atol=2e-5)
+    oi, ow = R.route_topk_act(lg, c["K"], R.SOFTMAX)
+    assert np.array_equal(ids, oi) and np.array_equal(wts, ow)
+    sel = np.asarray(tokens)
+    ref = oracle_layer(xn[sel], ids[sel], wts[sel], w, "swish", (None, LIMIT),
+                       (1 - LIMIT, 1 + LIMIT), experts=set(np.unique(ids[sel]).tolist()))
+    got = np_f32(out)[sel]
+    err = rel_l2(got, ref)
+    say("gpt-oss rel_l2", err)
+    assert err <= TOL_REL_L2, err
+    assert np.all(got[:, c["h_real"]:] == 0)  # padded hidden columns stay zero

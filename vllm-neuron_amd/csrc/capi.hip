@@ -319,3 +319,90 @@ extern "C" int moe_layer_forward_noalloc(
                             w2_shared_scale, B, out_bf16, residual_out_bf16, ids_out, weights_out,
                             logits_out, ws, (size_t)MOE_NOALLOC_SCRATCH_BYTES, stream);
 }
+
+// ---------------------------------------------------------------------------
+// The layer with MX experts (GPT-OSS): [residual add ->] [RMSNorm ->] router ->
+// top-k -> mapping (compact rows) -> MXFP8 quantization -> MX gate_up (bias,
+// clamps, activation) -> MX down (bias) -> combine. Same workspace as
+// moe_layer_forward without shared experts (the MX scale bytes take the room of
+// the 1x128 fp32 scales).
+// ---------------------------------------------------------------------------
+extern "C" int moe_layer_forward_mx(
+    const void* x_bf16, const void* residual_bf16, const float* gamma, float eps,
+    int hidden_actual, int T, int H, int I, int E, int K, const void* router_w_bf16,
+    const float* router_bias, int order, int scoring, int renorm, float renorm_eps,
+    float routed_scale, int wfmt, const uint8_t* w13, const uint8_t* w13_scale, const float* b13,
+    const uint8_t* w2, const uint8_t* w2_scale, const float* b2, int act, float gate_lo,
+    float gate_hi, float up_lo, float up_hi, int B, void* out_bf16, void* residual_out_bf16,
+    int32_t* ids_out, float* weights_out, float* logits_out, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  MOE_API_BEGIN("moe_layer_forward_mx");
+  MOE_CHECK_ARG(x_bf16 && router_w_bf16 && w13 && w13_scale && w2 && w2_scale && out_bf16 && workspace,
+                "null pointer argument");
+  MOE_CHECK_ARG(T > 0 && E > 0 && K > 0 && K <= E && B > 0, "bad sizes T=%d E=%d K=%d B=%d", T, E,
+                K, B);
+  MOE_CHECK_ARG(H % 256 == 0 && I % 128 == 0, "H must be a multiple of 256 and I of 128 (pad them)");
+  MOE_CHECK_ARG(order == MOE_ORDER_TOPK_ACT || order == MOE_ORDER_ACT_TOPK,
+                "the MX layer routes with the TOPK_ACT or ACT_TOPK order");
+  MOE_CHECK_ARG((residual_bf16 == nullptr) == (residual_out_bf16 == nullptr),
+                "residual and residual_out must be given together");
+  MOE_CHECK_ARG(gamma != nullptr || residual_bf16 == nullptr,
+                "the residual add is fused into the norm: residual needs gamma");
+  const bool norm = gamma != nullptr;
+  const size_t need = moe_layer_workspace_bytes(T, H, I, E, K, 0, B, norm);
+  MOE_CHECK_ARG(workspace_bytes >= need, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  MOE_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
+  LayerWs w = carve((char*)workspace, T, H, I, E, K, 0, B, norm);
+  const int N = moe_num_blocks(T, K, E, B);
+  const long NB = (long)N * B;
+  const long R = routed_rows(T, K, E);
+  MOE_CHECK_SUPPORTED(NB < (1L << 31), "too many slots");
+  const int mt = choose_mt(T, K, E);
+  const int max_tiles = moe_max_tiles(T, K, E, N, B, 0, mt);
+  float* logits = logits_out ? logits_out : w.logits;
+  int32_t* ids = ids_out ? ids_out : w.ids;
+  float* wts = weights_out ? weights_out : w.weights;
+  uint8_t* xs = (uint8_t*)w.xs;  // T * H/32 bytes of E8M0 scales
+  uint8_t* hs = (uint8_t*)w.hs;  // P * I/32 bytes
+
+  char saved[1024];
+  int rc;
+#define MOE_STEP(call)                                         \
+  rc = (call);                                                 \
+  if (rc != MOE_OK) {                                          \
+    snprintf(saved, sizeof(saved), "%s", moe_last_error());    \
+    moe::set_error(_moe_fn, "%s", saved);                      \
+    return rc;                                                 \
+  }
+  const void* xr = x_bf16;
+  if (norm) {
+    // residual add + RMSNorm (its 1x128 codes land in xq and are replaced below)
+    MOE_STEP(moe_rms_norm_quant(x_bf16, residual_bf16, gamma, T, H,
+                                hidden_actual > 0 ? hidden_actual : H, eps, w.xn,
+                                residual_out_bf16, w.xq, w.xs, stream));
+    xr = w.xn;
+  }
+  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+                              w.router_ws_bytes, nullptr, K, order, scoring, 1, 1, renorm,
+                              renorm_eps, routed_scale, ids, wts, stream));
+  TileOut to{};
+  to.tiles = (int4*)w.tiles;
+  to.num_tiles = w.num_tiles;
+  to.max_tiles = max_tiles;
+  to.mt = mt;
+  to.compact = 1;
+  to.row_shared = R;
+  MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
+                             w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
+  MOE_STEP(moe_act_quant_mx(xr, T, H, w.xq, xs, stream));
+  MOE_STEP(moe_expert_gate_up_mx(w.xq, xs, T, H, I, E, wfmt, w13, w13_scale, b13, nullptr, nullptr,
+                                 nullptr, 0, w.tpid, (int)NB, w.tiles, w.num_tiles, max_tiles, mt,
+                                 act, gate_lo, gate_hi, up_lo, up_hi, w.hq, hs, stream));
+  MOE_STEP(moe_expert_down_mx(w.hq, hs, T, H, I, E, wfmt, w2, w2_scale, b2, nullptr, nullptr,
+                              nullptr, 0, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y,
+                              stream));
+  MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)R, 0, out_bf16, stream));
+#undef MOE_STEP
+  return MOE_OK;
+}

@@ -65,6 +65,9 @@ PROTOTYPES = {
     "moe_expert_down_mx": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p, _p,
                                 _i, _i, _p, _p]),
     "moe_selftest_mfma_mx": (_i, [_p, _p, _p, _p, _i, _p, _p]),
+    "moe_layer_forward_mx": (_i, [_p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _p, _p, _i, _i, _i, _f,
+                                  _f, _i, _p, _p, _p, _p, _p, _p, _i, _f, _f, _f, _f, _i, _p, _p,
+                                  _p, _p, _p, _p, _sz, _p]),
     "moe_selftest_mfma_fp8": (_i, [_p, _p, _p, _i, _p]),
     "moe_selftest_fp8_encode": (_i, [ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),
     "moe_selftest_bf16_encode": (_i, [ctypes.c_uint32, ctypes.c_uint32, _p, _i, _p]),

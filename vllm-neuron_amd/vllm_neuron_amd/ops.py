@@ -531,3 +531,44 @@ def mx_experts(x, ids, wts, w, act="swish", gate_limits=(None, None), up_limits=
                                gate_limits, up_limits)
     y = expert_down_mx(hq, hs, w, T, NB, tiles, num, max_tiles, mt)
     return combine(y, m["inv_pos"], wts.contiguous(), T, H, NB, 0)
+
+
+def layer_forward_mx(x, w, top_k, act="swish", gate_limits=(None, None), up_limits=(None, None),
+                     scoring="softmax", order=ORDER_TOPK_ACT, renorm=False, return_routing=False,
+                     gamma=None, eps=1e-6, hidden_actual=None, residual=None, block_size=256):
+    """The layer with MX experts (moe_layer_forward_mx): x [T, H] bf16, w MxMoEWeights.
+    Returns out [T, H] bf16; (out, residual_sum) with a residual; the routing (ids,
+    weights, logits) appended when return_routing."""
+    _need_cuda(x, w.w13, gamma, residual)
+    T, H = x.shape
+    _need(x, torch.bfloat16, (T, H), "hidden_states")
+    if residual is not None:
+        if gamma is None:
+            raise ValueError("the residual add is fused into the norm: residual needs gamma")
+        _need(residual, torch.bfloat16, (T, H), "residual")
+    g = None
+    if gamma is not None:
+        g = gamma.reshape(-1).to(torch.float32).contiguous()
+        if g.numel() != H:
+            raise ValueError(f"gamma must hold H={H} values, got shape {tuple(gamma.shape)}")
+    E, I, K = w.n_experts, w.intermediate, int(top_k)
+    lib = _lib.load()
+    wsb = lib.moe_layer_workspace_bytes(T, H, I, E, K, 0, block_size, int(g is not None))
+    ws = torch.empty(wsb, device=x.device, dtype=torch.uint8)
+    out = torch.empty(T, H, device=x.device, dtype=torch.bfloat16)
+    rsum = torch.empty_like(x) if residual is not None else None
+    ids = torch.empty(T, K, device=x.device, dtype=torch.int32) if return_routing else None
+    wts = torch.empty(T, K, device=x.device, dtype=torch.float32) if return_routing else None
+    lg = torch.empty(T, E, device=x.device, dtype=torch.float32) if return_routing else None
+    ha = 0 if hidden_actual is None else int(hidden_actual)
+    _lib.call("moe_layer_forward_mx", ptr(x), ptr(residual), ptr(g), float(eps), ha, T, H, I, E, K,
+              ptr(w.router_w), ptr(w.router_bias), int(order),
+              SCORING[scoring] if isinstance(scoring, str) else int(scoring), int(bool(renorm)),
+              1e-20, 1.0, MX_FMT[w.fmt], ptr(_u8(w.w13)), ptr(w.w13_scale), ptr(w.b13),
+              ptr(_u8(w.w2)), ptr(w.w2_scale), ptr(w.b2), ACT[act], _lim(gate_limits[0]),
+              _lim(gate_limits[1]), _lim(up_limits[0]), _lim(up_limits[1]), block_size, ptr(out),
+              ptr(rsum), ptr(ids), ptr(wts), ptr(lg), ptr(ws), wsb, _stream())
+    res = (out,) if residual is None else (out, rsum)
+    if return_routing:
+        res = res + (ids, wts, lg)
+    return res[0] if len(res) == 1 else res

@@ -88,3 +88,47 @@ def make_weights(cfg, cfg_index, device="cpu", zipf=False, experts_device=None):
                   shared_w2=torch.stack(sw2).to(device), shared_w2_scale=torch.stack(ss2).to(device))
     return Fp8MoEWeights(router_w=router_w, w13=w13, w13_scale=s13, w2=w2, w2_scale=s2,
                          router_bias=rbias, corr_bias=corr, **kw).validate()
+
+
+def make_mx_weights(E, H, I, cfg_index, device="cpu", h_real=None, i_real=None, fmt="fp4",
+                    bias=True):
+    """MxMoEWeights of E experts at padded sizes H, I whose real sizes are h_real,
+    i_real (GPT-OSS: 2880 padded to 3072): N(0, 0.02) fp32 weights on the real block,
+    zero in the padding, OCP-quantized per 32 values along K; biases N(0, 0.1) with
+    the +1 of the reference's loaders on the up half (zero in the padding); router
+    weight N(0, 0.02) bf16 and bias N(0, 0.1). Generated one expert at a time."""
+    from .weights_mx import MxMoEWeights, quant_mx_weight
+    hr, ir = h_real or H, i_real or I
+    per = 2 if fmt == "fp4" else 1
+    cdt = torch.uint8 if fmt == "fp4" else torch.float8_e4m3fn
+    w13 = torch.empty(E, 2 * I, H // per, dtype=cdt, device=device)
+    s13 = torch.empty(E, 2 * I, H // 32, dtype=torch.uint8, device=device)
+    w2 = torch.empty(E, H, I // per, dtype=cdt, device=device)
+    s2 = torch.empty(E, H, I // 32, dtype=torch.uint8, device=device)
+    for e in range(E):
+        a, b = expert_fp32(cfg_index, e, hr, ir, device, tag_base=2000)
+        full13 = torch.zeros(2 * I, H, device=device)
+        full13[:ir, :hr] = a[:ir]
+        full13[I:I + ir, :hr] = a[ir:]
+        full2 = torch.zeros(H, I, device=device)
+        full2[:hr, :ir] = b
+        q, s = quant_mx_weight(full13, fmt)
+        w13[e].copy_(q)
+        s13[e].copy_(s)
+        q, s = quant_mx_weight(full2, fmt)
+        w2[e].copy_(q)
+        s2[e].copy_(s)
+    g = _gen("cpu", SEED_STRIDE * cfg_index + 2)
+    router_w = torch.zeros(E, H, dtype=torch.bfloat16)
+    router_w[:, :hr] = (torch.randn(E, hr, generator=g) * 0.02).to(torch.bfloat16)
+    router_b = (torch.randn(E, generator=g) * 0.1).float()
+    b13 = b2 = None
+    if bias:
+        b13 = torch.zeros(E, 2 * I)
+        b13[:, :ir] = torch.randn(E, ir, generator=g) * 0.1
+        b13[:, I:I + ir] = torch.randn(E, ir, generator=g) * 0.1 + 1.0
+        b2 = torch.zeros(E, H)
+        b2[:, :hr] = torch.randn(E, hr, generator=g) * 0.1
+        b13, b2 = b13.to(device), b2.to(device)
+    return MxMoEWeights(router_w=router_w.to(device), w13=w13, w13_scale=s13, w2=w2, w2_scale=s2,
+                        b13=b13, b2=b2, router_bias=router_b.to(device), fmt=fmt).validate()
