@@ -51,8 +51,7 @@ def _experts(E=2, H=256, I=128):
 
 
 @pytest.mark.parametrize("kw", [
-    dict(implementation=M.MoECTEImplementation.shard_on_block_mx),
-    dict(quantization_type=M.QuantizationType.MX),
+    dict(quantization_type=M.QuantizationType.STATIC_MX),
     dict(activation_function=M.ActFnType.GELU),
     dict(expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.PRE_SCALE),
     dict(gate_clamp_upper_limit=8.0),
@@ -69,6 +68,25 @@ def test_moe_cte_unsupported_options(kw):
     base.update(kw)
     with pytest.raises(NotImplementedError):
         M.moe_cte(**base)
+
+
+def test_moe_cte_mx_arguments():
+    """MX requested with weights that are not in an MX layout is an argument error; the
+    reference's Trainium-tiled uint16 MX layout is refused as unsupported."""
+    gu, dn = _experts()
+    base = dict(hidden_states=torch.zeros(4, 256, dtype=torch.bfloat16),
+                expert_affinities_masked=torch.zeros(8, 1), gate_up_proj_weight=gu,
+                down_proj_weight=dn, token_position_to_id=torch.zeros(512, dtype=torch.int32),
+                block_to_expert=torch.zeros(2, dtype=torch.int32), block_size=256,
+                implementation=M.MoECTEImplementation.shard_on_block_mx)
+    with pytest.raises(ValueError):
+        M.moe_cte(**base)
+    tiled = dict(base, gate_up_proj_weight=torch.zeros(2, 128, 2, 1, 128, dtype=torch.uint16),
+                 down_proj_weight=torch.zeros(2, 8, 1, 256, dtype=torch.uint16),
+                 gate_up_proj_scale=torch.zeros(2, 16, 2, 1, 128, dtype=torch.uint8),
+                 down_proj_scale=torch.zeros(2, 1, 1, 256, dtype=torch.uint8))
+    with pytest.raises(NotImplementedError, match="uint16"):
+        M.moe_cte(**tiled)
 
 
 def test_moe_cte_rejects_unquantized_experts():

@@ -114,11 +114,12 @@ def oracle_mx_weights(w):
 
 
 def oracle_layer(x, ids, wts, w, act, gl, ul, experts=None):
+    x = x if isinstance(x, np.ndarray) else np_f32(x)
     q13, s13, b13, q2, s2, b2 = oracle_mx_weights(w)
     if w.fmt == "fp4":
-        return OX.moe_sparse_mx(np_f32(x), ids, wts, q13, s13, b13, q2, s2, b2, act, gl, ul, experts)
+        return OX.moe_sparse_mx(x, ids, wts, q13, s13, b13, q2, s2, b2, act, gl, ul, experts)
     # fp8 weights: dequantize the codes with the same helper path
-    xhat = OX.dequant_mxfp8(*OX.quant_mxfp8(np_f32(x)))
+    xhat = OX.dequant_mxfp8(*OX.quant_mxfp8(x))
     out = np.zeros(x.shape, np.float32)
     for e in (range(w.n_experts) if experts is None else sorted(experts)):
         sel = ids == e
@@ -219,3 +220,79 @@ def test_gpt_oss_120b_layer(cuda, gpt_oss_weights, T, tokens):
     say("gpt-oss rel_l2", err)
     assert err <= TOL_REL_L2, err
     assert np.all(got[:, c["h_real"]:] == 0)  # padded hidden columns stay zero
+
+
+def _ids_from_dense(a):
+    K = int((a != 0).sum(1).max())
+    ids = np.zeros((a.shape[0], K), np.int32)
+    wts = np.zeros((a.shape[0], K), np.float32)
+    for t in range(a.shape[0]):
+        nz = np.nonzero(a[t])[0]
+        ids[t, :len(nz)] = nz
+        wts[t, :len(nz)] = a[t, nz]
+    return ids, wts
+
+
+def test_gpt_oss_moe_cte_mx_api(cuda, gpt_oss_weights):
+    """The reference's GPT-OSS prefill call chain on MX experts: router (softmax, router
+    bias) -> build_blockwise_mapping -> moe_cte(shard_on_block_mx, Swish, gate <= 7,
+    -6 <= up <= 8, biases in the reference's [E, 2, I] / [E, 1, H] shapes, POST_SCALE)
+    (model_bf16.py:1362-1470) against the oracle."""
+    from vllm_neuron_amd.functional import moe as M
+    c, w = GPT_OSS, gpt_oss_weights
+    T = 512
+    say("gpt-oss moe_cte mx", T)
+    x = _padded_hidden(T, 300, cuda)
+    aff = M.router(x, w.router_w.t(), c["K"], router_bias=w.router_bias, activation="softmax")
+    am, tpid, b2e, cond = M.build_blockwise_mapping(aff, c["E"], c["K"], 256)
+    E, I2 = w.w13.shape[:2]
+    out = M.moe_cte(x, am, w.w13, w.w2, tpid, b2e, 256, M.MoECTEImplementation.shard_on_block_mx,
+                    conditions=cond, gate_and_up_proj_bias=w.b13.reshape(E, 2, I2 // 2),
+                    down_proj_bias=w.b2.unsqueeze(1), gate_up_proj_scale=w.w13_scale,
+                    down_proj_scale=w.w2_scale, activation_function=M.ActFnType.Swish,
+                    quantization_type=M.QuantizationType.MX, gate_clamp_upper_limit=LIMIT,
+                    up_clamp_upper_limit=LIMIT + 1, up_clamp_lower_limit=-LIMIT + 1,
+                    expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.POST_SCALE)
+    ids, wts = _ids_from_dense(np_f32(aff))
+    sel = np.array([0, 111, 511])
+    ref = oracle_layer(x[sel], ids[sel], wts[sel], w, "swish", (None, LIMIT), (1 - LIMIT, 1 + LIMIT),
+                       experts=set(np.unique(ids[sel]).tolist()))
+    err = rel_l2(np_f32(out)[sel], ref)
+    say("moe_cte mx rel_l2", err)
+    assert err <= TOL_REL_L2, err
+
+
+def test_gpt_oss_moe_block_tkg_mx_api(cuda, gpt_oss_weights):
+    """The reference's GPT-OSS decode call (model_bf16.py:1274-1307): moe_block_tkg with
+    gamma, router bias, softmax top-4 after the linear (router_pre_norm False), Swish,
+    clamps, expert biases and hidden_actual 2880, on MX experts."""
+    from oracle import router as R
+    from oracle.moe import bf16_round
+    from vllm_neuron_amd.functional import moe as M
+    c, w = GPT_OSS, gpt_oss_weights
+    T = 32
+    say("gpt-oss moe_block_tkg mx", T)
+    x = _padded_hidden(T, 400, cuda)
+    gamma = torch.zeros(c["H"], device=cuda)
+    gamma[:c["h_real"]] = 1.0
+    E, I2 = w.w13.shape[:2]
+    out, lg = M.moe_block_tkg(
+        x.unsqueeze(0), gamma.unsqueeze(0), w.router_w.t(), w.w13, w.w2, top_k=c["K"],
+        expert_gate_up_weights_scale=w.w13_scale, expert_down_weights_scale=w.w2_scale,
+        router_bias=w.router_bias.unsqueeze(0), expert_gate_up_bias=w.b13.reshape(E, 2, I2 // 2),
+        expert_down_bias=w.b2, eps=1e-5, router_act_fn=M.RouterActFnType.SOFTMAX,
+        router_pre_norm=False, expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.POST_SCALE,
+        hidden_act_fn=M.ActFnType.Swish, gate_clamp_upper_limit=LIMIT,
+        up_clamp_upper_limit=LIMIT + 1, up_clamp_lower_limit=-LIMIT + 1,
+        hidden_actual=c["h_real"])
+    xn = bf16_round(R.rms_norm_padded(np_f32(x), np_f32(gamma), 1e-5, c["h_real"]))
+    lg = np_f32(lg)
+    assert np.allclose(lg, R.router_logits(xn, np_f32(w.router_w), np_f32(w.router_bias)),
+                       rtol=1e-5, atol=2e-5)
+    ids, wts = R.route_topk_act(lg, c["K"], R.SOFTMAX)
+    sel = np.array([0, 13, 31])
+    ref = oracle_layer(xn[sel], ids[sel], wts[sel], w, "swish", (None, LIMIT), (1 - LIMIT, 1 + LIMIT),
+                       experts=set(np.unique(ids[sel]).tolist()))
+    err = rel_l2(np_f32(out.reshape(T, -1))[sel], ref)
+    say("moe_block_tkg mx rel_l2", err)
+    assert err <= TOL_REL_L2, err

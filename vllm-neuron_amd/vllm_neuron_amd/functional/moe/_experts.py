@@ -217,3 +217,46 @@ def routed_forward(x_bf16, ids, wts, w, block_size=256, xq=None, xs=None):
     y, NB = run_experts(x_bf16, m["token_position_to_id"], m["block_to_expert"], block_size, K, K,
                         w, xq, xs)
     return ops.combine(y, m["inv_pos"], wts.contiguous(), T, H, NB, w.n_shared)
+
+
+# ---------------------------------------------------------------- MX experts
+
+def is_mx_weights(gate_up, gate_up_scale):
+    """MX experts are uint8 (packed fp4) or float8_e4m3fn codes with uint8 E8M0 scales."""
+    return gate_up_scale is not None and gate_up_scale.dtype == torch.uint8
+
+
+def mx_weights(gate_up, down, gate_up_scale, down_scale, gate_up_bias=None, down_bias=None):
+    """MxMoEWeights from the stacked MX layout: gate_up [E, 2I, H/2] uint8 (fp4) or
+    [E, 2I, H] float8_e4m3fn (fp8) with scales [E, 2I, H/32] uint8; down [E, H, I/2] or
+    [E, H, I] with [E, H, I/32]; biases [E, 2, I] (the reference's shape) or [E, 2I],
+    and [E, 1, H] or [E, H]. The reference's Trainium-tiled uint16 layout is refused
+    (load the HF checkpoint with weights_mx.from_hf_gpt_oss instead)."""
+    from ...weights_mx import MxMoEWeights
+    if gate_up.dtype == torch.uint16 or down.dtype == torch.uint16:
+        raise NotImplementedError(
+            "MX weights in the Trainium-tiled uint16 layout: pass the stacked layout "
+            "(vllm_neuron_amd.weights_mx.from_hf_gpt_oss converts the HF checkpoint)")
+    if gate_up.dim() != 3 or down.dim() != 3:
+        raise ValueError(f"MX gate_up must be [E, 2I, H/2] (fp4) or [E, 2I, H] (fp8), got "
+                         f"{tuple(gate_up.shape)}")
+    fmt = "fp4" if gate_up.dtype == torch.uint8 else "fp8"
+    if fmt == "fp8" and gate_up.dtype != FP8:
+        raise ValueError(f"MX expert codes must be uint8 (fp4) or float8_e4m3fn, got {gate_up.dtype}")
+    if down_scale is None or down_scale.dtype != torch.uint8:
+        raise ValueError("MX down_proj_scale must be uint8 E8M0 bytes")
+    E, I2 = gate_up.shape[:2]
+    H = down.shape[1]
+    b13 = None if gate_up_bias is None else gate_up_bias.reshape(E, I2).float().contiguous()
+    b2 = None if down_bias is None else down_bias.reshape(E, H).float().contiguous()
+    w = MxMoEWeights(router_w=gate_up.new_empty(E, H, dtype=torch.bfloat16), w13=gate_up.contiguous(),
+                     w13_scale=gate_up_scale.contiguous(), w2=down.contiguous(),
+                     w2_scale=down_scale.contiguous(), b13=b13, b2=b2, fmt=fmt)
+    w.validate()
+    return w
+
+
+def mx_dims(gate_up, down):
+    """(E, H, I) of stacked MX weights from shapes alone."""
+    E, I2 = gate_up.shape[:2]
+    return E, down.shape[1], I2 // 2

@@ -25,6 +25,9 @@ in the block-scale shapes); floating-point shared-expert weights are quantized
 once to the same format. router_mm_dtype is accepted for signature
 compatibility; the logits are always accumulated in fp32. The GPU work is one
 torch.library operator (moe_fp8::moe_block_tkg), an opaque node under torch.compile.
+MX experts (uint8 E8M0 scales: stacked MXFP4 / MXFP8 weights, the GPT-OSS decode
+call of model_bf16.py:1274-1307) take expert biases ([E, 2, I], [E, H]), SiLU or
+Swish and the gate / up clamps (moe_fp8::moe_block_tkg_mx).
 """
 from typing import Optional, Tuple
 
@@ -81,16 +84,21 @@ def moe_block_tkg(
     if hidden_act_scale_factor is not None or hidden_act_bias is not None:
         raise NotImplementedError(
             "hidden_act_scale_factor and hidden_act_bias are placeholders and must be None.")
+    mx = _experts.is_mx_weights(expert_gate_up_weights, expert_gate_up_weights_scale)
+    acts = (ActFnType.SiLU, ActFnType.Swish) if mx else (ActFnType.SiLU,)
     bad = {
-        "expert biases": any(v is not None for v in (
-            expert_gate_up_bias, expert_down_bias, shared_expert_gate_bias,
-            shared_expert_up_bias, shared_expert_down_bias)),
+        "expert biases with fp8 128x128 experts": not mx and (
+            expert_gate_up_bias is not None or expert_down_bias is not None),
+        "shared-expert biases": any(v is not None for v in (
+            shared_expert_gate_bias, shared_expert_up_bias, shared_expert_down_bias)),
+        "a shared expert with MX experts": mx and shared_expert_gate_w is not None,
         "STATIC_MX input scales": expert_gate_up_input_scale is not None
             or expert_down_input_scale is not None,
         "fused residual add on float32 input": residual is not None and inp.dtype != torch.bfloat16,
-        "gate/up clamps": any(v is not None for v in (gate_clamp_upper_limit, gate_clamp_lower_limit,
-                                                      up_clamp_upper_limit, up_clamp_lower_limit)),
-        f"activation {getattr(hidden_act_fn, 'name', hidden_act_fn)}": hidden_act_fn != ActFnType.SiLU,
+        "gate/up clamps with fp8 128x128 experts": not mx and any(v is not None for v in (
+            gate_clamp_upper_limit, gate_clamp_lower_limit, up_clamp_upper_limit,
+            up_clamp_lower_limit)),
+        f"activation {getattr(hidden_act_fn, 'name', hidden_act_fn)}": hidden_act_fn not in acts,
         f"scaling mode {expert_affinities_scaling_mode.name}": expert_affinities_scaling_mode not in (
             ExpertAffinityScaleMode.NO_SCALE, ExpertAffinityScaleMode.POST_SCALE),
     }
@@ -111,7 +119,10 @@ def moe_block_tkg(
         raise ValueError(f"router_weights must be [H, E] with H={H}, got "
                          f"{tuple(router_weights.shape)}")
     E_global = router_weights.shape[1]
-    E_L, H_w, _ = _experts.weight_dims(expert_gate_up_weights, expert_down_weights)
+    if mx:
+        E_L, H_w, _ = _experts.mx_dims(expert_gate_up_weights, expert_down_weights)
+    else:
+        E_L, H_w, _ = _experts.weight_dims(expert_gate_up_weights, expert_down_weights)
     if H_w != H:
         raise ValueError(f"expert weights have H={H_w}, inp H={H}")
     if E_L != E_global:
@@ -131,6 +142,23 @@ def moe_block_tkg(
         if tuple(r.shape) != (T, H) or r.dtype != torch.bfloat16:
             raise ValueError(f"residual must be bfloat16 [T, H] = [{T}, {H}], got "
                              f"{r.dtype} {tuple(residual.shape)}")
+    if mx:
+        nan = float("nan")
+        lim = lambda v: nan if v is None else float(v)
+        out, logits, res_out = _block_tkg_mx_op(
+            x, gamma, router_weights, expert_gate_up_weights, expert_down_weights,
+            expert_gate_up_weights_scale, expert_down_weights_scale, expert_gate_up_bias,
+            expert_down_bias, router_bias, r, int(top_k), float(eps),
+            0 if router_act_fn == RouterActFnType.SOFTMAX else 1, bool(router_pre_norm),
+            bool(norm_topk_prob),
+            expert_affinities_scaling_mode == ExpertAffinityScaleMode.POST_SCALE,
+            0 if hidden_actual is None else int(hidden_actual),
+            "swish" if hidden_act_fn == ActFnType.Swish else "silu", lim(gate_clamp_lower_limit),
+            lim(gate_clamp_upper_limit), lim(up_clamp_lower_limit), lim(up_clamp_upper_limit))
+        res = (out,) if skip_router_logits else (out, logits)
+        if residual is not None:
+            res = res + (res_out.reshape(inp.shape),)
+        return res[0] if len(res) == 1 else res
     out, logits, res_out = _block_tkg_op(
         x, gamma, router_weights, expert_gate_up_weights, expert_down_weights,
         expert_gate_up_weights_scale, expert_down_weights_scale, shared_expert_gate_w,
@@ -200,6 +228,71 @@ def _block_tkg_op(x: Tensor, gamma: Tensor, router_weights: Tensor, gate_up: Ten
 def _block_tkg_fake(x, gamma, router_weights, gate_up, down, gate_up_scale, down_scale,
                     shared_gate, shared_up, shared_down, router_bias, residual, top_k, eps,
                     scoring, pre_norm, norm_topk_prob, post_scale, hidden_actual):
+    T, H = x.shape
+    E = router_weights.shape[1]
+    nres = 0 if residual is None or x.dtype != torch.bfloat16 else T
+    return (x.new_empty(T, H), x.new_empty(T, E, dtype=torch.float32),
+            x.new_empty(nres, H, dtype=torch.bfloat16))
+
+
+def _norm_route(x, gamma, router_weights, router_bias, residual, top_k, eps, scoring, pre_norm,
+                norm_topk_prob, post_scale, ha):
+    """Steps 1-3 of the decode block on the GPU (RMSNorm with the residual add, fp32
+    router logits, selection): (xn, logits, ids, weights, residual_out)."""
+    res_out = None
+    if x.dtype == torch.bfloat16 and residual is not None:
+        xn, _, _, res_out = ops.rms_norm_quant(x.contiguous(), gamma, eps, ha, residual.contiguous())
+    else:
+        xn = ops.rms_norm(x.contiguous(), gamma, eps, ha, out_dtype=x.dtype)
+    wt = router_weights.t()
+    wt = wt if wt.is_contiguous() else wt.contiguous()
+    bias = None if router_bias is None else router_bias.reshape(-1).float().contiguous()
+    if xn.dtype == torch.bfloat16 and wt.dtype == torch.bfloat16:
+        logits = ops.router_logits(xn, wt, bias)
+    else:
+        if wt.dtype not in (torch.float32, torch.bfloat16):
+            wt = wt.float().contiguous()
+        logits = ops.router_logits_f32(xn.float().contiguous(), wt, bias)
+    order = ops.ORDER_ACT_TOPK if pre_norm else ops.ORDER_TOPK_ACT
+    ids, wts = ops.router_topk(logits, top_k, order, scoring, renorm=norm_topk_prob, eps=1e-20,
+                               scale=1.0)
+    if not post_scale:
+        wts = torch.ones_like(wts)
+    return xn, logits, ids, wts, res_out
+
+
+@torch.library.custom_op("moe_fp8::moe_block_tkg_mx", mutates_args=())
+def _block_tkg_mx_op(x: Tensor, gamma: Tensor, router_weights: Tensor, gate_up: Tensor,
+                     down: Tensor, gate_up_scale: Tensor, down_scale: Tensor,
+                     gate_up_bias: Optional[Tensor], down_bias: Optional[Tensor],
+                     router_bias: Optional[Tensor], residual: Optional[Tensor], top_k: int,
+                     eps: float, scoring: int, pre_norm: bool, norm_topk_prob: bool,
+                     post_scale: bool, hidden_actual: int, act: str, gate_lo: float,
+                     gate_hi: float, up_lo: float, up_hi: float) -> Tuple[Tensor, Tensor, Tensor]:
+    """Opaque graph node of moe_block_tkg with MX experts (GPT-OSS decode,
+    model_bf16.py:1274-1307: Swish, clamps, biases). Returns (out, logits,
+    residual_out or an empty [0, H])."""
+    T, H = x.shape
+    ha = None if hidden_actual <= 0 else hidden_actual
+    xn, logits, ids, wts, res_out = _norm_route(x, gamma, router_weights, router_bias, residual,
+                                                top_k, eps, scoring, pre_norm, norm_topk_prob,
+                                                post_scale, ha)
+    w = _experts.mx_weights(gate_up, down, gate_up_scale, down_scale, gate_up_bias, down_bias)
+    none = lambda v: None if v != v else v
+    out = ops.mx_experts(_experts.as_bf16(xn).contiguous(), ids, wts, w, act,
+                         (none(gate_lo), none(gate_hi)), (none(up_lo), none(up_hi)))
+    if x.dtype != torch.bfloat16:
+        out = out.to(x.dtype)
+    if res_out is None:
+        res_out = x.new_empty(0, H, dtype=torch.bfloat16)
+    return out, logits, res_out
+
+
+@_block_tkg_mx_op.register_fake
+def _block_tkg_mx_fake(x, gamma, router_weights, gate_up, down, gate_up_scale, down_scale,
+                       gate_up_bias, down_bias, router_bias, residual, top_k, eps, scoring,
+                       pre_norm, norm_topk_prob, post_scale, hidden_actual, act, gate_lo, gate_hi,
+                       up_lo, up_hi):
     T, H = x.shape
     E = router_weights.shape[1]
     nres = 0 if residual is None or x.dtype != torch.bfloat16 else T
