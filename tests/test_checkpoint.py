@@ -124,3 +124,50 @@ def test_missing_and_misshaped_tensors_raise(tmp_path, small):
     os.makedirs(tmp_path / "empty")
     with pytest.raises(FileNotFoundError):
         load_moe_layer(str(tmp_path / "empty"), LAYER, cfg, device=None)
+
+
+def gpt_oss_hf_tensors(gub, gus, gb, db, ds, dbias, rw, rb, norm, layer=LAYER):
+    base = f"model.layers.{layer}"
+    ex = f"{base}.mlp.experts"
+    return {f"{ex}.gate_up_proj_blocks": gub, f"{ex}.gate_up_proj_scales": gus,
+            f"{ex}.gate_up_proj_bias": gb, f"{ex}.down_proj_blocks": db,
+            f"{ex}.down_proj_scales": ds, f"{ex}.down_proj_bias": dbias,
+            f"{base}.mlp.router.weight": rw, f"{base}.mlp.router.bias": rb,
+            f"{base}.post_attention_layernorm.weight": norm}
+
+
+def test_gpt_oss_mxfp4_checkpoint_round_trip(tmp_path):
+    """A GPT-OSS MXFP4 layer under the HF keys the reference maps (model_mxfp4.py:
+    2660-2695) loads into the oracle's stacked layout: gate / up de-interleaved, +1 on
+    the up bias, H and I zero-padded, codes and scales unchanged."""
+    import numpy as np
+
+    from oracle import mx as OX
+    from vllm_neuron_amd.checkpoint import load_gpt_oss_moe_layer
+    g = torch.Generator().manual_seed(9)
+    E, I, H = 4, 96, 160
+    gub = torch.randint(0, 256, (E, 2 * I, H // 32, 16), generator=g, dtype=torch.int32).to(torch.uint8)
+    gus = torch.randint(118, 134, (E, 2 * I, H // 32), generator=g, dtype=torch.int32).to(torch.uint8)
+    gb = torch.randn(E, 2 * I, generator=g).to(torch.bfloat16)
+    db = torch.randint(0, 256, (E, H, I // 32, 16), generator=g, dtype=torch.int32).to(torch.uint8)
+    ds = torch.randint(118, 134, (E, H, I // 32), generator=g, dtype=torch.int32).to(torch.uint8)
+    dbias = torch.randn(E, H, generator=g).to(torch.bfloat16)
+    rw = torch.randn(E, H, generator=g).to(torch.bfloat16)
+    rb = torch.randn(E, generator=g).to(torch.bfloat16)
+    norm = torch.randn(H, generator=g).to(torch.bfloat16)
+    save_file(gpt_oss_hf_tensors(gub, gus, gb, db, ds, dbias, rw, rb, norm),
+              str(tmp_path / "model.safetensors"))
+    w, nw = load_gpt_oss_moe_layer(str(tmp_path), LAYER, hidden=256, intermediate=128, device=None)
+    ow13, os13, ob13, ow2, os2, ob2 = OX.from_hf_gpt_oss(
+        gub.numpy(), gus.numpy(), gb.float().numpy(), db.numpy(), ds.numpy(), dbias.float().numpy())
+    assert np.array_equal(w.w13[:, :I, :H // 2].numpy(), ow13[:, :I])
+    assert np.array_equal(w.w13[:, 128:128 + I, :H // 2].numpy(), ow13[:, I:])
+    assert np.array_equal(w.w13_scale[:, 128:128 + I, :H // 32].numpy(), os13[:, I:])
+    assert np.array_equal(w.b13[:, 128:128 + I].numpy(), ob13[:, I:])
+    assert np.array_equal(w.w2[:, :H, :I // 2].numpy(), ow2)
+    assert np.array_equal(w.w2_scale[:, :H, :I // 32].numpy(), os2)
+    assert np.array_equal(w.b2[:, :H].numpy(), ob2)
+    assert torch.equal(w.router_w[:, :H], rw) and torch.all(w.router_w[:, H:] == 0)
+    assert torch.equal(nw[:H], norm.float()) and torch.all(nw[H:] == 0)
+    with pytest.raises(KeyError):
+        load_gpt_oss_moe_layer(str(tmp_path), LAYER + 1, device=None)

@@ -1,4 +1,5 @@
-"""Load one MoE layer of a DeepSeek-V3-format fp8 checkpoint (local safetensors files).
+"""Load one MoE layer of a local safetensors checkpoint: DeepSeek-V3-format fp8
+experts (load_moe_layer) or GPT-OSS MXFP4 experts (load_gpt_oss_moe_layer).
 
 DeepSeek-V3, Kimi-K2 and GLM-4.5 publish their MoE layers under the same keys:
 
@@ -144,3 +145,53 @@ def load_moe_layer(path: str, layer: int, cfg, device="cuda", prefix: str = "mod
     w = Fp8MoEWeights(router_w=router_w, w13=w13, w13_scale=s13, w2=w2, w2_scale=s2,
                       corr_bias=corr, **kw).validate()
     return w.to(device) if device is not None else w
+
+
+def load_gpt_oss_moe_layer(path: str, layer: int, hidden: Optional[int] = None,
+                           intermediate: Optional[int] = None, device="cuda",
+                           prefix: str = "model.layers",
+                           index: Optional[CheckpointIndex] = None):
+    """(MxMoEWeights, norm_weight) of MoE layer ``layer`` of a local HF GPT-OSS MXFP4
+    checkpoint, under the keys the reference maps (model_mxfp4.py:2660-2695):
+
+        {prefix}.{L}.mlp.router.weight / .bias                     [E, H] / [E]
+        {prefix}.{L}.mlp.experts.gate_up_proj_blocks / _scales / _bias
+                                      [E, 2I, H/32, 16] uint8 / [E, 2I, H/32] / [E, 2I]
+        {prefix}.{L}.mlp.experts.down_proj_blocks / _scales / _bias
+                                      [E, H, I/32, 16] uint8 / [E, H, I/32] / [E, H]
+        {prefix}.{L}.post_attention_layernorm.weight                [H]
+
+    Gate and up are de-interleaved and the up bias gets +1 as the reference's loaders
+    do (weight_loaders_mxfp4.py:301-464); hidden / intermediate pad H and I with zeros
+    (GPT-OSS: 2880 -> 3072). Codes and scales are not changed."""
+    from .weights_mx import from_hf_gpt_oss
+    ix = index or CheckpointIndex(path)
+    base = f"{prefix}.{layer}"
+    ex = f"{base}.mlp.experts"
+    gub = ix.get(f"{ex}.gate_up_proj_blocks")
+    if gub.dtype != torch.uint8 or gub.dim() != 4 or gub.shape[-1] != 16:
+        raise ValueError(f"{ex}.gate_up_proj_blocks: expected uint8 [E, 2I, H/32, 16], got "
+                         f"{gub.dtype} {tuple(gub.shape)}")
+    E, I2, HB, _ = gub.shape
+    H, I = HB * 32, I2 // 2
+    gus = _check(ix.get(f"{ex}.gate_up_proj_scales"), (E, I2, HB), torch.uint8,
+                 f"{ex}.gate_up_proj_scales")
+    gb = _check(ix.get(f"{ex}.gate_up_proj_bias"), (E, I2), None, f"{ex}.gate_up_proj_bias")
+    db = _check(ix.get(f"{ex}.down_proj_blocks"), (E, H, I // 32, 16), torch.uint8,
+                f"{ex}.down_proj_blocks")
+    ds = _check(ix.get(f"{ex}.down_proj_scales"), (E, H, I // 32), torch.uint8,
+                f"{ex}.down_proj_scales")
+    dbias = _check(ix.get(f"{ex}.down_proj_bias"), (E, H), None, f"{ex}.down_proj_bias")
+    rw = _check(ix.get(f"{base}.mlp.router.weight"), (E, H), None, f"{base}.mlp.router.weight")
+    rb = _check(ix.get(f"{base}.mlp.router.bias"), (E,), None, f"{base}.mlp.router.bias")
+    kn = f"{base}.post_attention_layernorm.weight"
+    norm = _check(ix.get(kn), (H,), None, kn).float() if kn in ix else None
+    w = from_hf_gpt_oss(gub, gus, gb, db, ds, dbias, rw, rb, hidden=hidden,
+                        intermediate=intermediate)
+    if norm is not None and hidden is not None and hidden > H:
+        norm = torch.cat([norm, torch.zeros(hidden - H)])
+    if device is not None:
+        w = type(w)(**{k: (v.to(device) if isinstance(v, torch.Tensor) else v)
+                       for k, v in w.__dict__.items()})
+        norm = None if norm is None else norm.to(device)
+    return w, norm
