@@ -121,12 +121,13 @@ def test_layer_row_tile_heights_agree(cuda):
     assert rel_l2(np_f32(ref), np_f32(outs[0])) < 5e-3
 
 
-@pytest.mark.parametrize("T,E", [(64, 64), (4096, 128)])
+@pytest.mark.parametrize("T,E", [(64, 64), (4096, 128), (1, 384), (7, 1024)])
 def test_layer_router_matches_op_path(cuda, T, E):
     """Inside the layer the top-k kernel sums the router's split-K partials itself (28
-    partials at 64 tokens; 8 from the 128-token wide tiles at 4096). Logits, ids and
-    weights equal, bit for bit, those of ops.router_logits (reduce kernel) followed by
-    ops.router_topk."""
+    partials at 64 tokens and below; 8 from the 128-token wide tiles at 4096), a
+    workgroup's four tokens at a time (one token at T = 1, three in the last workgroup
+    at T = 7). Logits, ids and weights equal, bit for bit, those of ops.router_logits
+    (reduce kernel) followed by ops.router_topk."""
     cfg = PRESETS["dsv3"].with_(n_experts=E, intermediate=128, n_group=8, topk_group=4)
     say("layer router vs op path", T, E)
     w = synthetic.make_weights(cfg, 30 + E, device=cuda)

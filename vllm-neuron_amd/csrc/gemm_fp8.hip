@@ -19,9 +19,8 @@
 //
 // K loop: one v_mfma_f32_16x16x128_f8f6f4 per 128-wide K block (exactly one
 // scale block), accumulated in fp32 as acc += mfma(a, b) * (s_a[row] * s_w).
-// Activation rows are gathered into LDS (double buffered); weight fragments
-// stream from HBM straight into registers with a PD-deep prefetch ring, as
-// each weight byte is used by exactly one lane.
+// Weights, gathered activation rows and their scales stream into a PD-stage LDS
+// ring with direct-to-LDS loads (see expert_gemm_kernel below).
 //
 // Operand lane layout: lane l supplies row l%16 and the 32 bytes
 // [(l/16)*16, +16) and [64 + (l/16)*16, +16) of the K block. A and B use the
@@ -61,20 +60,98 @@ __device__ __forceinline__ v8i load_frag_global(const uint8_t* p) {
   return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 }
 
-__device__ __forceinline__ v8i load_frag_lds(const uint8_t* p) {
-  int4 lo = *(const int4*)p;
-  int4 hi = *(const int4*)(p + 64);
-  return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+// ---------------------------------------------------------------------------
+// The row-tile kernel. Weight rows stream with global_load_lds_dwordx4 in which
+// eight lanes cover one 128-byte row segment, so every load instruction reads
+// eight whole cache lines. Loading the MFMA operand layout straight into
+// registers reads, per instruction, the halves of sixteen lines instead, which
+// measured at about half the stream rate per workgroup (2.7 against 5.5 TB/s
+// with 144 workgroups streaming 264 MB), the regime of decode with few
+// tokens. The activation tile and its scales arrive the same way, so a K
+// step's loads are all direct-to-LDS and one vmcnt wait per step covers a stage.
+//
+// LDS per stage: wave w's 64 weight rows (8 KB: eight 1 KB loads of 8 rows),
+// the tile's activation rows (1 KB per 8 rows) and its 1x128 scales. Rows keep
+// the XOR chunk swizzle (swz), so the 16-row fragment reads are conflict-free.
+// Weights are wave-private (a wave reads only the rows it loads); activations
+// and scales are shared, ordered by one barrier per step. Every wave issues the
+// same number of loads per stage (NV; waves without activation rows to load
+// repeat row 0 into a spare slot), so the wait for the oldest stage is a
+// compile-time vmcnt.
+// ---------------------------------------------------------------------------
+constexpr int kRowTileMaxKB = 128;  // K <= 16384
+
+// LDS byte address of a pointer into a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
+  return (uint32_t)(uintptr_t)(lds_cptr)p;
 }
+
+// A step's fragment reads, each group in one asm statement that also waits for
+// its data: the compiler does not see these as reads of memory that
+// direct-to-LDS loads write, so it does not drain the loads in flight into the
+// other stages before them (it cannot tell the stages apart across the loop),
+// and the registers are complete when the statement ends.
+//   weights: 4 column tiles x (lo, hi) at b_lo / b_hi + 2048 j; activations
+//   (lo, hi) at a_lo / a_hi; the row group's 4 activation scales at sp.
+typedef int v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_read_b_a(uint32_t b_lo, uint32_t b_hi, uint32_t a_lo,
+                                             uint32_t a_hi, uint32_t sp, v4i (&b)[8], v4i& al,
+                                             v4i& ah, v4i& sa) {
+  asm volatile(
+      "ds_read_b128 %0, %11\n\t"
+      "ds_read_b128 %1, %12\n\t"
+      "ds_read_b128 %2, %11 offset:2048\n\t"
+      "ds_read_b128 %3, %12 offset:2048\n\t"
+      "ds_read_b128 %4, %11 offset:4096\n\t"
+      "ds_read_b128 %5, %12 offset:4096\n\t"
+      "ds_read_b128 %6, %11 offset:6144\n\t"
+      "ds_read_b128 %7, %12 offset:6144\n\t"
+      "ds_read_b128 %8, %13\n\t"
+      "ds_read_b128 %9, %14\n\t"
+      "ds_read_b128 %10, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]),
+        "=&v"(b[6]), "=&v"(b[7]), "=&v"(al), "=&v"(ah), "=&v"(sa)
+      : "v"(b_lo), "v"(b_hi), "v"(a_lo), "v"(a_hi), "v"(sp)
+      : "memory");
+}
+__device__ __forceinline__ void lds_read_a(uint32_t a_lo, uint32_t a_hi, uint32_t sp, v4i& al,
+                                           v4i& ah, v4i& sa) {
+  asm volatile(
+      "ds_read_b128 %0, %3\n\t"
+      "ds_read_b128 %1, %4\n\t"
+      "ds_read_b128 %2, %5\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(al), "=&v"(ah), "=&v"(sa)
+      : "v"(a_lo), "v"(a_hi), "v"(sp)
+      : "memory");
+}
+
+// One pipeline stage. Each stage is its own LDS object: the compiler then tells
+// the fragment reads of one stage from the direct-to-LDS loads in flight into the
+// others (it tracks such loads per LDS object) and does not drain them all.
+template <int MT>
+struct RowTileStage {
+  uint8_t b[4][8192];                       // wave w's 64 weight rows x 128 bytes
+  uint8_t a[MT / 8 + 1][1024];              // activation rows, 8 per slot (+ a spare slot)
+  float as[(MT + 63) / 64 + 1][64];         // activation scales (+ a spare slot)
+};
 
 template <int MT, int KIND, int PD>
 __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
   constexpr int MS = MT / 16;
-  constexpr int ACH = MT * 8;                 // 16-byte chunks per A tile per K block
-  constexpr int APT = (ACH + 255) / 256;      // chunks per thread
-  constexpr int LDA = 128 + 16;               // padded LDS row (bytes)
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][MT * LDA];
-  __shared__ __attribute__((aligned(16))) float sAs[2][MT];
+  constexpr int AQ = MT / 8;                // activation loads (8 rows) per stage
+  constexpr int NA = (AQ + 3) / 4;          // ... per wave (spare ones go to slot AQ)
+  constexpr int NSQ = (MT + 63) / 64;       // scale loads (64 rows) per stage
+  constexpr int NV = 8 + NA + 1;            // direct-to-LDS loads per wave per stage
+  static_assert(PD >= 2 && PD <= 4 && (PD - 2) * NV < 64, "pipeline depth");
+  using Stage = RowTileStage<MT>;
+  __shared__ __attribute__((aligned(1024))) Stage st0;
+  __shared__ __attribute__((aligned(1024))) Stage st1;
+  __shared__ __attribute__((aligned(1024))) Stage st2;
+  __shared__ __attribute__((aligned(1024))) Stage st3;
+  __shared__ float sWs[2][kRowTileMaxKB];
   __shared__ long sSrc[MT];
   __shared__ float sRed[4][MT];
 
@@ -95,6 +172,15 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
     const bool is_sh = e >= p.E;
     const int ej = is_sh ? e - p.E : e;
 
+    const uint8_t* wb;
+    const float* wsb;
+    if (KIND == 0) {
+      wb = (is_sh ? p.wsh : p.w) + (size_t)ej * 2 * p.I * p.H;
+      wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (2 * p.I / 128) * KB;
+    } else {
+      wb = (is_sh ? p.wsh : p.w) + (size_t)ej * p.H * p.I;
+      wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (p.H / 128) * KB;
+    }
     if (tid < MT) {
       long src = -1;
       if (tid < nrows) {
@@ -108,78 +194,59 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
       }
       sSrc[tid] = src;
     }
+    // weight block scales of the tile's two 128-row halves: gate / up blocks
+    // (gate_up) or the two output blocks (down)
+    for (int i = tid; i < 2 * KB; i += 256) {
+      const int h = i / KB, kb = i - h * KB;
+      const int rb = (KIND == 0) ? (h == 0 ? nt : p.I / 128 + nt) : nt * 2 + h;
+      sWs[h][kb] = wsb[(size_t)rb * KB + kb];
+    }
     __syncthreads();
 
-    // Activation chunk sources. Every load below is issued unconditionally (chunks
-    // and scales without a row read row 0 and are zeroed after the load), so the
-    // compiler counts the loads in flight exactly and keeps the weight prefetch
-    // ring in flight instead of draining it.
-    const uint8_t* aptr[APT];
-    int aoff[APT];
-    bool alive[APT];
+    // Load sources. Weight load i of wave w: rows [8i, 8i + 8) of the wave's 64
+    // (16-row column tile j = i / 2), lane l -> row 8 (i & 1) + l / 8 of the
+    // column tile, stored chunk l % 8 = logical chunk swz(row, l % 8).
+    uint32_t boff[8];
 #pragma unroll
-    for (int c = 0; c < APT; ++c) {
-      const int chunk = tid + 256 * c;
-      aptr[c] = p.a;
-      aoff[c] = -1;
-      alive[c] = false;
-      if (chunk < ACH) {
-        const int row = chunk >> 3, col = (chunk & 7) * 16;
-        aoff[c] = row * LDA + col;
-        const long src = sSrc[row];
-        if (src >= 0) {
-          aptr[c] = p.a + (size_t)src * Kdim + col;
-          alive[c] = true;
-        }
-      }
-    }
-    const bool as_alive = tid < MT && sSrc[tid] >= 0;
-    const float* asp = as_alive ? p.as + (size_t)sSrc[tid] * KB : p.as;
-
-    // weight fragments and scale rows
-    const uint8_t* wb;
-    const float* wsb;
-    if (KIND == 0) {
-      wb = (is_sh ? p.wsh : p.w) + (size_t)ej * 2 * p.I * p.H;
-      wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (2 * p.I / 128) * KB;
-    } else {
-      wb = (is_sh ? p.wsh : p.w) + (size_t)ej * p.H * p.I;
-      wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (p.H / 128) * KB;
-    }
-    const uint8_t* bp[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int i = 0; i < 8; ++i) {
+      const int j = i >> 1, rr = (i & 1) * 8 + (lane >> 3);
       int row;
       if (KIND == 0)
-        row = (j < 2) ? nt * 128 + wave * 32 + j * 16 + r16
-                      : p.I + nt * 128 + wave * 32 + (j - 2) * 16 + r16;
+        row = (j < 2) ? nt * 128 + wave * 32 + j * 16 + rr
+                      : p.I + nt * 128 + wave * 32 + (j - 2) * 16 + rr;
       else
-        row = nt * 256 + wave * 64 + j * 16 + r16;
-      bp[j] = wb + (size_t)row * Kdim + g * 16;
+        row = nt * 256 + wave * 64 + j * 16 + rr;
+      boff[i] = (uint32_t)row * (uint32_t)Kdim + (uint32_t)swz(rr, lane & 7) * 16;
     }
-    const float* sw0 = (KIND == 0) ? wsb + (size_t)nt * KB : wsb + (size_t)(nt * 2 + (wave >> 1)) * KB;
-    const float* sw1 = (KIND == 0) ? wsb + (size_t)(p.I / 128 + nt) * KB : sw0;
+    // Activation load a of wave w: tile rows [8q, 8q + 8), q = w NA + a (q >= AQ:
+    // a spare load of row 0 into slot AQ). Rows without a source read row 0; their
+    // products are never stored.
+    const uint8_t* aptr[NA];
+    int aslot[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      const int q = wave * NA + a;
+      const int r = q * 8 + (lane >> 3);
+      long src = 0;
+      if (q < AQ && sSrc[r] >= 0) src = sSrc[r];
+      aslot[a] = q < AQ ? q : AQ;
+      aptr[a] = p.a + (size_t)src * Kdim + swz(r, lane & 7) * 16;
+    }
+    // Scale load: wave w < NSQ fills the scales of rows [64 w, 64 w + 64).
+    long ssrc = 0;
+    {
+      const int r = wave * 64 + lane;
+      if (wave < NSQ && r < MT && sSrc[r] >= 0) ssrc = sSrc[r];
+    }
+    const float* asp = p.as + (size_t)ssrc * KB;
+    const int sslot = wave < NSQ ? wave : NSQ;
 
-    v8i bq[PD][4];
-    int4 aq[PD][APT];
-    float asq[PD];
-    float swq[PD][2];
-
-    auto load_stage = [&](int slot, int kb) {
+    auto issue = [&](Stage& S, int kb) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bq[slot][j] = load_frag_global(bp[j] + (size_t)kb * MOE_GROUP);
+      for (int i = 0; i < 8; ++i) load_lds16(wb + boff[i] + (size_t)kb * MOE_GROUP, &S.b[wave][i * 1024]);
 #pragma unroll
-      for (int c = 0; c < APT; ++c)
-        aq[slot][c] = *(const int4*)(aptr[c] + (alive[c] ? (size_t)kb * MOE_GROUP : 0));
-      asq[slot] = asp[as_alive ? kb : 0];
-      swq[slot][0] = sw0[kb];
-      swq[slot][1] = sw1[kb];
-    };
-    auto store_A = [&](int buf, int slot) {
-#pragma unroll
-      for (int c = 0; c < APT; ++c)
-        if (aoff[c] >= 0) *(int4*)&sA[buf][aoff[c]] = alive[c] ? aq[slot][c] : make_int4(0, 0, 0, 0);
-      if (tid < MT) sAs[buf][tid] = as_alive ? asq[slot] : 0.f;
+      for (int a = 0; a < NA; ++a) load_lds16(aptr[a] + (size_t)kb * MOE_GROUP, &S.a[aslot[a]][0]);
+      load_lds4(asp + kb, (uint8_t*)&S.as[sslot][0]);
     };
 
     v4f acc[MS][4];
@@ -188,41 +255,71 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[ms][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-    for (int s = 0; s < PD - 1; ++s) load_stage(s, min(s, KB - 1));
-    store_A(0, 0);
-    __syncthreads();
+    // Fragment reads: row r16 of a 16-row group sits in load slot 2m + r16 / 8 at
+    // byte (r16 % 8) * 128; its logical chunks g and 4 + g are stored swizzled.
+    const int fr = (r16 >> 3) * 1024 + (r16 & 7) * 128;
+    const int o_lo = fr + swz(r16, g) * 16, o_hi = fr + swz(r16, 4 + g) * 16;
+    auto cat = [](const v4i& lo, const v4i& hi) -> v8i {
+      return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    };
 
-    // One K block: prefetch block kb + PD - 1 (past the end, the last block again,
-    // into a slot that is not read again), MFMAs of block kb from slot s, stage
-    // block kb + 1's activations into the other LDS buffer.
-    auto kstep = [&](int kb, int s) {
-      load_stage((s + PD - 1) % PD, min(kb + PD - 1, KB - 1));
-      const int buf = kb & 1;
+    // Step kb: wait for block kb (stage cur), then load block kb + PD - 1 into the
+    // stage block kb - 1 used (nxt; past the end, the last block again into a
+    // stage that is not read again, so the waits stay exact) and multiply block kb.
+    auto step = [&](int kb, Stage& cur, Stage& nxt) {
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm<(PD - 2) * NV>();      // this wave's share of block kb has landed
+      __builtin_amdgcn_s_barrier();  // ... every wave's, and block kb - 1 is consumed
+      __builtin_amdgcn_sched_barrier(0);
+      issue(nxt, min(kb + PD - 1, KB - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      const float sw0 = (KIND == 0) ? sWs[0][kb] : sWs[wave >> 1][kb];
+      const float sw1 = (KIND == 0) ? sWs[1][kb] : sw0;
+      const uint32_t bw = lds_addr(&cur.b[wave][0]), aw = lds_addr(&cur.a[0][0]);
+      v4i bq[8];
+      v8i b[4];
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) {
-        const v8i a = load_frag_lds(&sA[buf][(ms * 16 + r16) * LDA + g * 16]);
-        const v4f sa = *(const v4f*)&sAs[buf][ms * 16 + 4 * g];
-        const v4f c0 = sa * swq[s][0];
-        const v4f c1 = sa * swq[s][1];
+        v4i alo, ahi, sai;
+        const uint32_t sp = lds_addr(&cur.as[(ms * 16) >> 6][(ms * 16 + 4 * g) & 63]);
+        if (ms == 0) {
+          lds_read_b_a(bw + o_lo, bw + o_hi, aw + o_lo, aw + o_hi, sp, bq, alo, ahi, sai);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) b[j] = cat(bq[2 * j], bq[2 * j + 1]);
+        } else {
+          lds_read_a(aw + 2048 * ms + o_lo, aw + 2048 * ms + o_hi, sp, alo, ahi, sai);
+        }
+        const v8i a = cat(alo, ahi);
+        const v4f sa = {__int_as_float(sai.x), __int_as_float(sai.y), __int_as_float(sai.z), __int_as_float(sai.w)};
+        const v4f c0 = sa * sw0;
+        const v4f c1 = sa * sw1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const v4f part = mfma_fp8(a, bq[s][j]);
+          const v4f part = mfma_fp8(a, b[j]);
           acc[ms][j] += part * ((KIND == 0 && j >= 2) ? c1 : c0);
         }
       }
-      if (kb + 1 < KB) store_A((kb + 1) & 1, (s + 1) % PD);
-      // Orders the activation double buffer only; the weight prefetches stay in flight.
-      lds_barrier();
     };
-    int kb0 = 0;
-    for (; kb0 + PD <= KB; kb0 += PD) {
-#pragma unroll
-      for (int s = 0; s < PD; ++s) kstep(kb0 + s, s);
+    wait_vm<0>();  // no earlier load is still landing in a stage buffer
+    issue(st0, 0);
+    if (PD >= 3) issue(st1, min(1, KB - 1));
+    if (PD >= 4) issue(st2, min(2, KB - 1));
+    for (int kb = 0; kb < KB; kb += PD) {
+      if (PD == 2) {
+        step(kb, st0, st1);
+        if (kb + 1 < KB) step(kb + 1, st1, st0);
+      } else if (PD == 3) {
+        step(kb, st0, st2);
+        if (kb + 1 < KB) step(kb + 1, st1, st0);
+        if (kb + 2 < KB) step(kb + 2, st2, st1);
+      } else {
+        step(kb, st0, st3);
+        if (kb + 1 < KB) step(kb + 1, st1, st0);
+        if (kb + 2 < KB) step(kb + 2, st2, st1);
+        if (kb + 3 < KB) step(kb + 3, st3, st2);
+      }
     }
-#pragma unroll
-    for (int s = 0; s < PD - 1; ++s)
-      if (kb0 + s < KB) kstep(kb0 + s, s);
+    wait_vm<0>();  // the tail's repeated loads land before the stages are reused
 
     if (KIND == 0) {
       // h = SiLU(gate) * up, written over the gate accumulators.
@@ -329,7 +426,7 @@ static int launch_gemm(const GemmArgs& a, int max_tiles, int mt, hipStream_t st)
       hipLaunchKernelGGL((expert_gemm_kernel<32, KIND, 3>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 64:
-      hipLaunchKernelGGL((expert_gemm_kernel<64, KIND, 2>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((expert_gemm_kernel<64, KIND, 3>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 128:
       hipLaunchKernelGGL((expert_gemm_kernel<128, KIND, 2>), dim3(grid), dim3(256), 0, st, a);
@@ -359,6 +456,9 @@ extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int
   MOE_CHECK_ARG(T > 0 && E > 0 && NB >= 0 && max_tiles > 0, "bad sizes");
   MOE_CHECK_ARG(H > 0 && H % 128 == 0 && I > 0 && I % 128 == 0,
                 "H and I must be positive multiples of 128 (H=%d I=%d)", H, I);
+  MOE_CHECK_SUPPORTED(H <= 128 * kRowTileMaxKB && I <= 128 * kRowTileMaxKB && 2L * I * H < (1L << 32),
+                      "H and I up to %d and one expert's weights under 4 GiB (H=%d I=%d)",
+                      128 * kRowTileMaxKB, H, I);
   MOE_CHECK_ARG(n_shared == 0 || (w13_shared && w13_shared_scale), "shared weights missing");
   MOE_CHECK_ARG(mt == 16 || mt == 32 || mt == 64 || mt == 128, "mt must be 16/32/64/128");
   MOE_CHECK_ALIGN16(xq);
@@ -397,6 +497,9 @@ extern "C" int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H,
   MOE_CHECK_ARG(T > 0 && E > 0 && NB >= 0 && max_tiles > 0, "bad sizes");
   MOE_CHECK_ARG(H > 0 && H % 256 == 0 && I > 0 && I % 128 == 0,
                 "H must be a multiple of 256 and I of 128 (H=%d I=%d)", H, I);
+  MOE_CHECK_SUPPORTED(H <= 128 * kRowTileMaxKB && I <= 128 * kRowTileMaxKB && 2L * I * H < (1L << 32),
+                      "H and I up to %d and one expert's weights under 4 GiB (H=%d I=%d)",
+                      128 * kRowTileMaxKB, H, I);
   MOE_CHECK_ARG(n_shared == 0 || (w2_shared && w2_shared_scale), "shared weights missing");
   MOE_CHECK_ARG(mt == 16 || mt == 32 || mt == 64 || mt == 128, "mt must be 16/32/64/128");
   MOE_CHECK_ALIGN16(hq);

@@ -66,21 +66,6 @@ __device__ __forceinline__ v4f mfma16_fp8_acc(const v8i& a, const v8i& b, const 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-__device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
-}
-
-__device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 4, 0, 0);
-}
-
-
-// Logical 16-byte chunk c of row r lives at chunk c ^ ((r >> 1) & 7): any 16
-// consecutive rows read at one logical chunk touch 16 distinct 16-byte bank
-// groups of the 64-bank LDS (two 128-byte rows span the banks once).
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 // The workgroup's LDS, allocated once by the kernel. The pipeline stages are
 // distinct objects, so the compiler can tell that fragment reads of one stage do

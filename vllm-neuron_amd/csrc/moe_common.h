@@ -119,6 +119,23 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// Direct-to-LDS loads (global_load_lds_dwordx4 / _dword): lane l's 16 (4) bytes
+// from g land at lds_wave_base + 16 l (4 l); completion is counted by vmcnt.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 4, 0, 0);
+}
+
+// Logical 16-byte chunk c of row r lives at chunk c ^ ((r >> 1) & 7): any 16
+// consecutive rows read at one logical chunk touch 16 distinct 16-byte bank
+// groups of the 64-bank LDS (two 128-byte rows span the banks once).
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
 // Workgroup barrier that waits only for this wave's LDS operations (lgkmcnt).
 // __syncthreads() also drains vmcnt: it waits for every global load in flight,
 // prefetches included. Direct-to-LDS data needs its own explicit vmcnt wait.

@@ -371,51 +371,65 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   __shared__ float s_key[4][PM * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;  // wave-uniform; no workgroup barrier below
-  const float* row = logits + (size_t)t * E;
   const int P = (E + 63) / 64;
   const float NEG_INF = -__builtin_inff();
   const bool need_act = order != MOE_ORDER_TOPK_ACT;
 
+  // The correction bias is loaded first so its latency overlaps the logits' loads.
+  float cb[PM];
+#pragma unroll
+  for (int j = 0; j < PM; ++j) {
+    const int e = lane + 64 * j;
+    cb[j] = (order == MOE_ORDER_GROUPED && corr_bias != nullptr && j < P && e < E) ? corr_bias[e] : 0.f;
+  }
+
+  if (part != nullptr) {
+    // Split-K partials [ksplit, T, E] summed by the whole workgroup for its (up to)
+    // four tokens, in split order and then + bias, exactly as router_logits_reduce
+    // does; the sums are also written to logits_out. A thread owns (token, expert)
+    // pairs and keeps up to 32 partial loads in flight, so a single token (decode)
+    // costs one memory round trip per pair for up to 32 splits (H / 256 splits up
+    // to H = 8192) instead of one per pair of splits. The sums are staged in
+    // s_act[token], which each wave reads back for its own token below before it
+    // writes activations there.
+    constexpr int Q = 32;
+    const size_t TE = (size_t)T * E;
+    const int t0 = blockIdx.x * 4;
+    const int npairs = min(4, T - t0) * E;
+    for (int q = threadIdx.x; q < npairs; q += 256) {
+      const int tl = q / E, e = q - tl * E;
+      const float* src = part + (size_t)(t0 + tl) * E + e;
+      const float bv = (lbias != nullptr) ? lbias[e] : 0.f;
+      float sum = 0.f;
+      for (int k0 = 0; k0 < ksplit; k0 += Q) {
+        float v[Q];
+#pragma unroll
+        for (int u = 0; u < Q; ++u) v[u] = src[(size_t)min(k0 + u, ksplit - 1) * TE];
+#pragma unroll
+        for (int u = 0; u < Q; ++u)
+          if (k0 + u < ksplit) sum += v[u];
+      }
+      const float lgv = (lbias != nullptr) ? sum + bv : sum;
+      if (logits_out != nullptr) logits_out[(size_t)(t0 + tl) * E + e] = lgv;
+      s_act[tl][e] = lgv;
+    }
+    __syncthreads();
+  }
+  if (t >= T) return;  // wave-uniform; no workgroup barrier below
+
   float lg[PM];
   if (part == nullptr) {
+    const float* row = logits + (size_t)t * E;
 #pragma unroll
     for (int j = 0; j < PM; ++j) {
       int e = lane + 64 * j;
       lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
     }
   } else {
-    // Split-K partials [ksplit, T, E] summed here, in split order and then + bias,
-    // exactly as router_logits_reduce does; the sums are also written to logits_out.
-    constexpr int Q = (PM >= 8) ? 2 : 8;
-    const size_t TE = (size_t)T * E;
-    float sum[PM];
-#pragma unroll
-    for (int j = 0; j < PM; ++j) sum[j] = 0.f;
-    for (int k0 = 0; k0 < ksplit; k0 += Q) {
-      float v[Q][PM];
-#pragma unroll
-      for (int q = 0; q < Q; ++q)
-#pragma unroll
-        for (int j = 0; j < PM; ++j) {
-          const int e = lane + 64 * j;
-          v[q][j] = (j < P && e < E) ? part[(size_t)min(k0 + q, ksplit - 1) * TE + (size_t)t * E + e] : 0.f;
-        }
-#pragma unroll
-      for (int q = 0; q < Q; ++q)
-        if (k0 + q < ksplit)
-#pragma unroll
-          for (int j = 0; j < PM; ++j) sum[j] += v[q][j];
-    }
 #pragma unroll
     for (int j = 0; j < PM; ++j) {
-      const int e = lane + 64 * j;
-      if (j < P && e < E) {
-        lg[j] = (lbias != nullptr) ? sum[j] + lbias[e] : sum[j];
-        if (logits_out != nullptr) logits_out[(size_t)t * E + e] = lg[j];
-      } else {
-        lg[j] = NEG_INF;
-      }
+      int e = lane + 64 * j;
+      lg[j] = (j < P && e < E) ? s_act[wave][e] : NEG_INF;
     }
   }
 
@@ -465,7 +479,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       } else if (order == MOE_ORDER_ACT_TOPK) {
         kv = s_act[wave][e];
       } else {
-        kv = s_act[wave][e] + (corr_bias != nullptr ? corr_bias[e] : 0.f);
+        kv = s_act[wave][e] + cb[j];
       }
       s_key[wave][e] = kv;
     }
