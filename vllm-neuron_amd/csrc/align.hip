@@ -196,10 +196,13 @@ __device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __r
     const int c = s_cnt[e];
     const long base = (long)(s_blk[e] - (c + B - 1) / B) * B;
     if (to.span) {
-      const long in_e = (long)loc * mt;  // first slot of the tile, relative to the expert
+      // the expert's ceil(c / mt) tiles share its rows equally, so sibling tiles
+      // advance through K at the same rate and share each weight block in L2
+      const int ntl = s_tile[e] - first, h = (c + ntl - 1) / ntl;
+      const long in_e = (long)loc * h;  // first slot of the tile, relative to the expert
       const long row = to.compact ? s_cex[e] + in_e : base + in_e;
-      to.tiles[i] = make_int4(e, (int)(base + in_e), min(mt, c - loc * mt), (int)row);
-      to.seg[i] = make_int2(first, s_tile[e] - first);
+      to.tiles[i] = make_int4(e, (int)(base + in_e), min(h, c - loc * h), (int)row);
+      to.seg[i] = make_int2(first, ntl);
     } else {
       const int j = loc / tpb, m = loc - j * tpb;
       const int rows = min(B, c - j * B);
@@ -209,13 +212,14 @@ __device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __r
     }
   }
   const int per = (T + mt - 1) / mt;
+  const int hsh = to.span ? (T + per - 1) / per : mt;  // equal block-tile heights
   const long nb_total = (long)N * B;
   const long row_sh = to.compact ? to.row_shared : nb_total;
   for (int i = tid; i < to.n_shared * per; i += blockDim.x) {
     const int j = i / per, m = i - j * per, idx = ntiles + i;
     if (idx < to.max_tiles) {
-      const long in_sh = (long)j * T + (long)m * mt;
-      to.tiles[idx] = make_int4(E + j, (int)(nb_total + in_sh), min(mt, T - m * mt), (int)(row_sh + in_sh));
+      const long in_sh = (long)j * T + (long)m * hsh;
+      to.tiles[idx] = make_int4(E + j, (int)(nb_total + in_sh), min(hsh, T - m * hsh), (int)(row_sh + in_sh));
       if (to.span) to.seg[idx] = make_int2(ntiles + j * per, per);
     }
   }

@@ -25,7 +25,13 @@
 //  * work items (row tile, column tile) are enumerated expert by expert, column
 //    tile by column tile, and mapped so that one XCD runs the items of one
 //    expert together: the row tiles of an expert share each weight tile through
-//    the XCD's L2, and the column tiles share the activation rows.
+//    the XCD's L2, and the column tiles share the activation rows. An expert's
+//    ceil(rows / 256) row tiles split its rows equally, so sibling tiles advance
+//    through K at the same pace and read each weight block once from HBM (a
+//    256-row tile next to a short remainder tile left it behind: 12.3 GB read
+//    for 7.6 GB of weights at 8192 tokens, 9.6 GB with equal tiles);
+//  * the next block's loads are spread among the MFMAs of the current one,
+//    weights first (6 % faster gate_up than issuing them at once).
 //
 // Fragment lane layout (16x16x128): lane l supplies row l%16 and the bytes
 // [(l/16)*16, +16) and [64 + (l/16)*16, +16) of the 128-wide K block, the same
@@ -236,7 +242,22 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   };
   auto brow0 = [](int n) { return (KIND == 0) ? ((n < 4) ? 16 * n : 128 + 16 * (n - 4)) : 16 * n; };
 
-  auto compute = [&](const uint8_t* sa, const uint8_t* sb, const float* sr) {
+  // Load i of issue(), alone: the computing waves spread the next block's loads
+  // over the eight column tiles of the current one, weights (loads 4-7, and the
+  // scales) first, which keeps the load path and the LDS writes from arriving as
+  // one burst at the start of the step.
+  auto issue_part = [&](int i, uint8_t* sa, uint8_t* sb, uint8_t* ss, int kb) {
+    if (i == 4) load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, ss + sa_dst);
+    if (i < 4) {
+      if (a_live[i]) load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (4 * wave + i) * 1024);
+    } else {
+      load_lds16(wb + off[i] + (size_t)kb * kBK, sb + (4 * wave + i - 4) * 1024);
+    }
+  };
+  // MFMAs of the current block (stage sa / sb, ratios sr) with the loads of block
+  // kn into the next stage (na / nb / nsa) issued along the way.
+  auto compute = [&](const uint8_t* sa, const uint8_t* sb, const float* sr, uint8_t* na,
+                     uint8_t* nb, uint8_t* nsa, int kn) {
     const uint8_t* ta = sa + a_wave;
     const uint8_t* tb = sb + b_wave;
     v8i a[MF];
@@ -246,35 +267,32 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
       a[m] = frag(ta + 16 * m * kBK);
       rr[m] = *(const v4f*)&sr[((KIND == 0) ? 0 : wn) * kBM + RG * wm + 16 * m + 4 * g];
     }
-    // B fragments double-buffered: the reads of column tile n + 1 are issued
-    // before the MFMAs of tile n, so LDS latency hides under them.
+    // B fragments double-buffered: the reads of column tile n + 1 (and, at the
+    // gate / up boundary, the up-half ratios) are issued before the MFMAs of tile
+    // n, fenced off from them so the scheduler does not sink them to their use.
     v8i b = frag(tb + brow0(0) * kBK);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
+      issue_part((n + 4) & 7, na, nb, nsa, kn);
       v8i bn = b;
       if (n + 1 < 8) bn = frag(tb + brow0(n + 1) * kBK);
+      v4f rn[MF];
+#pragma unroll
+      for (int m = 0; m < MF; ++m) {
+        rn[m] = rr[m];
+        if (KIND == 0 && n == 3) rn[m] = *(const v4f*)&sr[kBM + RG * wm + 16 * m + 4 * g];
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int m = 0; m < MF; ++m) {
         const v4f c = acc[m][n] * rr[m];
-        if (KIND == 0 && n == 3) rr[m] = *(const v4f*)&sr[kBM + RG * wm + 16 * m + 4 * g];
         acc[m][n] = mfma16_fp8_acc(a[m], b, c);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < MF; ++m) rr[m] = rn[m];
       b = bn;
-    }
-    // Instruction order for the scheduler (it would otherwise sink each B read
-    // next to its first use): the A, ratio and first B reads; then per column
-    // tile the next tile's B reads and four (4 ratio multiplies, 1 MFMA) pairs;
-    // gate_up reads the up-half ratios once the gate-half ones are used.
-    __builtin_amdgcn_sched_group_barrier(0x100, 3 * MF + 2, 0);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      if (n + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-      for (int m = 0; m < MF; ++m) {
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        if (KIND == 0 && n == 3) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      }
     }
   };
 
@@ -285,16 +303,18 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   (shalf ? sR0 + kBM : sR0)[srow] = ratio(stage_sa(sA0), sW[shalf][0]);  // 0: the accumulators start at 0
   __syncthreads();
 
-  // One step: loads of block kb + 1 (scales first) into the other stage, the
-  // MFMAs of block kb, then the ratios of block kb + 1 once its loads landed.
+  // One step: the MFMAs of block kb with the loads of block kb + 1 into the other
+  // stage spread among them (waves without rows issue them at once), then the
+  // ratios of block kb + 1 once its loads landed.
   auto step = [&](int kb, const uint8_t* ca, const uint8_t* cb, const float* cr, uint8_t* na,
                   uint8_t* nb, uint8_t* nsa, float* nr) {
     // Every step issues the same loads (past the last block it re-reads block
     // KB - 1 into the stage that is not read again), so the waits stay exact.
     const int kn = min(kb + 1, KB - 1);
-    issue(na, nb, nsa, kn);
-    __builtin_amdgcn_sched_barrier(0);
-    if (active) compute(ca, cb, cr);
+    if (active)
+      compute(ca, cb, cr, na, nb, nsa, kn);
+    else
+      issue(na, nb, nsa, kn);
     __builtin_amdgcn_sched_barrier(0);
     // Past the last block the ratio of the re-read block is 1 and lands in a
     // stage that is not read again.
@@ -477,11 +497,12 @@ __global__ __launch_bounds__(1024) void build_block_tiles_kernel(
       for (int q = b; q < N && b2e[q] == b2e[b]; ++q)
         if (vlen[q] > 0) last = q;
       const long s0 = (long)b * B, s1 = (long)last * B + vlen[last];
+      const long h = (s1 - s0 + v - 1) / v;  // equal heights (sibling tiles share weight blocks in L2)
       for (int c = 0; c < v; ++c) {
         const int idx = off + c;
         if (idx < max_tiles) {
-          tiles[idx] = make_int4(b2e[b], (int)(s0 + (long)c * kBM), (int)min((long)kBM, s1 - s0 - (long)c * kBM),
-                                 (int)(s0 + (long)c * kBM));
+          tiles[idx] = make_int4(b2e[b], (int)(s0 + (long)c * h), (int)min(h, s1 - s0 - (long)c * h),
+                                 (int)(s0 + (long)c * h));
           seg[idx] = make_int2(off, v);
         }
       }
@@ -490,13 +511,14 @@ __global__ __launch_bounds__(1024) void build_block_tiles_kernel(
     __syncthreads();
   }
   const int per = (T + kBM - 1) / kBM;
+  const int hsh = (T + per - 1) / per;
   const long NB = (long)N * B;
   for (int i = tid; i < n_shared * per; i += blockDim.x) {
     const int jj = i / per, m = i - jj * per;
     const int idx = base + i;
     if (idx < max_tiles) {
-      const int s0 = (int)(NB + (long)jj * T + (long)m * kBM);
-      tiles[idx] = make_int4(E + jj, s0, min(kBM, T - m * kBM), s0);
+      const int s0 = (int)(NB + (long)jj * T + (long)m * hsh);
+      tiles[idx] = make_int4(E + jj, s0, min(hsh, T - m * hsh), s0);
       seg[idx] = make_int2(base + jj * per, per);
     }
   }
