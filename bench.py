@@ -14,8 +14,12 @@ Phases:
      two expert GEMMs on the launch stream, for the per-kernel roofline.
   C  the same layer at prefill (8192 tokens), reported under "prefill8k".
   D  the CPU oracle on a bounded token sample (rank 0, N = 1 only).
-With --extra it also times the Kimi-K2 layer over 1..16384 tokens and the
-GLM-4.5 layer with Zipf-skewed routing (reported under "extra").
+  E  (unless --no-extra) the other workloads, under "extra": the small layer
+     (64 tokens, hidden 1024, 8 experts, top-2), Kimi-K2 over 1..16384 tokens
+     (1 token also with 32 inputs cycled so the weights do not stay in the 256 MB
+     MALL), GLM-4.5 with Zipf-skewed routing, and the GPT-OSS-120B layer with
+     MXFP4 experts; and under "cpu_extra" the oracle timed on the small layer in
+     the reference's dense all-experts form and on token samples of each layer.
 Prints one JSON line.
 """
 import argparse
@@ -152,15 +156,92 @@ def run_prologue(calls, torch, ops, dev, H=7168):
         torch.cuda.synchronize()
 
 
-def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev):
-    """Kimi-K2 over its token sweep and GLM-4.5 with Zipf-skewed routing."""
-    out = []
+def rotated_report(name, xs, w, cfg, torch, ops, rounds=3):
+    """Whole-layer timing cycling through the inputs xs (different tokens route to
+    different experts, so the weights of one step are not cache-resident in the next)."""
+    T = xs[0].shape[0]
+    H, I, E = cfg.hidden, cfg.intermediate, cfg.n_experts
+    for x in xs[:4]:
+        ops.layer_forward(x, w, cfg)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(rounds):
+        for x in xs:
+            ops.layer_forward(x, w, cfg)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / (rounds * len(xs))
+    act = []
+    for x in xs:
+        ids = ops.layer_forward(x, w, cfg, return_routing=True)[1]
+        act.append(layer_counts(ids, E))
+    active = sum(a for a, _ in act) / len(act)
+    rows = sum(r for _, r in act) / len(act)
+    nbytes = ((active + cfg.n_shared) * (expert_bytes(H, I, "gate_up") + expert_bytes(H, I, "down"))
+              + E * H * 2 + T * H * 2 * 2)
+    flops = 2 * (rows + T * cfg.n_shared) * 3 * H * I + 2 * T * H * E
+    return {"workload": name, "tokens": T, "inputs_cycled": len(xs),
+            "ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(T / sec, 1),
+            "active_experts": active, "alg_bytes": int(nbytes), "alg_flops": int(flops),
+            "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
+
+
+def mx_report(name, layer, x, steps, torch):
+    """Whole-layer timing of the GPT-OSS MXFP4 layer (module forward, decode form)."""
+    w = layer.w
+    T, H = x.shape
+    E, I, hr = w.n_experts, w.intermediate, layer.hidden_actual or H
+    for _ in range(2):
+        layer(x, None, True, None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        layer(x, None, True, None)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+    from vllm_neuron_amd import ops
+    ids = ops.layer_forward_mx(x, w, layer.top_k, layer.act, layer.limits[:2], layer.limits[2:],
+                               return_routing=True, gamma=layer.norm_weight, eps=layer.rms_norm_eps,
+                               hidden_actual=layer.hidden_actual)[1]
+    active, rows = layer_counts(ids, E)
+    # per expert: fp4 codes (half a byte per weight), one E8M0 byte per 32 weights, fp32 biases
+    per_expert = 3 * H * I // 2 + 3 * H * I // 32 + 4 * (2 * I + H)
+    nbytes = active * per_expert + E * H * 2 + T * H * 2 * 2
+    flops = 2 * rows * 3 * hr * hr + 2 * T * H * E
+    return {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
+            "tokens_per_s": round(T / sec, 1), "active_experts": active,
+            "alg_bytes": nbytes, "alg_flops": flops,
+            "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9),
+                                       flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
+
+
+def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev, cpu_tokens):
+    """The small layer, Kimi-K2 over its token sweep, GLM-4.5 with Zipf-skewed
+    routing and GPT-OSS-120B with MXFP4 experts on the GPU; the oracle on token
+    samples of each (and the small layer in the dense form) on the CPU."""
+    out, cpu = [], []
+    cfg = PRESETS["small"]
+    print("[bench] extra: small T=64", file=sys.stderr, flush=True)
+    w = synthetic.make_weights(cfg, 0, device=dev)
+    x = synthetic.hidden_states(64, cfg.hidden, 0).to(dev)
+    out.append(workload_report("small MoE layer, 64 tokens, hidden 1024, 8 experts, softmax top-2",
+                               x, w, cfg, steps * 4, torch, ops))
+    if cpu_tokens > 0:
+        cpu.append(cpu_dense_small(x, w, cfg))
+        cpu.append(oracle_sample("small MoE layer (64 tokens)", x, w, cfg, 64))
     cfg = PRESETS["kimi_k2"]
     w = synthetic.make_weights(cfg, 3, device=dev, experts_device=dev)
     for T in (1, 16, 256, 2048, 16384):
         print(f"[bench] extra: kimi_k2 T={T}", file=sys.stderr, flush=True)
         x = synthetic.hidden_states(T, cfg.hidden, 3).to(dev)
         out.append(workload_report(f"Kimi-K2 MoE layer, {T} tokens", x, w, cfg, steps, torch, ops))
+        if T == 1:
+            xs = [synthetic.hidden_states(1, cfg.hidden, 100 + i).to(dev) for i in range(32)]
+            out.append(rotated_report("Kimi-K2 MoE layer, 1 token, 32 inputs cycled", xs, w, cfg,
+                                      torch, ops))
+        if T == 16 and cpu_tokens > 0:
+            cpu.append(oracle_sample("Kimi-K2 MoE layer", x, w, cfg, max(1, cpu_tokens // 4)))
     del w
     torch.cuda.empty_cache()
     cfg = PRESETS["glm45"]
@@ -169,29 +250,69 @@ def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev):
     x = synthetic.hidden_states(4096, cfg.hidden, 4).to(dev)
     out.append(workload_report("GLM-4.5 MoE layer, 4096 tokens, Zipf(1.2) routing, 10% empty experts",
                                x, w, cfg, steps, torch, ops))
+    if cpu_tokens > 0:
+        cpu.append(oracle_sample("GLM-4.5 MoE layer (Zipf)", x, w, cfg, max(1, cpu_tokens // 4)))
     del w
     torch.cuda.empty_cache()
-    return out
+    from vllm_neuron_amd import MXFP4MoE
+    print("[bench] extra: gpt-oss-120b mxfp4", file=sys.stderr, flush=True)
+    E, Hp, Ip, Hr = 128, 3072, 3072, 2880
+    wm = synthetic.make_mx_weights(E, Hp, Ip, 5, device=dev, h_real=Hr, i_real=Hr)
+    gamma = (1 + 0.1 * torch.randn(Hp, generator=torch.Generator().manual_seed(5))).to(dev)
+    gamma[Hr:] = 0
+    layer = MXFP4MoE(wm, 4, norm_weight=gamma, eps=1e-5, hidden_actual=Hr)
+    for T in (1, 64, 2048):
+        x = torch.zeros(T, Hp)
+        x[:, :Hr] = torch.randn(T, Hr, generator=torch.Generator().manual_seed(6))
+        x = x.to(torch.bfloat16).to(dev)
+        out.append(mx_report(f"GPT-OSS-120B MoE layer, MXFP4 experts (128, top-4, Swish, clamps, "
+                             f"biases), {T} tokens", layer, x, steps, torch))
+    del wm, layer
+    torch.cuda.empty_cache()
+    return out, cpu
+
+
+def cpu_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:
+        return os.cpu_count()
+
+
+def _route_cpu(cfg, lg, w):
+    import numpy as np
+    from oracle import router as R
+    sc = R.SOFTMAX if cfg.scoring == "softmax" else R.SIGMOID
+    if cfg.grouped:
+        cb = None if w.corr_bias is None else w.corr_bias.float().cpu().numpy()
+        return R.route_grouped(lg, cb, cfg.top_k, cfg.n_group, cfg.topk_group, sc, cfg.renorm,
+                               1e-20, cfg.routed_scaling)
+    return R.route_topk_act(lg, cfg.top_k, sc, cfg.renorm, 1e-20, cfg.routed_scaling)
 
 
 def cpu_baseline(x, w, cfg, n_tokens):
-    """The oracle (numpy, fp32) on the first n_tokens tokens of the workload."""
+    """The oracle (numpy, fp32; sparse per-expert form: router, top-k, each routed
+    expert's weights dequantized and applied to its tokens, weighted combine) on
+    the first n_tokens tokens of the workload. Returns (tokens/s, experts, seconds)."""
     import numpy as np
     import torch
     from oracle import router as R
     from oracle.moe import moe_sparse_fp8
     xs = x[:n_tokens].float().cpu().numpy()
     t0 = time.perf_counter()
-    lg = R.router_logits(xs, w.router_w.float().cpu().numpy(), None)
-    ids, wts = R.route_grouped(lg, w.corr_bias.cpu().numpy(), cfg.top_k, cfg.n_group, cfg.topk_group,
-                               R.SIGMOID, cfg.renorm, 1e-20, cfg.routed_scaling)
+    rb = None if w.router_bias is None else w.router_bias.float().cpu().numpy()
+    lg = R.router_logits(xs, w.router_w.float().cpu().numpy(), rb)
+    ids, wts = _route_cpu(cfg, lg, w)
     experts = sorted(set(np.unique(ids).tolist()))
     q13 = {e: w.w13[e].view(torch.uint8).cpu().numpy() for e in experts}
     s13 = {e: w.w13_scale[e].cpu().numpy() for e in experts}
     q2 = {e: w.w2[e].view(torch.uint8).cpu().numpy() for e in experts}
     s2 = {e: w.w2_scale[e].cpu().numpy() for e in experts}
-    sh = (w.shared_w13[0].view(torch.uint8).cpu().numpy(), w.shared_w13_scale[0].cpu().numpy(),
-          w.shared_w2[0].view(torch.uint8).cpu().numpy(), w.shared_w2_scale[0].cpu().numpy())
+    sh = None
+    if w.n_shared:
+        sh = (w.shared_w13[0].view(torch.uint8).cpu().numpy(), w.shared_w13_scale[0].cpu().numpy(),
+              w.shared_w2[0].view(torch.uint8).cpu().numpy(), w.shared_w2_scale[0].cpu().numpy())
 
     class _D(dict):
         shape = (cfg.n_experts,)
@@ -201,6 +322,51 @@ def cpu_baseline(x, w, cfg, n_tokens):
     return n_tokens / dt, len(experts), dt
 
 
+def oracle_sample(name, x, w, cfg, n_tokens):
+    print(f"[bench] cpu: {name}, {n_tokens} tokens", file=sys.stderr, flush=True)
+    tps, nexp, dt = cpu_baseline(x, w, cfg, n_tokens)
+    return {"workload": name, "form": "sparse per-expert (oracle)", "tokens": n_tokens,
+            "routed_experts": nexp, "seconds": round(dt, 3), "tokens_per_s": round(tps, 3),
+            "cores": cpu_threads()}
+
+
+def cpu_dense_small(x, w, cfg, reps=3):
+    """The small layer in the reference's dense form (_torch_moe_impl, moe_cte.py:465-612:
+    every expert on every token, weighted by the dense affinities), on dequantized
+    weights; median of `reps` timed runs after one warm-up."""
+    import numpy as np
+    import torch
+    from oracle import router as R
+    from oracle.fp8 import dequant_weight_128x128
+    from oracle.moe import moe_dense_reference
+    print("[bench] cpu: small layer, dense form", file=sys.stderr, flush=True)
+    xs = x.float().cpu().numpy()
+    T, E, I = xs.shape[0], cfg.n_experts, cfg.intermediate
+    w13 = np.stack([dequant_weight_128x128(w.w13[e].view(torch.uint8).cpu().numpy(),
+                                           w.w13_scale[e].cpu().numpy()) for e in range(E)])
+    w2 = np.stack([dequant_weight_128x128(w.w2[e].view(torch.uint8).cpu().numpy(),
+                                          w.w2_scale[e].cpu().numpy()) for e in range(E)])
+    gate_up = np.stack([w13[:, :I].transpose(0, 2, 1), w13[:, I:].transpose(0, 2, 1)], axis=2)
+    down = np.ascontiguousarray(w2.transpose(0, 2, 1))
+
+    def run():
+        lg = R.router_logits(xs, w.router_w.float().cpu().numpy(), None)
+        ids, wts = _route_cpu(cfg, lg, w)
+        aff = R.scatter_dense(ids, wts, E).reshape(T * E, 1)
+        return moe_dense_reference(xs, aff, gate_up, down)
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[len(times) // 2]
+    return {"workload": "small MoE layer (64 tokens)", "form": "dense all-experts (_torch_moe_impl)",
+            "tokens": T, "seconds": round(dt, 4), "tokens_per_s": round(T / dt, 1),
+            "cores": cpu_threads()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -208,8 +374,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=4)
-    ap.add_argument("--extra", action="store_true",
-                    help="also time Kimi-K2 (1..16384 tokens) and GLM-4.5 (Zipf) layers")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the other workloads (small, Kimi-K2 sweep, GLM-4.5 Zipf, GPT-OSS "
+                         "MXFP4) and the CPU samples of them")
     ap.add_argument("--prologue-calls", type=int, default=0,
                     help="only run the decode prologue (fused, then as separate launches) this "
                          "many times at 64 and 8192 tokens, for a kernel trace; no timing")
@@ -307,19 +474,18 @@ def main():
     if args.cpu_tokens > 0:
         print("[bench] phase D: CPU oracle sample", file=sys.stderr, flush=True)
         tps, nexp, dt = cpu_baseline(x, w, cfg, args.cpu_tokens)
-        try:
-            from threadpoolctl import threadpool_info
-            cores = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-        except Exception:
-            cores = os.cpu_count()
+        cores = cpu_threads()
         result["cpu_baseline"] = {
             "value": round(tps, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"first {args.cpu_tokens} of the 64 decode tokens ({nexp} routed experts + shared, "
                       f"full layer math incl. per-expert dequant), numpy fp32 BLAS, {dt:.1f} s"}
-    if args.extra:
+    if not args.no_extra:
         del w
         torch.cuda.empty_cache()
-        result["extra"] = extra_workloads(max(3, args.steps // 4), torch, ops, synthetic, PRESETS, dev)
+        result["extra"], cpu_extra = extra_workloads(max(3, args.steps // 4), torch, ops, synthetic,
+                                                     PRESETS, dev, args.cpu_tokens)
+        if cpu_extra:
+            result["cpu_extra"] = cpu_extra
     print(json.dumps(result))
 
 
