@@ -33,6 +33,10 @@ static int choose_mt(int T, int K, int E) {
   return 128;
 }
 
+// The MX row-tile kernels stop at 64-row tiles: at 128 rows the MXFP4 form of the
+// kernel spills registers, and larger tiles only save L2 reads of the weights.
+static int choose_mt_mx(int T, int K, int E) { return std::min(choose_mt(T, K, E), 64); }
+
 struct LayerWs {
   uint16_t* xn;  // normalized rows (bf16), when the layer normalizes
   float* logits;
@@ -80,7 +84,8 @@ static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, in
   const int N = moe_num_blocks(T, K, E, B);
   const long NB = (long)N * B;
   const long P = routed_rows(T, K, E) + (long)n_sh * T;
-  const int mt = choose_mt(T, K, E);
+  // tile list sized for the smaller of the two layers' tile heights (more tiles)
+  const int mt = choose_mt_mx(T, K, E);
   const int max_tiles = moe_max_tiles(T, K, E, N, B, n_sh, mt);
   size_t off = 0;
   auto take = [&](size_t bytes) -> char* {
@@ -358,7 +363,7 @@ extern "C" int moe_layer_forward_mx(
   const long NB = (long)N * B;
   const long R = routed_rows(T, K, E);
   MOE_CHECK_SUPPORTED(NB < (1L << 31), "too many slots");
-  const int mt = choose_mt(T, K, E);
+  const int mt = choose_mt_mx(T, K, E);
   const int max_tiles = moe_max_tiles(T, K, E, N, B, 0, mt);
   float* logits = logits_out ? logits_out : w.logits;
   int32_t* ids = ids_out ? ids_out : w.ids;

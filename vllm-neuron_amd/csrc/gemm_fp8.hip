@@ -81,12 +81,6 @@ __device__ __forceinline__ v8i load_frag_global(const uint8_t* p) {
 // ---------------------------------------------------------------------------
 constexpr int kRowTileMaxKB = 128;  // K <= 16384
 
-// LDS byte address of a pointer into a __shared__ object.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
-  return (uint32_t)(uintptr_t)(lds_cptr)p;
-}
-
 // A step's fragment reads, each group in one asm statement that also waits for
 // its data: the compiler does not see these as reads of memory that
 // direct-to-LDS loads write, so it does not drain the loads in flight into the
@@ -94,7 +88,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // and the registers are complete when the statement ends.
 //   weights: 4 column tiles x (lo, hi) at b_lo / b_hi + 2048 j; activations
 //   (lo, hi) at a_lo / a_hi; the row group's 4 activation scales at sp.
-typedef int v4i __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void lds_read_b_a(uint32_t b_lo, uint32_t b_hi, uint32_t a_lo,
                                              uint32_t a_hi, uint32_t sp, v4i (&b)[8], v4i& al,
                                              v4i& ah, v4i& sa) {

@@ -100,22 +100,109 @@ __device__ __forceinline__ float mx_act(float g, int act) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(k * g));
 }
 
+// ---------------------------------------------------------------------------
+// The MX row-tile kernel. Like the fp8 row-tile kernel, every operand arrives by
+// direct-to-LDS loads into a PD-stage ring whose stages are separate LDS objects,
+// eight lanes per 128-byte weight row segment so each load instruction reads
+// eight whole cache lines. A stage is one 128-byte segment of each weight row:
+// two 128-K blocks of MXFP4 (64 bytes each) or one of MXFP8, with the matching
+// MXFP8 activation rows and the E8M0 scale dwords of both operands. Every wave
+// issues the same number of loads per stage (NV; spare loads go to spare slots),
+// so the wait for the oldest stage is a compile-time vmcnt; the fragment reads
+// are asm statements that wait for their own data (see gemm_fp8.hip).
+// ---------------------------------------------------------------------------
+template <int MT, int WFMT>
+struct MxStage {
+  static constexpr int KPS = (WFMT == kFmtFp4) ? 2 : 1;  // 128-K blocks per stage
+  static constexpr int AQ = MT / 8;                     // activation loads per K block
+  static constexpr int NSQ = (MT + 63) / 64;            // activation scale loads per K block
+  uint8_t b[4][8192];                  // wave w's 64 weight rows x 128 bytes
+  uint32_t bs[4][KPS][64];             // their scale dwords (row 16 j + r of the wave)
+  uint8_t a[KPS * AQ + 1][1024];       // activation rows: slot kk * AQ + q = rows 8q.. of block kk
+  uint32_t as[KPS][NSQ + 1][64];       // activation scale dwords per 64-row group (+ a spare)
+};
+
+// Weight fragments of four 16-row column tiles (j at +2048 j), their four scale
+// dwords (at +64 j), one activation fragment (lo / hi) and its scale dword, read
+// in one statement that waits for its data. fp4 weights: one 16-byte chunk per
+// tile (the MFMA's fp4 operand); fp8 weights: two.
+__device__ __forceinline__ void mx_read_w4(uint32_t b, uint32_t bs, uint32_t a_lo, uint32_t a_hi,
+                                           uint32_t as, v4i (&w)[4], int (&ws)[4], v4i& al,
+                                           v4i& ah, int& sa) {
+  asm volatile(
+      "ds_read_b128 %0, %11\n\t"
+      "ds_read_b128 %1, %11 offset:2048\n\t"
+      "ds_read_b128 %2, %11 offset:4096\n\t"
+      "ds_read_b128 %3, %11 offset:6144\n\t"
+      "ds_read_b32 %4, %12\n\t"
+      "ds_read_b32 %5, %12 offset:64\n\t"
+      "ds_read_b32 %6, %12 offset:128\n\t"
+      "ds_read_b32 %7, %12 offset:192\n\t"
+      "ds_read_b128 %8, %13\n\t"
+      "ds_read_b128 %9, %14\n\t"
+      "ds_read_b32 %10, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(ws[0]), "=&v"(ws[1]),
+        "=&v"(ws[2]), "=&v"(ws[3]), "=&v"(al), "=&v"(ah), "=&v"(sa)
+      : "v"(b), "v"(bs), "v"(a_lo), "v"(a_hi), "v"(as)
+      : "memory");
+}
+__device__ __forceinline__ void mx_read_w8(uint32_t b_lo, uint32_t b_hi, uint32_t bs, uint32_t a_lo,
+                                           uint32_t a_hi, uint32_t as, v4i (&w)[8], int (&ws)[4],
+                                           v4i& al, v4i& ah, int& sa) {
+  asm volatile(
+      "ds_read_b128 %0, %15\n\t"
+      "ds_read_b128 %1, %16\n\t"
+      "ds_read_b128 %2, %15 offset:2048\n\t"
+      "ds_read_b128 %3, %16 offset:2048\n\t"
+      "ds_read_b128 %4, %15 offset:4096\n\t"
+      "ds_read_b128 %5, %16 offset:4096\n\t"
+      "ds_read_b128 %6, %15 offset:6144\n\t"
+      "ds_read_b128 %7, %16 offset:6144\n\t"
+      "ds_read_b32 %8, %17\n\t"
+      "ds_read_b32 %9, %17 offset:64\n\t"
+      "ds_read_b32 %10, %17 offset:128\n\t"
+      "ds_read_b32 %11, %17 offset:192\n\t"
+      "ds_read_b128 %12, %18\n\t"
+      "ds_read_b128 %13, %19\n\t"
+      "ds_read_b32 %14, %20\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
+        "=&v"(w[6]), "=&v"(w[7]), "=&v"(ws[0]), "=&v"(ws[1]), "=&v"(ws[2]), "=&v"(ws[3]),
+        "=&v"(al), "=&v"(ah), "=&v"(sa)
+      : "v"(b_lo), "v"(b_hi), "v"(bs), "v"(a_lo), "v"(a_hi), "v"(as)
+      : "memory");
+}
+__device__ __forceinline__ void mx_read_a(uint32_t a_lo, uint32_t a_hi, uint32_t as, v4i& al,
+                                          v4i& ah, int& sa) {
+  asm volatile(
+      "ds_read_b128 %0, %3\n\t"
+      "ds_read_b128 %1, %4\n\t"
+      "ds_read_b32 %2, %5\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(al), "=&v"(ah), "=&v"(sa)
+      : "v"(a_lo), "v"(a_hi), "v"(as)
+      : "memory");
+}
+
 template <int MT, int KIND, int PD, int WFMT>
 __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
+  using Stage = MxStage<MT, WFMT>;
   constexpr int MS = MT / 16;
-  constexpr int ACH = MT * 8;             // 16-byte chunks per A tile per K block
-  constexpr int APT = (ACH + 255) / 256;  // chunks per thread
-  constexpr int LDA = 128 + 16;           // padded LDS row (bytes)
-  constexpr int WKB = (WFMT == kFmtFp4) ? 64 : 128;  // weight bytes per row per K block
-  __shared__ __attribute__((aligned(16))) uint8_t sA[2][MT * LDA];
-  __shared__ __attribute__((aligned(16))) uint32_t sAs[2][MT];  // 4 scale bytes per row
+  constexpr int KPS = Stage::KPS, AQ = Stage::AQ, NSQ = Stage::NSQ;
+  constexpr int NA = (KPS * AQ + 3) / 4;       // activation loads per wave per stage
+  constexpr int NV = 8 + KPS + NA + KPS;       // direct-to-LDS loads per wave per stage
+  static_assert(PD >= 2 && PD <= 3 && (PD - 2) * NV < 64, "pipeline depth");
+  __shared__ __attribute__((aligned(1024))) Stage st0;
+  __shared__ __attribute__((aligned(1024))) Stage st1;
+  __shared__ __attribute__((aligned(1024))) Stage st2;
   __shared__ long sSrc[MT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
   const int Kdim = (KIND == 0) ? p.H : p.I;
-  const int KB = Kdim / 128;
-  const int KS = Kdim / 32;  // scale bytes per row
+  const int KS = Kdim / 32;               // scale bytes per row
+  const int NSTG = Kdim / (128 * KPS);    // stages (K % (128 KPS) == 0, checked by the entry points)
   const int NT = (KIND == 0) ? p.I / 128 : p.H / 256;
   const int total = p.num_tiles[0] * NT;
   const std::integral_constant<int, WFMT> wfmt{};
@@ -144,71 +231,65 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
     }
     __syncthreads();
 
-    // Activation chunks: every load is issued unconditionally (rows without a
-    // source read row 0 and are zeroed), so the loads in flight stay countable.
-    const uint8_t* aptr[APT];
-    int aoff[APT];
-    bool alive[APT];
-#pragma unroll
-    for (int c = 0; c < APT; ++c) {
-      const int chunk = tid + 256 * c;
-      aptr[c] = p.a;
-      aoff[c] = -1;
-      alive[c] = false;
-      if (chunk < ACH) {
-        const int row = chunk >> 3, col = (chunk & 7) * 16;
-        aoff[c] = row * LDA + col;
-        const long src = sSrc[row];
-        if (src >= 0) {
-          aptr[c] = p.a + (size_t)src * Kdim + col;
-          alive[c] = true;
-        }
-      }
-    }
-    const bool as_alive = tid < MT && sSrc[tid] >= 0;
-    const uint8_t* asp = as_alive ? p.as + (size_t)sSrc[tid] * KS : p.as;
-
-    const size_t wrow_bytes = (size_t)Kdim * WKB / 128;
+    const size_t wrow_bytes = (size_t)Kdim * ((WFMT == kFmtFp4) ? 64 : 128) / 128;
     const int rows_w = (KIND == 0) ? 2 * p.I : p.H;
     const uint8_t* wb = (is_sh ? p.wsh : p.w) + (size_t)ej * rows_w * wrow_bytes;
     const uint8_t* wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * rows_w * KS;
     const float* bb = is_sh ? p.bsh : p.bias;
     if (bb != nullptr) bb += (size_t)ej * rows_w;
-    int wrow[4];
-    const uint8_t* bp[4];
-    const uint32_t* sp[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    // weight row of column tile j, row r of the tile, for this wave
+    auto wrow_of = [&](int j, int r) -> int {
       if (KIND == 0)
-        wrow[j] = (j < 2) ? nt * 128 + wave * 32 + j * 16 + r16
-                          : p.I + nt * 128 + wave * 32 + (j - 2) * 16 + r16;
-      else
-        wrow[j] = nt * 256 + wave * 64 + j * 16 + r16;
-      bp[j] = wb + (size_t)wrow[j] * wrow_bytes + g * 16;
-      sp[j] = (const uint32_t*)(wsb + (size_t)wrow[j] * KS);  // KS % 4 == 0: dword aligned
-    }
-
-    v8i bq[PD][4];
-    uint32_t bsq[PD][4];
-    int4 aq[PD][APT];
-    uint32_t asq[PD];
-
-    auto load_stage = [&](int s, int kb) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        bq[s][j] = load_frag<WFMT>(bp[j] + (size_t)kb * WKB);
-        bsq[s][j] = sp[j][kb];  // the 4 scale bytes of the K block; lane uses byte g
-      }
-#pragma unroll
-      for (int c = 0; c < APT; ++c)
-        aq[s][c] = *(const int4*)(aptr[c] + (alive[c] ? (size_t)kb * 128 : 0));
-      asq[s] = *(const uint32_t*)(asp + (as_alive ? (size_t)kb * 4 : 0));
+        return (j < 2) ? nt * 128 + wave * 32 + j * 16 + r : p.I + nt * 128 + wave * 32 + (j - 2) * 16 + r;
+      return nt * 256 + wave * 64 + j * 16 + r;
     };
-    auto store_A = [&](int buf, int s) {
+    // Load sources. Weight load i: rows 8 (i & 1) + l / 8 of column tile i / 2, stored
+    // chunk l % 8 = logical chunk swz(row, l % 8) of the row's 128-byte segment.
+    uint32_t boff[8];
 #pragma unroll
-      for (int c = 0; c < APT; ++c)
-        if (aoff[c] >= 0) *(int4*)&sA[buf][aoff[c]] = alive[c] ? aq[s][c] : make_int4(0, 0, 0, 0);
-      if (tid < MT) sAs[buf][tid] = as_alive ? asq[s] : 0x7f7f7f7fu;  // scale 1 for zero rows
+    for (int i = 0; i < 8; ++i) {
+      const int rr = (i & 1) * 8 + (lane >> 3);
+      boff[i] = (uint32_t)wrow_of(i >> 1, rr) * (uint32_t)wrow_bytes + (uint32_t)swz(rr, lane & 7) * 16;
+    }
+    // weight scale dword of row (j = l / 16, r = l % 16): byte offset of the row
+    const uint32_t bsoff = (uint32_t)wrow_of(lane >> 4, lane & 15) * (uint32_t)KS;
+    // activation load a of the wave: slot s = wave NA + a (s >= KPS AQ: a spare load
+    // of row 0 into slot KPS AQ); rows without a source read row 0 (never stored)
+    const uint8_t* aptr[NA];
+    int aslot[NA], akk[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      const int sl = wave * NA + a;
+      const int q = (sl < KPS * AQ) ? sl % AQ : 0;
+      const int r = q * 8 + (lane >> 3);
+      long src = 0;
+      if (sl < KPS * AQ && sSrc[r] >= 0) src = sSrc[r];
+      aslot[a] = (sl < KPS * AQ) ? sl : KPS * AQ;
+      akk[a] = (sl < KPS * AQ) ? sl / AQ : 0;
+      aptr[a] = p.a + (size_t)src * Kdim + swz(r, lane & 7) * 16;
+    }
+    long ssrc = 0;
+    {
+      const int r = wave * 64 + lane;
+      if (wave < NSQ && r < MT && sSrc[r] >= 0) ssrc = sSrc[r];
+    }
+    const uint8_t* asp = p.as + (size_t)ssrc * KS;
+    const int sslot = wave < NSQ ? wave : NSQ;
+
+    // Loads of stage t (K blocks [KPS t, KPS t + KPS)).
+    auto issue = [&](Stage& S, int t) {
+      const size_t kb0 = (size_t)t * KPS;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) load_lds16(wb + boff[i] + (size_t)t * 128, &S.b[wave][i * 1024]);
+#pragma unroll
+      for (int kk = 0; kk < KPS; ++kk)
+        load_lds4(wsb + bsoff + (kb0 + kk) * 4, (uint8_t*)&S.bs[wave][kk][0]);
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+        load_lds16(aptr[a] + (kb0 + akk[a]) * 128, &S.a[aslot[a]][0]);
+#pragma unroll
+      for (int kk = 0; kk < KPS; ++kk)
+        load_lds4(asp + (kb0 + kk) * 4, (uint8_t*)&S.as[kk][sslot][0]);
     };
 
     v4f acc[MS][4];
@@ -217,34 +298,77 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[ms][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-    for (int s = 0; s < PD - 1; ++s) load_stage(s, min(s, KB - 1));
-    store_A(0, 0);
-    __syncthreads();
-
-    auto kstep = [&](int kb, int s) {
-      load_stage((s + PD - 1) % PD, min(kb + PD - 1, KB - 1));
-      const int buf = kb & 1;
-#pragma unroll
-      for (int ms = 0; ms < MS; ++ms) {
-        const v8i a = load_frag<kFmtFp8>(&sA[buf][(ms * 16 + r16) * LDA + g * 16]);
-        const int sa = (int)(sAs[buf][ms * 16 + r16] >> (8 * g));
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[ms][j] = mfma_mx(a, bq[s][j], acc[ms][j], sa, (int)(bsq[s][j] >> (8 * g)), wfmt);
-      }
-      if (kb + 1 < KB) store_A((kb + 1) & 1, (s + 1) % PD);
-      lds_barrier();  // orders the activation double buffer; weight prefetches stay in flight
+    const int fr = (r16 >> 3) * 1024 + (r16 & 7) * 128;
+    auto cat = [](const v4i& lo, const v4i& hi) -> v8i {
+      return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     };
-    int kb0 = 0;
-    for (; kb0 + PD <= KB; kb0 += PD) {
+    auto step = [&](int t, Stage& cur, Stage& nxt) {
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm<(PD - 2) * NV>();      // this wave's share of stage t has landed
+      __builtin_amdgcn_s_barrier();  // ... every wave's, and stage t - 1 is consumed
+      __builtin_amdgcn_sched_barrier(0);
+      issue(nxt, min(t + PD - 1, NSTG - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t bw = lds_addr(&cur.b[wave][0]);
 #pragma unroll
-      for (int s = 0; s < PD; ++s) kstep(kb0 + s, s);
+      for (int kk = 0; kk < KPS; ++kk) {
+        const uint32_t aw = lds_addr(&cur.a[kk * AQ][0]);
+        const uint32_t bsw = lds_addr(&cur.bs[wave][kk][r16]);
+        v8i b[4];
+        int bsc[4];
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+          v4i alo, ahi;
+          int sa;
+          const uint32_t a_lo = aw + 2048 * ms + fr + swz(r16, g) * 16;
+          const uint32_t a_hi = aw + 2048 * ms + fr + swz(r16, 4 + g) * 16;
+          const uint32_t asw = lds_addr(&cur.as[kk][(ms * 16) >> 6][(ms * 16 + r16) & 63]);
+          if (ms == 0) {
+            if (WFMT == kFmtFp4) {
+              v4i w[4];
+              mx_read_w4(bw + fr + swz(r16, kk * 4 + g) * 16, bsw, a_lo, a_hi, asw, w, bsc, alo,
+                         ahi, sa);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) b[j] = (v8i){w[j].x, w[j].y, w[j].z, w[j].w, 0, 0, 0, 0};
+            } else {
+              v4i w[8];
+              mx_read_w8(bw + fr + swz(r16, g) * 16, bw + fr + swz(r16, 4 + g) * 16, bsw, a_lo, a_hi,
+                         asw, w, bsc, alo, ahi, sa);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) b[j] = cat(w[2 * j], w[2 * j + 1]);
+            }
+          } else {
+            mx_read_a(a_lo, a_hi, asw, alo, ahi, sa);
+          }
+          const v8i a = cat(alo, ahi);
+          const int sab = (int)((uint32_t)sa >> (8 * g));
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[ms][j] = mfma_mx(a, b[j], acc[ms][j], sab, (int)((uint32_t)bsc[j] >> (8 * g)), wfmt);
+          // keeps each row group's MFMAs next to its reads (the scheduler would
+          // otherwise hold every group's fragments live at once)
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    wait_vm<0>();  // no earlier load is still landing in a stage buffer
+    issue(st0, 0);
+    if (PD >= 3) issue(st1, min(1, NSTG - 1));
+    for (int t = 0; t < NSTG; t += PD) {
+      if (PD == 2) {
+        step(t, st0, st1);
+        if (t + 1 < NSTG) step(t + 1, st1, st0);
+      } else {
+        step(t, st0, st2);
+        if (t + 1 < NSTG) step(t + 1, st1, st0);
+        if (t + 2 < NSTG) step(t + 2, st2, st1);
+      }
     }
-#pragma unroll
-    for (int s = 0; s < PD - 1; ++s)
-      if (kb0 + s < KB) kstep(kb0 + s, s);
+    wait_vm<0>();  // the tail's repeated loads land before the stages are reused
 
+    int wrow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wrow[j] = wrow_of(j, r16);
     // Accumulator layout: lane l, register i holds D[4 * (l / 16) + i][l % 16]
     // (row of the tile, weight row of the fragment).
     if (KIND == 0) {

@@ -6,6 +6,7 @@
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 #define MOE_WAVE 64
@@ -129,6 +130,12 @@ __device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds_wave_base
 
 __device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 4, 0, 0);
+}
+
+// LDS byte address of a pointer into a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  typedef __attribute__((address_space(3))) const uint8_t* lds_cptr;
+  return (uint32_t)(uintptr_t)(lds_cptr)p;
 }
 
 // Logical 16-byte chunk c of row r lives at chunk c ^ ((r >> 1) & 7): any 16

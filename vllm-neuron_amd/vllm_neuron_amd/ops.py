@@ -525,7 +525,7 @@ def mx_experts(x, ids, wts, w, act="swish", gate_limits=(None, None), up_limits=
     NB = tpid.numel()
     if xq is None:
         xq, xs = act_quant_mx(x)
-    mt = choose_mt(T, K, E)
+    mt = min(choose_mt(T, K, E), 64)  # the MX kernels stop at 64-row tiles (as the layer)
     tiles, num, max_tiles = build_tiles(tpid, b2e, block_size, T, K, E, 0, mt)
     hq, hs = expert_gate_up_mx(xq, xs, w, tpid, NB, tiles, num, max_tiles, mt, NB, act,
                                gate_limits, up_limits)
