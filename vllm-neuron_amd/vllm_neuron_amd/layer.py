@@ -105,13 +105,22 @@ class FP8BlockMoE(torch.nn.Module):
         if res is not None and self.norm_weight is None:
             raise ValueError("residual is added inside the layer's norm: give norm_weight")
         w, cfg = self.w, self.cfg
-        out, rsum = moe_layer(
-            x2.contiguous(), None if res is None else res.contiguous(), self.norm_weight,
-            self.rms_norm_eps, 0 if self.hidden_actual is None else self.hidden_actual,
-            w.router_w, w.router_bias, w.corr_bias, w.w13, w.w13_scale, w.w2, w.w2_scale,
-            w.shared_w13, w.shared_w13_scale, w.shared_w2, w.shared_w2_scale, cfg.top_k,
-            cfg.grouped, cfg.scoring, cfg.n_group, cfg.topk_group, cfg.renorm,
-            float(cfg.routed_scaling), cfg.block_size)
+        xc, rc = x2.contiguous(), None if res is None else res.contiguous()
+        if torch.compiler.is_compiling():
+            # one opaque node of the compiled graph
+            out, rsum = moe_layer(
+                xc, rc, self.norm_weight, self.rms_norm_eps,
+                0 if self.hidden_actual is None else self.hidden_actual,
+                w.router_w, w.router_bias, w.corr_bias, w.w13, w.w13_scale, w.w2, w.w2_scale,
+                w.shared_w13, w.shared_w13_scale, w.shared_w2, w.shared_w2_scale, cfg.top_k,
+                cfg.grouped, cfg.scoring, cfg.n_group, cfg.topk_group, cfg.renorm,
+                float(cfg.routed_scaling), cfg.block_size)
+        else:
+            # eager: the operator's body without the dispatcher (about 20 us of host
+            # time per call, which a one-token decode step would otherwise wait on)
+            r = ops.layer_forward(xc, w, cfg, gamma=self.norm_weight, eps=self.rms_norm_eps,
+                                  hidden_actual=self.hidden_actual, residual=rc)
+            out, rsum = (r, None) if rc is None else r
         if res is None:
             rsum = None
         if positions is not None and not is_decode:

@@ -97,11 +97,23 @@ class MXFP4MoE(torch.nn.Module):
             raise ValueError("residual is added inside the layer's norm: give norm_weight")
         w = self.w
         gl, gh, ul, uh = self.limits
-        out, rsum = moe_layer_mx(
-            x2.contiguous(), None if res is None else res.contiguous(), self.norm_weight,
-            self.rms_norm_eps, 0 if self.hidden_actual is None else self.hidden_actual,
-            w.router_w, w.router_bias, w.w13, w.w13_scale, w.b13, w.w2, w.w2_scale, w.b2, w.fmt,
-            self.top_k, self.act, gl, gh, ul, uh, self.scoring, self.block_size)
+        xc, rc = x2.contiguous(), None if res is None else res.contiguous()
+        if torch.compiler.is_compiling():
+            # one opaque node of the compiled graph
+            out, rsum = moe_layer_mx(
+                xc, rc, self.norm_weight, self.rms_norm_eps,
+                0 if self.hidden_actual is None else self.hidden_actual,
+                w.router_w, w.router_bias, w.w13, w.w13_scale, w.b13, w.w2, w.w2_scale, w.b2,
+                w.fmt, self.top_k, self.act, gl, gh, ul, uh, self.scoring, self.block_size)
+        else:
+            # eager: the operator's body without the dispatcher
+            nan_none = lambda v: None if v != v else v
+            r = ops.layer_forward_mx(xc, w, self.top_k, self.act, (nan_none(gl), nan_none(gh)),
+                                     (nan_none(ul), nan_none(uh)), scoring=self.scoring,
+                                     gamma=self.norm_weight, eps=self.rms_norm_eps,
+                                     hidden_actual=self.hidden_actual, residual=rc,
+                                     block_size=self.block_size)
+            out, rsum = (r, None) if rc is None else r
         if positions is not None and not is_decode:
             # model_bf16.py:1380-1384: tokens after the last real position are padding
             pos = positions.reshape(-1)
