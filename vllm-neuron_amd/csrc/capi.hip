@@ -23,13 +23,14 @@ void set_error(const char* fn, const char* fmt, ...) {
 
 void clear_error() { g_err[0] = 0; }
 
-// Rows per expert tile: 16 up to 8 routed rows per expert on average (measured
-// ahead of 32-row tiles there), else the next supported MFMA tile height.
+// Rows per expert tile (see use_block for the measurements): 16-row tiles up to 4
+// routed rows per expert on average, 32 up to 24, 64 up to 48 (the MX layer, which
+// has no block kernels, past 32), else 128.
 static int choose_mt(int T, int K, int E) {
   long avg = ((long)T * std::min(K, E) + E - 1) / E;
-  if (avg <= 8) return 16;
-  if (avg <= 32) return 32;
-  if (avg <= 64) return 64;
+  if (avg <= 4) return 16;
+  if (avg <= 24) return 32;
+  if (avg <= 48) return 64;
   return 128;
 }
 
@@ -63,13 +64,15 @@ struct LayerWs {
   size_t bytes;
 };
 
-// The 256x256 ("block") kernels take over above 20 rows per expert on average.
-// Expert GEMM time on the DeepSeek-V3 and Kimi-K2 layers: 16-row tiles are best
-// up to 8 rows, 32-row tiles from 10 to 16 rows (3-6 % ahead of the block
-// kernels), the two are level at 20 rows and the block kernels lead from 24 rows
-// on (5-25 % at 24-32 rows).
+// The 256x256 ("block") kernels take over above 32 rows per expert on average.
+// Expert GEMM time (gate_up + down) on the DeepSeek-V3 layer by rows per expert,
+// ms, row tiles of 16 / 32 / 64 rows against the block kernels: 4 rows 1.81 /
+// 1.81 / 1.93 vs 2.05; 8: 1.95 / 1.92 / 2.08 vs 2.15; 16: 2.30 / 2.03 / 2.13 vs
+// 2.29; 24: 2.78 / 2.11 / 2.19 vs 2.37; 32: 3.32 / 2.36 / 2.28 vs 2.42; 48: - /
+// 2.95 / 2.47 vs 2.51; 64: - / 3.58 / 3.01 vs 2.60. On the Kimi-K2 layer at 42.7
+// rows the block kernels lead (whole layer 3.90 against 3.95-4.00 ms), hence 32.
 static bool use_block(int T, int K, int E) {
-  return ((long)T * std::min(K, E) + E - 1) / E > 20;
+  return ((long)T * std::min(K, E) + E - 1) / E > 32;
 }
 
 static inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }

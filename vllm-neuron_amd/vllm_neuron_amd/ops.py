@@ -45,14 +45,14 @@ def num_blocks(T, K, E, B):
 
 
 def use_block_kernels(T, K, E):
-    """The layer switches to the 256x256 block kernels above 20 rows per expert on
+    """The layer switches to the 256x256 block kernels above 32 rows per expert on
     average (the measured crossover against every row-tile height)."""
-    return -(-T * min(K, E) // E) > 20
+    return -(-T * min(K, E) // E) > 32
 
 
 def choose_mt(T, K, E):
     avg = -(-T * min(K, E) // E)
-    for limit, mt in ((8, 16), (32, 32), (64, 64)):
+    for limit, mt in ((4, 16), (24, 32), (48, 64)):
         if avg <= limit:
             return mt
     return 128
