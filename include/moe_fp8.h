@@ -189,7 +189,7 @@ int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int
  * moe_block_tiles_workspace_bytes(N, max_tiles). Same outputs as
  * moe_expert_gate_up / moe_expert_down (same replaced reference interface,
  * moe_cte.py:356-421 and :557-588); the layer uses them when the average
- * expert receives more than 20 rows. */
+ * expert receives more than 32 rows. */
 int moe_max_block_tiles(int T, int K, int E, int N, int B, int n_shared);
 size_t moe_block_tiles_workspace_bytes(int N, int max_tiles);
 int moe_build_block_tiles(const int32_t* token_position_to_id, const int32_t* block_to_expert,
