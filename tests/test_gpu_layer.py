@@ -318,7 +318,7 @@ def test_layer_glm45_full_size_zipf(cuda):
 
 @pytest.mark.parametrize("T,E,K,S", [(2048, 8, 2, 0), (3000, 16, 4, 1), (700, 4, 2, 1)])
 def test_layer_block_kernels(cuda, T, E, K, S):
-    """Block-kernel path (> 20 rows per expert): block kernels against the oracle,
+    """Block-kernel path (> 32 rows per expert): block kernels against the oracle,
     including partial 256-row tiles, and agreement with the row-tile kernels."""
     cfg = MoEConfig(1024, 512, E, K, n_shared=S, scoring="sigmoid", grouped=True, n_group=1,
                     topk_group=1, renorm=True, routed_scaling=1.0)

@@ -8,17 +8,20 @@
 //    up to 256 consecutive slots of one expert, the columns 256 weight rows
 //    (gate_up: 128 gate rows + the matching 128 up rows; down: 256 outputs).
 //    Per 128-K step the tile moves 64 KB through L1 for 16.8 MFLOP;
-//  * both operands are staged through LDS in two stages of 128 K (one K block of
-//    look-ahead), loaded with global_load_lds_dwordx4 (no register staging);
-//    16-byte chunks are XOR-swizzled by row pairs so 16-lane fragment reads hit
-//    distinct banks of the 64-bank LDS;
+//  * both operands are staged through LDS, loaded with global_load_lds_dwordx4
+//    (no register staging): the weight (B) tiles in a ring of three 128-K stages
+//    (two blocks in flight, for the HBM stream), the token (A) tile in one stage
+//    refilled as soon as every wave holds its fragments (two barriers per K
+//    step). 16-byte chunks are XOR-swizzled by row pairs so 16-lane fragment
+//    reads hit distinct banks of the 64-bank LDS;
 //  * wave (wm, wn) owns rows [64 wm, +64) and 128 columns as 4 x 8 tiles of
 //    v_mfma_f32_16x16x128_f8f6f4: one MFMA per tile covers a whole 128-K scale
 //    block. The block scales s_k = s_a[row, k] * s_w[k] are folded into the
 //    running accumulator: acc = acc * (s_{k-1} / s_k) + A_k B_k, and the result
 //    is acc * s_last, which equals sum_k s_k A_k B_k (one fp32 multiply per
 //    accumulator element per K block, no separate partial products). The
-//    ratios are computed once per (row, column half) per K block into LDS;
+//    ratios are computed once per (row, column half) per K block into LDS, one
+//    block ahead, from activation scales loaded two blocks ahead;
 //  * for gate_up wave column half wn holds gate and up columns [64 wn, +64) of
 //    the tile's 128 h columns, so SiLU(g) * u is wave-local and only the row
 //    amax of the 1x128 quantization group is combined across the two halves;
@@ -30,8 +33,8 @@
 //    through K at the same pace and read each weight block once from HBM (a
 //    256-row tile next to a short remainder tile left it behind: 12.3 GB read
 //    for 7.6 GB of weights at 8192 tokens, 9.6 GB with equal tiles);
-//  * the next block's loads are spread among the MFMAs of the current one,
-//    weights first (6 % faster gate_up than issuing them at once).
+//  * the next token tile is loaded once the current one has been read, and the
+//    weight tile two blocks ahead is spread among the current block's MFMAs.
 //
 // Fragment lane layout (16x16x128): lane l supplies row l%16 and the bytes
 // [(l/16)*16, +16) and [64 + (l/16)*16, +16) of the 128-wide K block, the same
@@ -77,14 +80,87 @@ __device__ __forceinline__ v4f mfma16_fp8_acc(const v8i& a, const v8i& b, const 
 // distinct objects, so the compiler can tell that fragment reads of one stage do
 // not alias the direct-to-LDS loads in flight into another.
 struct BlkLds {
-  uint8_t *ta0, *tb0, *ta1, *tb1;  // A and B tiles of stages 0 and 1
-  uint8_t *sa0, *sa1;              // A scales of each stage's block
-  float *r0, *r1;                  // scale ratio per (half, row) of each stage
+  uint8_t* ta;                     // A tile of the current block (one stage)
+  uint8_t *tb0, *tb1, *tb2;        // B tiles: three-stage ring
+  uint8_t* sa;                     // A scales (loaded two blocks ahead), one copy per column half
+  float *r0, *r1;                  // scale ratios per (half, row) of even / odd blocks
   float* last;                     // last block scale per (half, row)
   int* src;                        // token (gate_up) or slot (down) of each tile row
   float (*red)[kBM];               // row amax of the two column halves
   float (*w)[kMaxKB];              // weight block scales of the two column halves
 };
+
+// LDS reads in asm. The compiler cannot tell a direct-to-LDS load into another
+// stage from one into the stage read here once the K loop merges its paths, and
+// would wait for every load in flight before a plain read. Reads that finish
+// inside their statement wait for themselves; lds_frag_issue leaves its reads in
+// flight until lds_frag_wait, which takes the same registers (LDS reads complete
+// in order, so waiting for all of them is exact).
+template <int OFF>
+__device__ __forceinline__ void lds_frag_issue(uint32_t lo_addr, uint32_t hi_addr, v4i& lo, v4i& hi) {
+  asm volatile(
+      "ds_read_b128 %0, %2 offset:%4\n\t"
+      "ds_read_b128 %1, %3 offset:%4"
+      : "=&v"(lo), "=&v"(hi)
+      : "v"(lo_addr), "v"(hi_addr), "n"(OFF)
+      : "memory");
+}
+__device__ __forceinline__ void lds_frag_wait(v4i& lo, v4i& hi) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(lo), "+v"(hi) : : "memory");
+}
+template <int OFF>
+__device__ __forceinline__ void lds_v4_issue(uint32_t addr, v4i& v) {
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(v) : "v"(addr), "n"(OFF) : "memory");
+}
+__device__ __forceinline__ void lds_v4_wait(v4i& v) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v) : : "memory");
+}
+// MF A fragments at rows 0, 16, 32, 48 of the wave's row group: all reads, one wait.
+template <int MF>
+__device__ __forceinline__ void lds_frags_a(uint32_t lo_addr, uint32_t hi_addr, v4i (&lo)[MF],
+                                            v4i (&hi)[MF]) {
+  if constexpr (MF == 1) {
+    asm volatile(
+        "ds_read_b128 %0, %2\n\tds_read_b128 %1, %3\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(lo[0]), "=&v"(hi[0]) : "v"(lo_addr), "v"(hi_addr) : "memory");
+  } else if constexpr (MF == 2) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %5\n\t"
+        "ds_read_b128 %2, %4 offset:2048\n\tds_read_b128 %3, %5 offset:2048\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]) : "v"(lo_addr), "v"(hi_addr)
+        : "memory");
+  } else if constexpr (MF == 3) {
+    asm volatile(
+        "ds_read_b128 %0, %6\n\tds_read_b128 %1, %7\n\t"
+        "ds_read_b128 %2, %6 offset:2048\n\tds_read_b128 %3, %7 offset:2048\n\t"
+        "ds_read_b128 %4, %6 offset:4096\n\tds_read_b128 %5, %7 offset:4096\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(lo[2]), "=&v"(hi[2])
+        : "v"(lo_addr), "v"(hi_addr)
+        : "memory");
+  } else {
+    static_assert(MF == 4, "1 to 4 fragments");
+    asm volatile(
+        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %9\n\t"
+        "ds_read_b128 %2, %8 offset:2048\n\tds_read_b128 %3, %9 offset:2048\n\t"
+        "ds_read_b128 %4, %8 offset:4096\n\tds_read_b128 %5, %9 offset:4096\n\t"
+        "ds_read_b128 %6, %8 offset:6144\n\tds_read_b128 %7, %9 offset:6144\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(lo[2]), "=&v"(hi[2]),
+          "=&v"(lo[3]), "=&v"(hi[3])
+        : "v"(lo_addr), "v"(hi_addr)
+        : "memory");
+  }
+}
+__device__ __forceinline__ float lds_f32(uint32_t addr) {
+  float v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ v8i cat8(const v4i& lo, const v4i& hi) {
+  return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+}
 
 // One work item: tile rows [slot0, slot0 + nrows) of expert e against column
 // tile nt; they use hq / y rows [rbase, rbase + nrows). MF is the number of 16-row fragments per wave: the four row groups
@@ -94,12 +170,11 @@ template <int KIND, int MF>
 __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, const int e,
                                            const long slot0, const long rbase, const int nrows,
                                            const int nt) {
-  uint8_t* const sTA0 = s.ta0;
+  uint8_t* const sTA = s.ta;
   uint8_t* const sTB0 = s.tb0;
-  uint8_t* const sTA1 = s.ta1;
   uint8_t* const sTB1 = s.tb1;
-  uint8_t* const sA0 = s.sa0;
-  uint8_t* const sA1 = s.sa1;
+  uint8_t* const sTB2 = s.tb2;
+  uint8_t* const sSA = s.sa;
   float* const sR0 = s.r0;
   float* const sR1 = s.r1;
   float* const sLast = s.last;
@@ -172,10 +247,10 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // Scale writers: every thread owns one (row, column half) and keeps the
   // previous block's scale; invalid rows use scale 1 (never stored). A zero
   // block scale (an all-zero weight block) repeats the previous scale: that
-  // block's products are zero. The activation scales of a stage's block reach
-  // LDS with its loads (one 4-byte direct-to-LDS load per wave: wave (wm, wn)
-  // fills rows 64 wm + lane of the copy for column half wn);
-  // the weight scales are staged once per tile.
+  // block's products are zero. The activation scales of a block reach LDS with
+  // the B tile of the same block, two blocks ahead of its MFMAs (one 4-byte
+  // direct-to-LDS load per wave: wave (wm, wn) fills rows 64 wm + lane of the copy
+  // for column half wn); the weight scales are staged once per tile.
   // Thread (wave (wm, wn), lane j) owns row 64 wm + j and half wn: the rows its
   // own wave's scale load fills, so its own vmcnt wait covers them.
   const int srow = 64 * wm + lane, shalf = wn;
@@ -183,6 +258,7 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // Byte offsets of operand rows fit 32 bits: the entry points reject larger operands.
   const uint32_t off_sa = (uint32_t)(sSrc[64 * wm + lane] >= 0 ? sSrc[64 * wm + lane] : 0) * (uint32_t)(KB * 4);
   const int sa_dst = (wn * kBM + 64 * wm) * 4;
+  const uint32_t sa_own = lds_addr(sSA) + (uint32_t)((shalf * kBM + srow) * 4);
   for (int i = tid; i < 2 * KB; i += kBlkThreads) {
     const int hf = i / KB, kb = i - hf * KB;
     const int wr = (KIND == 0) ? (hf == 0 ? nt : p.I / 128 + nt) : nt * 2 + hf;
@@ -196,25 +272,27 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
     s_prev = s;
     return r;
   };
-  // Writer's activation scale from a stage's scale buffer.
-  auto stage_sa = [&](const uint8_t* ss) { return *(const float*)(ss + (shalf * kBM + srow) * 4); };
 
   // A regions past the tile's last row are not loaded: their rows are never
-  // stored, and every step ends with a full vmcnt wait, so skipped loads need no
-  // accounting.
+  // stored. The vmcnt waits count only the B group, which every wave issues.
   bool a_live[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) a_live[i] = 8 * (4 * wave + i) < nrows;  // wave-uniform
-  auto issue = [&](uint8_t* sa, uint8_t* sb, uint8_t* ss, int kb) {
-    load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, ss + sa_dst);
+  // Loads of a block: the A group (the tile's live A rows) and the B group (the
+  // block's activation scales, then the B tile: exactly kBGroup loads per wave).
+  constexpr int kBLoads = kDmaPerWave - 4;
+  constexpr int kBGroup = kBLoads + 1;
+  auto issue_a = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-      if (i < 4) {
-        if (a_live[i]) load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (4 * wave + i) * 1024);
-      } else {
-        load_lds16(wb + off[i] + (size_t)kb * kBK, sb + (4 * wave + i - 4) * 1024);
-      }
-    }
+    for (int i = 0; i < 4; ++i)
+      if (a_live[i]) load_lds16(abase + off[i] + (size_t)kb * kBK, sTA + (4 * wave + i) * 1024);
+  };
+  // Load i of block kb's B group into stage sb (i = 0: the scales).
+  auto issue_b = [&](uint8_t* sb, int i, int kb) {
+    if (i == 0)
+      load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, sSA + sa_dst);
+    else
+      load_lds16(wb + off[3 + i] + (size_t)kb * kBK, sb + (4 * wave + i - 1) * 1024);
   };
 
   // Accumulators: MF row tiles (16 rows) x 8 column tiles (16 columns).
@@ -231,104 +309,152 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // offset (f_lo / f_hi) plus a constant, and the reads use immediate offsets.
   const uint32_t f_lo = l16 * kBK + ((g ^ ((l16 >> 1) & 7)) << 4);
   const uint32_t f_hi = l16 * kBK + (((g + 4) ^ ((l16 >> 1) & 7)) << 4);
-  const uint32_t a_wave = RG * wm * kBK;
+  const uint32_t a_lo = lds_addr(sTA) + RG * wm * kBK + f_lo;
+  const uint32_t a_hi = lds_addr(sTA) + RG * wm * kBK + f_hi;
   // B rows of this wave's eight 16-column tiles. gate_up: tiles 0-3 gate columns
   // [64 wn, +64), tiles 4-7 the matching up columns; down: columns [128 wn, +128).
   const uint32_t b_wave = (KIND == 0 ? 64 * wn : 128 * wn) * kBK;
-  auto frag = [&](const uint8_t* t) -> v8i {
-    const int4 lo = *(const int4*)(t + f_lo);
-    const int4 hi = *(const int4*)(t + f_hi);
-    return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  constexpr int kBRow[8] = {0, 16, 32, 48, (KIND == 0) ? 128 : 64, (KIND == 0) ? 144 : 80,
+                            (KIND == 0) ? 160 : 96, (KIND == 0) ? 176 : 112};
+  static_assert(16 * kBK == 2048, "A fragment stride");
+  auto read_a = [&](v8i (&a)[MF]) {
+    v4i lo[MF], hi[MF];
+    lds_frags_a<MF>(a_lo, a_hi, lo, hi);
+#pragma unroll
+    for (int m = 0; m < MF; ++m) a[m] = cat8(lo[m], hi[m]);
   };
-  auto brow0 = [](int n) { return (KIND == 0) ? ((n < 4) ? 16 * n : 128 + 16 * (n - 4)) : 16 * n; };
-
-  // Load i of issue(), alone: the computing waves spread the next block's loads
-  // over the eight column tiles of the current one, weights (loads 4-7, and the
-  // scales) first, which keeps the load path and the LDS writes from arriving as
-  // one burst at the start of the step.
-  auto issue_part = [&](int i, uint8_t* sa, uint8_t* sb, uint8_t* ss, int kb) {
-    if (i == 4) load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, ss + sa_dst);
-    if (i < 4) {
-      if (a_live[i]) load_lds16(abase + off[i] + (size_t)kb * kBK, sa + (4 * wave + i) * 1024);
-    } else {
-      load_lds16(wb + off[i] + (size_t)kb * kBK, sb + (4 * wave + i - 4) * 1024);
-    }
-  };
-  // MFMAs of the current block (stage sa / sb, ratios sr) with the loads of block
-  // kn into the next stage (na / nb / nsa) issued along the way.
-  auto compute = [&](const uint8_t* sa, const uint8_t* sb, const float* sr, uint8_t* na,
-                     uint8_t* nb, uint8_t* nsa, int kn) {
-    const uint8_t* ta = sa + a_wave;
-    const uint8_t* tb = sb + b_wave;
-    v8i a[MF];
-    v4f rr[MF];  // ratios of the column half in use: gate, then up (gate_up)
+  // B fragment of column tile n: issued here, completed by lds_frag_wait.
+  // Ratios of MF 16-row fragments (4 rows per lane, fragment m at +64 m bytes).
+  auto issue_ratios = [&](uint32_t addr, v4i (&r)[MF]) {
 #pragma unroll
     for (int m = 0; m < MF; ++m) {
-      a[m] = frag(ta + 16 * m * kBK);
-      rr[m] = *(const v4f*)&sr[((KIND == 0) ? 0 : wn) * kBM + RG * wm + 16 * m + 4 * g];
+      switch (m) {
+        case 0: lds_v4_issue<0>(addr, r[m]); break;
+        case 1: lds_v4_issue<64>(addr, r[m]); break;
+        case 2: lds_v4_issue<128>(addr, r[m]); break;
+        default: lds_v4_issue<192>(addr, r[m]); break;
+      }
     }
-    // B fragments double-buffered: the reads of column tile n + 1 (and, at the
-    // gate / up boundary, the up-half ratios) are issued before the MFMAs of tile
-    // n, fenced off from them so the scheduler does not sink them to their use.
-    v8i b = frag(tb + brow0(0) * kBK);
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto wait_ratios = [&](v4i (&r)[MF], v4f (&f)[MF]) {
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      issue_part((n + 4) & 7, na, nb, nsa, kn);
-      v8i bn = b;
-      if (n + 1 < 8) bn = frag(tb + brow0(n + 1) * kBK);
-      v4f rn[MF];
-#pragma unroll
-      for (int m = 0; m < MF; ++m) {
-        rn[m] = rr[m];
-        if (KIND == 0 && n == 3) rn[m] = *(const v4f*)&sr[kBM + RG * wm + 16 * m + 4 * g];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int m = 0; m < MF; ++m) {
-        const v4f c = acc[m][n] * rr[m];
-        acc[m][n] = mfma16_fp8_acc(a[m], b, c);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int m = 0; m < MF; ++m) rr[m] = rn[m];
-      b = bn;
+    for (int m = 0; m < MF; ++m) {
+      lds_v4_wait(r[m]);
+      f[m] = (v4f){__int_as_float(r[m].x), __int_as_float(r[m].y), __int_as_float(r[m].z),
+                   __int_as_float(r[m].w)};
+    }
+  };
+  auto issue_bfrag = [&](uint32_t lo_addr, uint32_t hi_addr, int n, v4i& lo, v4i& hi) {
+    switch (n) {
+      case 0: lds_frag_issue<kBRow[0] * kBK>(lo_addr, hi_addr, lo, hi); break;
+      case 1: lds_frag_issue<kBRow[1] * kBK>(lo_addr, hi_addr, lo, hi); break;
+      case 2: lds_frag_issue<kBRow[2] * kBK>(lo_addr, hi_addr, lo, hi); break;
+      case 3: lds_frag_issue<kBRow[3] * kBK>(lo_addr, hi_addr, lo, hi); break;
+      case 4: lds_frag_issue<kBRow[4] * kBK>(lo_addr, hi_addr, lo, hi); break;
+      case 5: lds_frag_issue<kBRow[5] * kBK>(lo_addr, hi_addr, lo, hi); break;
+      case 6: lds_frag_issue<kBRow[6] * kBK>(lo_addr, hi_addr, lo, hi); break;
+      default: lds_frag_issue<kBRow[7] * kBK>(lo_addr, hi_addr, lo, hi); break;
     }
   };
 
-  // Prologue: block 0 and its scales.
-  issue(sTA0, sTB0, sA0, 0);
-  wait_vm<0>();
-  __syncthreads();  // sW and block 0's stage
-  (shalf ? sR0 + kBM : sR0)[srow] = ratio(stage_sa(sA0), sW[shalf][0]);  // 0: the accumulators start at 0
-  __syncthreads();
+  // Ratios of block kb + 1 (scales of block kb + 1 landed) into sr.
+  auto store_ratio = [&](float* sr, int kb) {
+    (shalf ? sr + kBM : sr)[srow] = ratio(lds_f32(sa_own), sW[shalf][kb]);
+  };
 
-  // One step: the MFMAs of block kb with the loads of block kb + 1 into the other
-  // stage spread among them (waves without rows issue them at once), then the
-  // ratios of block kb + 1 once its loads landed.
-  auto step = [&](int kb, const uint8_t* ca, const uint8_t* cb, const float* cr, uint8_t* na,
-                  uint8_t* nb, uint8_t* nsa, float* nr) {
-    // Every step issues the same loads (past the last block it re-reads block
-    // KB - 1 into the stage that is not read again), so the waits stay exact.
-    const int kn = min(kb + 1, KB - 1);
-    if (active)
-      compute(ca, cb, cr, na, nb, nsa, kn);
-    else
-      issue(na, nb, nsa, kn);
-    __builtin_amdgcn_sched_barrier(0);
-    // Past the last block the ratio of the re-read block is 1 and lands in a
-    // stage that is not read again.
-    wait_vm<0>();
-    __builtin_amdgcn_sched_barrier(0);
-    (shalf ? nr + kBM : nr)[srow] = ratio(stage_sa(nsa), sW[shalf][kn]);
-    __builtin_amdgcn_sched_barrier(0);
+  // One K step: the MFMAs of block kb (B tile in stage cb, ratios in cr). On entry
+  // the A tile and the B tile of block kb have been issued and the B group of
+  // block kb + 1 may still be in flight.
+  //  1. wait for all but the last B group, barrier: A(kb) and B(kb) have landed,
+  //     the ratios of block kb are visible, and every wave is done with the B
+  //     stage about to be refilled;
+  //  2. read this wave's A fragments, run the MFMAs of column tiles 0 and 1;
+  //     the scales of block kb + 1 (oldest loads in flight) land, the scale
+  //     writers store block kb + 1's ratios into nr;
+  //  3. barrier: the A stage is free;
+  //  4. issue the A group of block kb + 1 and, spread among the remaining MFMAs,
+  //     the B group of block kb + 2 (into stage nb).
+  // Past the last block the loads re-read block KB - 1 into stages that are not
+  // read again, so every step issues the same loads and the waits stay exact.
+  auto step = [&](int kb, const uint8_t* cb, const float* cr, uint8_t* nb, float* nr) {
+    wait_vm<kBGroup>();
     lds_barrier();
+    const int kb2 = min(kb + 2, KB - 1);
+    if (active) {
+      const uint32_t b_lo = lds_addr(cb) + b_wave + f_lo, b_hi = lds_addr(cb) + b_wave + f_hi;
+      // ratios of the column half in use: gate, then up (gate_up)
+      const uint32_t r_addr = lds_addr(cr) + 4 * (((KIND == 0) ? 0 : wn) * kBM + RG * wm + 4 * g);
+      v4i rq[MF];
+      v4f rr[MF];
+      issue_ratios(r_addr, rq);
+      v4i blo, bhi;
+      issue_bfrag(b_lo, b_hi, 0, blo, bhi);
+      v8i a[MF];
+      read_a(a);  // waits for the ratio and B reads issued before it too
+      wait_ratios(rq, rr);
+      lds_frag_wait(blo, bhi);
+      v8i b = cat8(blo, bhi);
+      __builtin_amdgcn_sched_barrier(0);
+      // B fragments double-buffered: the reads of column tile n + 1 (and, at the
+      // gate / up boundary, the up-half ratios) are issued before the MFMAs of
+      // tile n and waited for after them.
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        v4i nlo, nhi;
+        if (n + 1 < 8) issue_bfrag(b_lo, b_hi, n + 1, nlo, nhi);
+        v4i uq[MF];
+        if (KIND == 0 && n == 3) issue_ratios(r_addr + 4 * kBM, uq);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < MF; ++m) {
+          const v4f c = acc[m][n] * rr[m];
+          acc[m][n] = mfma16_fp8_acc(a[m], b, c);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (n == 1) {
+          wait_vm<kBGroup - 1>();
+          if (kb + 1 < KB) store_ratio(nr, kb + 1);
+          lds_barrier();
+          issue_a(min(kb + 1, KB - 1));
+        }
+        if (n >= 2 && n < 2 + kBGroup) issue_b(nb, n - 2, kb2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (KIND == 0 && n == 3) wait_ratios(uq, rr);
+        if (n + 1 < 8) {
+          lds_frag_wait(nlo, nhi);
+          b = cat8(nlo, nhi);
+        }
+      }
+    } else {
+      wait_vm<kBGroup - 1>();
+      if (kb + 1 < KB) store_ratio(nr, kb + 1);
+      lds_barrier();
+      issue_a(min(kb + 1, KB - 1));
+#pragma unroll
+      for (int i = 0; i < kBGroup; ++i) issue_b(nb, i, kb2);
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
-  for (int kb = 0; kb < KB; kb += 2) {
-    step(kb, sTA0, sTB0, sR0, sTA1, sTB1, sA1, sR1);
-    if (kb + 1 < KB) step(kb + 1, sTA1, sTB1, sR1, sTA0, sTB0, sA0, sR0);
+  // Prologue: A(0), the B groups of blocks 0 and 1, and block 0's ratios, which
+  // the first step's barrier publishes.
+  issue_a(0);
+#pragma unroll
+  for (int i = 0; i < kBGroup; ++i) issue_b(sTB0, i, 0);
+  wait_vm<0>();
+  __syncthreads();      // sW's stores (other threads) before the first ratio
+  store_ratio(sR0, 0);  // s_prev = 0: the accumulators start at 0
+  // the scale buffer is refilled only after its reader has read it
+#pragma unroll
+  for (int i = 0; i < kBGroup; ++i) issue_b(sTB1, i, min(1, KB - 1));
+  for (int kb = 0; kb < KB; kb += 6) {
+    step(kb, sTB0, sR0, sTB2, sR1);
+    if (kb + 1 < KB) step(kb + 1, sTB1, sR1, sTB0, sR0);
+    if (kb + 2 < KB) step(kb + 2, sTB2, sR0, sTB1, sR1);
+    if (kb + 3 < KB) step(kb + 3, sTB0, sR1, sTB2, sR0);
+    if (kb + 4 < KB) step(kb + 4, sTB1, sR0, sTB0, sR1);
+    if (kb + 5 < KB) step(kb + 5, sTB2, sR1, sTB1, sR0);
   }
+  wait_vm<0>();  // no load is still landing in LDS past this point
   (shalf ? sLast + kBM : sLast)[srow] = s_prev;
   __syncthreads();
 
@@ -396,19 +522,18 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
 
 template <int KIND>
 __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t sTA0[kStageA];
+  __shared__ __attribute__((aligned(16))) uint8_t sTA[kStageA];
   __shared__ __attribute__((aligned(16))) uint8_t sTB0[kStageB];
-  __shared__ __attribute__((aligned(16))) uint8_t sTA1[kStageA];
   __shared__ __attribute__((aligned(16))) uint8_t sTB1[kStageB];
-  __shared__ __attribute__((aligned(16))) uint8_t sA0[kStageSA];
-  __shared__ __attribute__((aligned(16))) uint8_t sA1[kStageSA];
+  __shared__ __attribute__((aligned(16))) uint8_t sTB2[kStageB];
+  __shared__ __attribute__((aligned(16))) uint8_t sSA[kStageSA];
   __shared__ __attribute__((aligned(16))) float sR0[2 * kBM];
   __shared__ __attribute__((aligned(16))) float sR1[2 * kBM];
   __shared__ __attribute__((aligned(16))) float sLast[2 * kBM];
   __shared__ int sSrc[kBM];
   __shared__ float sRed[2][kBM];
   __shared__ float sW[2][kMaxKB];
-  const BlkLds s{sTA0, sTB0, sTA1, sTB1, sA0, sA1, sR0, sR1, sLast, sSrc, sRed, sW};
+  const BlkLds s{sTA, sTB0, sTB1, sTB2, sSA, sR0, sR1, sLast, sSrc, sRed, sW};
 
   // XCD-aware item index: workgroup b runs on XCD b % 8; XCD x takes the
   // contiguous item range [x * per, (x + 1) * per).
