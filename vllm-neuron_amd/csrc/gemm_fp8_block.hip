@@ -273,19 +273,17 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
     return r;
   };
 
-  // A regions past the tile's last row are not loaded: their rows are never
-  // stored. The vmcnt waits count only the B group, which every wave issues.
-  bool a_live[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) a_live[i] = 8 * (4 * wave + i) < nrows;  // wave-uniform
-  // Loads of a block: the A group (the tile's live A rows) and the B group (the
+  // Loads of a block: the A group (the tile's rows, exactly kAGroup loads per wave;
+  // rows past the tile's end re-read row 0, never stored) and the B group (the
   // block's activation scales, then the B tile: exactly kBGroup loads per wave).
+  // Fixed counts keep every vmcnt wait exact.
+  constexpr int kAGroup = 4;
   constexpr int kBLoads = kDmaPerWave - 4;
   constexpr int kBGroup = kBLoads + 1;
   auto issue_a = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (a_live[i]) load_lds16(abase + off[i] + (size_t)kb * kBK, sTA + (4 * wave + i) * 1024);
+    for (int i = 0; i < kAGroup; ++i)
+      load_lds16(abase + off[i] + (size_t)kb * kBK, sTA + (4 * wave + i) * 1024);
   };
   // Load i of block kb's B group into stage sb (i = 0: the scales).
   auto issue_b = [&](uint8_t* sb, int i, int kb) {
@@ -368,12 +366,13 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   //  1. wait for all but the last B group, barrier: A(kb) and B(kb) have landed,
   //     the ratios of block kb are visible, and every wave is done with the B
   //     stage about to be refilled;
-  //  2. read this wave's A fragments, run the MFMAs of column tiles 0 and 1;
-  //     the scales of block kb + 1 (oldest loads in flight) land, the scale
-  //     writers store block kb + 1's ratios into nr;
-  //  3. barrier: the A stage is free;
-  //  4. issue the A group of block kb + 1 and, spread among the remaining MFMAs,
-  //     the B group of block kb + 2 (into stage nb).
+  //  2. read this wave's A fragments, issue the MFMAs of column tile 0;
+  //  3. barrier: the A stage is free; issue the A group of block kb + 1;
+  //  4. after column tile 1 the scales of block kb + 1 (the oldest loads in flight
+  //     but the A group) have landed: the scale writers store block kb + 1's
+  //     ratios into nr, which the next step's first barrier publishes;
+  //  5. the B group of block kb + 2 (into stage nb) is spread among the
+  //     remaining MFMAs.
   // Past the last block the loads re-read block KB - 1 into stages that are not
   // read again, so every step issues the same loads and the waits stay exact.
   auto step = [&](int kb, const uint8_t* cb, const float* cr, uint8_t* nb, float* nr) {
@@ -411,11 +410,13 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
           acc[m][n] = mfma16_fp8_acc(a[m], b, c);
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (n == 1) {
-          wait_vm<kBGroup - 1>();
-          if (kb + 1 < KB) store_ratio(nr, kb + 1);
+        if (n == 0) {
           lds_barrier();
           issue_a(min(kb + 1, KB - 1));
+        }
+        if (n == 1) {
+          wait_vm<kBGroup - 1 + kAGroup>();
+          if (kb + 1 < KB) store_ratio(nr, kb + 1);
         }
         if (n >= 2 && n < 2 + kBGroup) issue_b(nb, n - 2, kb2);
         __builtin_amdgcn_sched_barrier(0);
@@ -426,10 +427,10 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
         }
       }
     } else {
-      wait_vm<kBGroup - 1>();
-      if (kb + 1 < KB) store_ratio(nr, kb + 1);
       lds_barrier();
       issue_a(min(kb + 1, KB - 1));
+      wait_vm<kBGroup - 1 + kAGroup>();
+      if (kb + 1 < KB) store_ratio(nr, kb + 1);
 #pragma unroll
       for (int i = 0; i < kBGroup; ++i) issue_b(nb, i, kb2);
     }
