@@ -153,6 +153,9 @@ __device__ __forceinline__ void lds_frags_a(uint32_t lo_addr, uint32_t hi_addr, 
         : "memory");
   }
 }
+__device__ __forceinline__ void lds_st32(uint32_t addr, int v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
 __device__ __forceinline__ float lds_f32(uint32_t addr) {
   float v;
   asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
@@ -193,21 +196,6 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   const bool is_sh = e >= p.E;
   const int ej = is_sh ? e - p.E : e;
 
-  for (int r = tid; r < kBM; r += kBlkThreads) {
-    int src = -1;
-    if (r < nrows) {
-      const long slot = slot0 + r;
-      if (KIND == 0) {
-        long sv = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
-        src = (sv >= 0 && sv < p.T) ? (int)sv : -1;
-      } else {
-        src = (int)(rbase + r);
-      }
-    }
-    sSrc[r] = src;
-  }
-  __syncthreads();
-
   const uint8_t* wb;
   const float* wsb;
   if (KIND == 0) {
@@ -222,25 +210,63 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // chunk l%8.
   uint32_t off[kDmaPerWave];
 #pragma unroll
-  for (int i = 0; i < kDmaPerWave; ++i) {
+  for (int i = 4; i < kDmaPerWave; ++i) {
     const int row = 8 * (4 * wave + (i & 3)) + (lane >> 3);
-    if (i < 4) {
-      const int src = sSrc[row];
-      off[i] = (uint32_t)(src >= 0 ? src : 0) * (uint32_t)Kdim + (uint32_t)(swz(row, lane & 7) * 16);
+    // Tile row -> weight row. Column tile n of a wave reads tile rows 16 n + j,
+    // and they hold output columns 4 j + n (gate_up, per 64-column wave half) or
+    // 8 j + n (down, per 128-column half): lane j then holds consecutive output
+    // columns and stores them directly (4 fp8 codes or 8 bf16 values).
+    int wrow;
+    if (KIND == 0) {
+      const int r = row & 127;
+      const int hc = (r & 64) + 4 * (r & 15) + ((r >> 4) & 3);
+      wrow = (row < 128) ? nt * 128 + hc : p.I + nt * 128 + hc;
     } else {
-      // Tile row -> weight row. Column tile n of a wave reads tile rows 16 n + j,
-      // and they hold output columns 4 j + n (gate_up, per 64-column wave half) or
-      // 8 j + n (down, per 128-column half): lane j then holds consecutive output
-      // columns and stores them directly (4 fp8 codes or 8 bf16 values).
-      int wrow;
-      if (KIND == 0) {
-        const int r = row & 127;
-        const int hc = (r & 64) + 4 * (r & 15) + ((r >> 4) & 3);
-        wrow = (row < 128) ? nt * 128 + hc : p.I + nt * 128 + hc;
-      } else {
-        wrow = nt * kBN + (row & 128) + 8 * (row & 15) + ((row >> 4) & 7);
-      }
-      off[i] = (uint32_t)(wrow * Kdim + swz(row, lane & 7) * 16);
+      wrow = nt * kBN + (row & 128) + 8 * (row & 15) + ((row >> 4) & 7);
+    }
+    off[i] = (uint32_t)(wrow * Kdim + swz(row, lane & 7) * 16);
+  }
+
+  // The loads that do not depend on each other are in flight together: block 0's
+  // B tile (issued first), each tile row's token (gate_up) or slot (down) and the
+  // weight block scales (2 KB <= 256 values); the A rows need the tokens. The LDS
+  // stores and reads around them are asm so the compiler does not add waits for
+  // the B tile's loads.
+#pragma unroll
+  for (int i = 4; i < kDmaPerWave; ++i) load_lds16(wb + off[i], sTB0 + (4 * wave + i - 4) * 1024);
+  const int srow = 64 * wm + lane, shalf = wn;  // the scale writer's row and half (below)
+  const int sa_dst = (wn * kBM + 64 * wm) * 4;
+  if constexpr (KIND == 1) {
+    // down: tile row r is h row rbase + r, so block 0's A tile and scales need no
+    // lookup and join the first round trip
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 8 * (4 * wave + i) + (lane >> 3);
+      const uint32_t rs = (uint32_t)(row < nrows ? rbase + row : rbase);
+      off[i] = rs * (uint32_t)Kdim + (uint32_t)(swz(row, lane & 7) * 16);
+      load_lds16(p.a + off[i], sTA + (4 * wave + i) * 1024);
+    }
+    const uint32_t rs = (uint32_t)(srow < nrows ? rbase + srow : rbase);
+    load_lds4((const uint8_t*)p.as + rs * (uint32_t)(KB * 4), sSA + sa_dst);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int whf = tid < KB ? 0 : 1, wkb = min(tid, 2 * KB - 1) - whf * KB;
+  const int wr = (KIND == 0) ? (whf == 0 ? nt : p.I / 128 + nt) : nt * 2 + whf;
+  const float wsv = wsb[(size_t)wr * KB + wkb];
+  const int trow = min(tid, nrows - 1);  // nrows in [1, kBM]
+  long sv = (KIND == 0) ? (is_sh ? slot0 + trow - p.NB - (long)ej * p.T : (long)p.tpid[slot0 + trow])
+                        : rbase + trow;
+  if (KIND == 0 && (sv < 0 || sv >= p.T)) sv = -1;
+  const int src = tid < nrows ? (int)sv : -1;
+  if (tid < kBM) lds_st32(lds_addr(sSrc) + 4 * tid, src);
+  if (tid < 2 * KB) lds_st32(lds_addr(&sW[whf][wkb]), __float_as_int(wsv));
+  lds_barrier();
+  if constexpr (KIND == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 8 * (4 * wave + i) + (lane >> 3);
+      const int rs = __float_as_int(lds_f32(lds_addr(sSrc) + 4 * row));
+      off[i] = (uint32_t)(rs >= 0 ? rs : 0) * (uint32_t)Kdim + (uint32_t)(swz(row, lane & 7) * 16);
     }
   }
   const uint8_t* abase = p.a;
@@ -253,17 +279,11 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // for column half wn); the weight scales are staged once per tile.
   // Thread (wave (wm, wn), lane j) owns row 64 wm + j and half wn: the rows its
   // own wave's scale load fills, so its own vmcnt wait covers them.
-  const int srow = 64 * wm + lane, shalf = wn;
-  const bool svalid = sSrc[srow] >= 0;
+  const int ssrc = __float_as_int(lds_f32(lds_addr(sSrc) + 4 * srow));
+  const bool svalid = ssrc >= 0;
   // Byte offsets of operand rows fit 32 bits: the entry points reject larger operands.
-  const uint32_t off_sa = (uint32_t)(sSrc[64 * wm + lane] >= 0 ? sSrc[64 * wm + lane] : 0) * (uint32_t)(KB * 4);
-  const int sa_dst = (wn * kBM + 64 * wm) * 4;
+  const uint32_t off_sa = (uint32_t)(svalid ? ssrc : 0) * (uint32_t)(KB * 4);
   const uint32_t sa_own = lds_addr(sSA) + (uint32_t)((shalf * kBM + srow) * 4);
-  for (int i = tid; i < 2 * KB; i += kBlkThreads) {
-    const int hf = i / KB, kb = i - hf * KB;
-    const int wr = (KIND == 0) ? (hf == 0 ? nt : p.I / 128 + nt) : nt * 2 + hf;
-    sW[hf][kb] = wsb[(size_t)wr * KB + kb];
-  }
   float s_prev = 0.f;
   auto ratio = [&](float sa, float sw) {
     float s = svalid ? sa * sw : 1.f;
@@ -436,13 +456,14 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  // Prologue: A(0), the B groups of blocks 0 and 1, and block 0's ratios, which
-  // the first step's barrier publishes.
-  issue_a(0);
-#pragma unroll
-  for (int i = 0; i < kBGroup; ++i) issue_b(sTB0, i, 0);
+  // Prologue (block 0's B tile, and for down its A tile and scales, are on their
+  // way): A(0) and block 0's scales, block 0's ratios, which the first step's
+  // barrier publishes, and the B group of block 1.
+  if constexpr (KIND == 0) {
+    issue_a(0);
+    issue_b(sTB0, 0, 0);
+  }
   wait_vm<0>();
-  __syncthreads();      // sW's stores (other threads) before the first ratio
   store_ratio(sR0, 0);  // s_prev = 0: the accumulators start at 0
   // the scale buffer is refilled only after its reader has read it
 #pragma unroll
