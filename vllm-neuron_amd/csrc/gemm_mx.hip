@@ -111,21 +111,33 @@ __device__ __forceinline__ float mx_act(float g, int act) {
 // so the wait for the oldest stage is a compile-time vmcnt; the fragment reads
 // are asm statements that wait for their own data (see gemm_fp8.hip).
 // ---------------------------------------------------------------------------
-template <int MT, int WFMT>
+template <int MT, int WFMT, bool TBL>
 struct MxStage {
   static constexpr int KPS = (WFMT == kFmtFp4) ? 2 : 1;  // 128-K blocks per stage
   static constexpr int AQ = MT / 8;                     // activation loads per K block
   static constexpr int NSQ = (MT + 63) / 64;            // activation scale loads per K block
   uint8_t b[4][8192];                  // wave w's 64 weight rows x 128 bytes
-  uint32_t bs[4][KPS][64];             // their scale dwords (row 16 j + r of the wave)
+  uint32_t bs[TBL ? 1 : 4][KPS][64];   // their scale dwords (row 16 j + r of the wave; unused
+                                       // with the per-item scale table)
   uint8_t a[KPS * AQ + 1][1024];       // activation rows: slot kk * AQ + q = rows 8q.. of block kk
   uint32_t as[KPS][NSQ + 1][64];       // activation scale dwords per 64-row group (+ a spare)
 };
+
+// Per-item weight scale table (K <= 4096): the E8M0 bytes of each wave's 64
+// weight rows for the whole K, one 128-byte LDS row per weight row. Loaded once
+// per work item with 16-byte direct-to-LDS loads (whole row segments) instead of
+// one 4-byte load per row and stage, whose 64 distinct lines per instruction
+// cost the load path more than the stage's weight tile. The table's 16-byte
+// pieces are XOR-swizzled by row so a fragment's 16 rows hit distinct banks.
+constexpr int kMxTblMaxK = 4096;
 
 // Weight fragments of four 16-row column tiles (j at +2048 j), their four scale
 // dwords (at +64 j), one activation fragment (lo / hi) and its scale dword, read
 // in one statement that waits for its data. fp4 weights: one 16-byte chunk per
 // tile (the MFMA's fp4 operand); fp8 weights: two.
+// SST: byte stride between the column tiles' scale dwords (64 in a stage, 2048 in
+// the per-item table).
+template <int SST>
 __device__ __forceinline__ void mx_read_w4(uint32_t b, uint32_t bs, uint32_t a_lo, uint32_t a_hi,
                                            uint32_t as, v4i (&w)[4], int (&ws)[4], v4i& al,
                                            v4i& ah, int& sa) {
@@ -135,18 +147,19 @@ __device__ __forceinline__ void mx_read_w4(uint32_t b, uint32_t bs, uint32_t a_l
       "ds_read_b128 %2, %11 offset:4096\n\t"
       "ds_read_b128 %3, %11 offset:6144\n\t"
       "ds_read_b32 %4, %12\n\t"
-      "ds_read_b32 %5, %12 offset:64\n\t"
-      "ds_read_b32 %6, %12 offset:128\n\t"
-      "ds_read_b32 %7, %12 offset:192\n\t"
+      "ds_read_b32 %5, %12 offset:%16\n\t"
+      "ds_read_b32 %6, %12 offset:%17\n\t"
+      "ds_read_b32 %7, %12 offset:%18\n\t"
       "ds_read_b128 %8, %13\n\t"
       "ds_read_b128 %9, %14\n\t"
       "ds_read_b32 %10, %15\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(ws[0]), "=&v"(ws[1]),
         "=&v"(ws[2]), "=&v"(ws[3]), "=&v"(al), "=&v"(ah), "=&v"(sa)
-      : "v"(b), "v"(bs), "v"(a_lo), "v"(a_hi), "v"(as)
+      : "v"(b), "v"(bs), "v"(a_lo), "v"(a_hi), "v"(as), "n"(SST), "n"(2 * SST), "n"(3 * SST)
       : "memory");
 }
+template <int SST>
 __device__ __forceinline__ void mx_read_w8(uint32_t b_lo, uint32_t b_hi, uint32_t bs, uint32_t a_lo,
                                            uint32_t a_hi, uint32_t as, v4i (&w)[8], int (&ws)[4],
                                            v4i& al, v4i& ah, int& sa) {
@@ -160,9 +173,9 @@ __device__ __forceinline__ void mx_read_w8(uint32_t b_lo, uint32_t b_hi, uint32_
       "ds_read_b128 %6, %15 offset:6144\n\t"
       "ds_read_b128 %7, %16 offset:6144\n\t"
       "ds_read_b32 %8, %17\n\t"
-      "ds_read_b32 %9, %17 offset:64\n\t"
-      "ds_read_b32 %10, %17 offset:128\n\t"
-      "ds_read_b32 %11, %17 offset:192\n\t"
+      "ds_read_b32 %9, %17 offset:%21\n\t"
+      "ds_read_b32 %10, %17 offset:%22\n\t"
+      "ds_read_b32 %11, %17 offset:%23\n\t"
       "ds_read_b128 %12, %18\n\t"
       "ds_read_b128 %13, %19\n\t"
       "ds_read_b32 %14, %20\n\t"
@@ -170,7 +183,8 @@ __device__ __forceinline__ void mx_read_w8(uint32_t b_lo, uint32_t b_hi, uint32_
       : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]),
         "=&v"(w[6]), "=&v"(w[7]), "=&v"(ws[0]), "=&v"(ws[1]), "=&v"(ws[2]), "=&v"(ws[3]),
         "=&v"(al), "=&v"(ah), "=&v"(sa)
-      : "v"(b_lo), "v"(b_hi), "v"(bs), "v"(a_lo), "v"(a_hi), "v"(as)
+      : "v"(b_lo), "v"(b_hi), "v"(bs), "v"(a_lo), "v"(a_hi), "v"(as), "n"(SST), "n"(2 * SST),
+        "n"(3 * SST)
       : "memory");
 }
 __device__ __forceinline__ void mx_read_a(uint32_t a_lo, uint32_t a_hi, uint32_t as, v4i& al,
@@ -185,17 +199,18 @@ __device__ __forceinline__ void mx_read_a(uint32_t a_lo, uint32_t a_hi, uint32_t
       : "memory");
 }
 
-template <int MT, int KIND, int PD, int WFMT>
+template <int MT, int KIND, int PD, int WFMT, bool TBL>
 __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
-  using Stage = MxStage<MT, WFMT>;
+  using Stage = MxStage<MT, WFMT, TBL>;
   constexpr int MS = MT / 16;
   constexpr int KPS = Stage::KPS, AQ = Stage::AQ, NSQ = Stage::NSQ;
   constexpr int NA = (KPS * AQ + 3) / 4;       // activation loads per wave per stage
-  constexpr int NV = 8 + KPS + NA + KPS;       // direct-to-LDS loads per wave per stage
+  constexpr int NV = 8 + (TBL ? 0 : KPS) + NA + KPS;  // direct-to-LDS loads per wave per stage
   static_assert(PD >= 2 && PD <= 3 && (PD - 2) * NV < 64, "pipeline depth");
   __shared__ __attribute__((aligned(1024))) Stage st0;
   __shared__ __attribute__((aligned(1024))) Stage st1;
   __shared__ __attribute__((aligned(1024))) Stage st2;
+  __shared__ __attribute__((aligned(16))) uint8_t sTbl[TBL ? 4 * 64 * 128 : 16];
   __shared__ long sSrc[MT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -281,9 +296,11 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
       const size_t kb0 = (size_t)t * KPS;
 #pragma unroll
       for (int i = 0; i < 8; ++i) load_lds16(wb + boff[i] + (size_t)t * 128, &S.b[wave][i * 1024]);
+      if constexpr (!TBL) {
 #pragma unroll
-      for (int kk = 0; kk < KPS; ++kk)
-        load_lds4(wsb + bsoff + (kb0 + kk) * 4, (uint8_t*)&S.bs[wave][kk][0]);
+        for (int kk = 0; kk < KPS; ++kk)
+          load_lds4(wsb + bsoff + (kb0 + kk) * 4, (uint8_t*)&S.bs[wave][kk][0]);
+      }
 #pragma unroll
       for (int a = 0; a < NA; ++a)
         load_lds16(aptr[a] + (kb0 + akk[a]) * 128, &S.a[aslot[a]][0]);
@@ -313,7 +330,13 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
 #pragma unroll
       for (int kk = 0; kk < KPS; ++kk) {
         const uint32_t aw = lds_addr(&cur.a[kk * AQ][0]);
-        const uint32_t bsw = lds_addr(&cur.bs[wave][kk][r16]);
+        // scale dword of row r16 of column tile 0, K block kb = KPS t + kk (table:
+        // piece kb / 4 of the row stored at chunk (kb / 4) ^ (r16 % 8))
+        const int kbs = t * KPS + kk;
+        const uint32_t bsw = TBL ? lds_addr(sTbl) + wave * 8192 + r16 * 128 +
+                                       ((((kbs >> 2) ^ (r16 & 7))) << 4) + ((kbs & 3) << 2)
+                                 : lds_addr(&cur.bs[TBL ? 0 : wave][kk][r16]);
+        constexpr int SST = TBL ? 2048 : 64;
         v8i b[4];
         int bsc[4];
 #pragma unroll
@@ -326,14 +349,14 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
           if (ms == 0) {
             if (WFMT == kFmtFp4) {
               v4i w[4];
-              mx_read_w4(bw + fr + swz(r16, kk * 4 + g) * 16, bsw, a_lo, a_hi, asw, w, bsc, alo,
-                         ahi, sa);
+              mx_read_w4<SST>(bw + fr + swz(r16, kk * 4 + g) * 16, bsw, a_lo, a_hi, asw, w, bsc,
+                              alo, ahi, sa);
 #pragma unroll
               for (int j = 0; j < 4; ++j) b[j] = (v8i){w[j].x, w[j].y, w[j].z, w[j].w, 0, 0, 0, 0};
             } else {
               v4i w[8];
-              mx_read_w8(bw + fr + swz(r16, g) * 16, bw + fr + swz(r16, 4 + g) * 16, bsw, a_lo, a_hi,
-                         asw, w, bsc, alo, ahi, sa);
+              mx_read_w8<SST>(bw + fr + swz(r16, g) * 16, bw + fr + swz(r16, 4 + g) * 16, bsw, a_lo,
+                              a_hi, asw, w, bsc, alo, ahi, sa);
 #pragma unroll
               for (int j = 0; j < 4; ++j) b[j] = cat(w[2 * j], w[2 * j + 1]);
             }
@@ -352,6 +375,20 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
       }
     };
     wait_vm<0>();  // no earlier load is still landing in a stage buffer
+    if constexpr (TBL) {
+      // the item's weight scale table: LDS chunk c = 64 i + lane of the wave's
+      // region is stored chunk c % 8 of row c / 8 and holds the row's scale bytes
+      // [16 pc, +16), pc = (c % 8) ^ (row % 8), so the 16 rows of a fragment read
+      // spread over the LDS banks (KS <= 128 and KS % 16 == 0, checked at launch;
+      // pieces past KS re-read piece 0 and are never read back). The first step's
+      // wait covers these loads, which precede the ring's.
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = 64 * i + lane, row = c >> 3, pc = (c & 7) ^ (row & 7);
+        const int off = (16 * pc < KS) ? 16 * pc : 0;
+        load_lds16(wsb + (size_t)wrow_of(row >> 4, row & 15) * KS + off, sTbl + wave * 8192 + i * 1024);
+      }
+    }
     issue(st0, 0);
     if (PD >= 3) issue(st1, min(1, NSTG - 1));
     for (int t = 0; t < NSTG; t += PD) {
@@ -482,18 +519,28 @@ static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
   const int NT = (KIND == 0) ? a.I / 128 : a.H / 256;
   const long items = (long)max_tiles * NT;
   const int grid = (int)std::max(1L, std::min(items, 4096L));
+  // the per-item scale table for K <= 4096 in whole 16-byte pieces per row
+  // (K % 512 == 0), and for the tiles whose LDS has room
+  const int Kdim = (KIND == 0) ? a.H : a.I;
+  const bool tbl = Kdim <= kMxTblMaxK && Kdim % 512 == 0;
   switch (mt) {
     case 16:
-      hipLaunchKernelGGL((expert_gemm_mx_kernel<16, KIND, 3, WFMT>), dim3(grid), dim3(256), 0, st, a);
+      if (tbl)
+        hipLaunchKernelGGL((expert_gemm_mx_kernel<16, KIND, 3, WFMT, true>), dim3(grid), dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((expert_gemm_mx_kernel<16, KIND, 3, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 32:
-      hipLaunchKernelGGL((expert_gemm_mx_kernel<32, KIND, 3, WFMT>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((expert_gemm_mx_kernel<32, KIND, 3, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 64:
-      hipLaunchKernelGGL((expert_gemm_mx_kernel<64, KIND, 2, WFMT>), dim3(grid), dim3(256), 0, st, a);
+      if (tbl)
+        hipLaunchKernelGGL((expert_gemm_mx_kernel<64, KIND, 2, WFMT, true>), dim3(grid), dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((expert_gemm_mx_kernel<64, KIND, 2, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 128:
-      hipLaunchKernelGGL((expert_gemm_mx_kernel<128, KIND, 2, WFMT>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((expert_gemm_mx_kernel<128, KIND, 2, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
       break;
     default:
       return MOE_ERR_ARG;
