@@ -531,7 +531,10 @@ static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
         hipLaunchKernelGGL((expert_gemm_mx_kernel<16, KIND, 3, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 32:
-      hipLaunchKernelGGL((expert_gemm_mx_kernel<32, KIND, 3, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
+      if (tbl)
+        hipLaunchKernelGGL((expert_gemm_mx_kernel<32, KIND, 2, WFMT, true>), dim3(grid), dim3(256), 0, st, a);
+      else
+        hipLaunchKernelGGL((expert_gemm_mx_kernel<32, KIND, 3, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 64:
       if (tbl)
