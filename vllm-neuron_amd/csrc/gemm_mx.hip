@@ -199,6 +199,36 @@ __device__ __forceinline__ void mx_read_a(uint32_t a_lo, uint32_t a_hi, uint32_t
       : "memory");
 }
 
+// One work item's load sources (per lane).
+template <int NA>
+struct MxSrc {
+  const uint8_t* wb;          // expert weights
+  const uint8_t* wsb;         // expert weight scales
+  uint32_t boff[8];           // weight rows of the lane's eight loads
+  uint32_t bsoff;             // weight scale row of the lane's per-stage scale loads
+  const uint8_t* aptr[NA];    // activation rows
+  const uint8_t* asp;         // activation scale row
+};
+
+// 4-byte global load whose completion the caller's later vmcnt waits cover (the
+// compiler does not count it, so it adds no wait that would drain the ring);
+// vm_ready() marks the point after such a wait from which the value is used.
+__device__ __forceinline__ int gload_i32(const void* p) {
+  int v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ void vm_ready(int& v) { asm volatile("" : "+v"(v)); }
+
+// Persistent streaming form: workgroup b runs items b, b + G, ... (G = grid) and
+// keeps its load ring going across them. During item j's first step the next
+// item's token ids and biases are requested; PD - 1 stages before item j ends
+// the ring moves on to item j + 1, so item j's epilogue runs with item j + 1's
+// first stages in flight. With the scale table, each wave reloads its own table
+// rows for item j + 1 right after its last multiply of item j (no other wave
+// reads them); with three stages the ring's second block of item j + 1 is issued
+// after that reload, so the first step's wait covers the table as well. Items
+// with fewer stages than the ring depth drain between items instead.
 template <int MT, int KIND, int PD, int WFMT, bool TBL>
 __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
   using Stage = MxStage<MT, WFMT, TBL>;
@@ -207,11 +237,9 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
   constexpr int NA = (KPS * AQ + 3) / 4;       // activation loads per wave per stage
   constexpr int NV = 8 + (TBL ? 0 : KPS) + NA + KPS;  // direct-to-LDS loads per wave per stage
   static_assert(PD >= 2 && PD <= 3 && (PD - 2) * NV < 64, "pipeline depth");
-  __shared__ __attribute__((aligned(1024))) Stage st0;
-  __shared__ __attribute__((aligned(1024))) Stage st1;
-  __shared__ __attribute__((aligned(1024))) Stage st2;
+  __shared__ __attribute__((aligned(1024))) Stage st[PD];
   __shared__ __attribute__((aligned(16))) uint8_t sTbl[TBL ? 4 * 64 * 128 : 16];
-  __shared__ long sSrc[MT];
+  __shared__ long sSrc[2][MT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r16 = lane & 15;
@@ -220,94 +248,179 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
   const int NSTG = Kdim / (128 * KPS);    // stages (K % (128 KPS) == 0, checked by the entry points)
   const int NT = (KIND == 0) ? p.I / 128 : p.H / 256;
   const int total = p.num_tiles[0] * NT;
+  const int G = gridDim.x;
   const std::integral_constant<int, WFMT> wfmt{};
+  int wi = blockIdx.x;
+  if (wi >= total) return;
+  const bool stream = NSTG >= PD;  // crossing step NSTG - PD + 1 >= 1 follows the token loads
+  const size_t wrow_bytes = (size_t)Kdim * ((WFMT == kFmtFp4) ? 64 : 128) / 128;
+  const int rows_w = (KIND == 0) ? 2 * p.I : p.H;
 
-  for (int wi = blockIdx.x; wi < total; wi += gridDim.x) {
-    const int tile = wi / NT, nt = wi - tile * NT;
-    const int4 td = p.tiles[tile];
-    const int e = td.x, nrows = td.z;
-    const long slot0 = td.y, row0 = td.w;
-    if (e < 0 || e >= p.E + p.nsh) continue;  // workgroup-uniform: malformed tile
-    const bool is_sh = e >= p.E;
-    const int ej = is_sh ? e - p.E : e;
-
-    if (tid < MT) {
-      long src = -1;
-      if (tid < nrows) {
-        const long slot = slot0 + tid;
-        if (KIND == 0) {
-          src = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
-          if (src >= p.T) src = -1;  // token ids outside [0, T) are padding
-        } else {
-          src = row0 + tid;
-        }
-      }
-      sSrc[tid] = src;
-    }
-    __syncthreads();
-
-    const size_t wrow_bytes = (size_t)Kdim * ((WFMT == kFmtFp4) ? 64 : 128) / 128;
-    const int rows_w = (KIND == 0) ? 2 * p.I : p.H;
-    const uint8_t* wb = (is_sh ? p.wsh : p.w) + (size_t)ej * rows_w * wrow_bytes;
-    const uint8_t* wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * rows_w * KS;
-    const float* bb = is_sh ? p.bsh : p.bias;
-    if (bb != nullptr) bb += (size_t)ej * rows_w;
-    // weight row of column tile j, row r of the tile, for this wave
-    auto wrow_of = [&](int j, int r) -> int {
-      if (KIND == 0)
-        return (j < 2) ? nt * 128 + wave * 32 + j * 16 + r : p.I + nt * 128 + wave * 32 + (j - 2) * 16 + r;
-      return nt * 256 + wave * 64 + j * 16 + r;
-    };
-    // Load sources. Weight load i: rows 8 (i & 1) + l / 8 of column tile i / 2, stored
-    // chunk l % 8 = logical chunk swz(row, l % 8) of the row's 128-byte segment.
-    uint32_t boff[8];
+  // Work item descriptor (workgroup-uniform); an expert out of range (only in a
+  // malformed tile list) runs as expert 0 with no rows.
+  struct ItemDesc {
+    int e, nrows, nt;
+    long slot0, row0;
+  };
+  typedef __attribute__((address_space(4))) const int* const_int_ptr;
+  const const_int_ptr ctiles = (const_int_ptr)p.tiles;  // scalar loads: no vmcnt
+  auto desc = [&](int w) {
+    ItemDesc d;
+    const int tile = w / NT;
+    d.nt = w - tile * NT;
+    const int4 td = make_int4(ctiles[4 * tile], ctiles[4 * tile + 1], ctiles[4 * tile + 2],
+                              ctiles[4 * tile + 3]);
+    const bool ok = td.x >= 0 && td.x < p.E + p.nsh;
+    d.e = ok ? td.x : 0;
+    d.nrows = ok ? td.z : 0;
+    d.slot0 = td.y;
+    d.row0 = td.w;
+    return d;
+  };
+  // weight row of column tile j, row r of the tile, for this wave
+  auto wrow_of = [&](const ItemDesc& d, int j, int r) -> int {
+    if (KIND == 0)
+      return (j < 2) ? d.nt * 128 + wave * 32 + j * 16 + r : p.I + d.nt * 128 + wave * 32 + (j - 2) * 16 + r;
+    return d.nt * 256 + wave * 64 + j * 16 + r;
+  };
+  // token (gate_up) or h row (down) of tile row r; -1 for padding. tp: the
+  // token-position entry (gate_up, routed experts).
+  auto row_src = [&](const ItemDesc& d, int r, long tp) -> long {
+    if (r >= d.nrows) return -1;
+    if (KIND == 1) return d.row0 + r;
+    const long s = (d.e >= p.E) ? d.slot0 + r - p.NB - (long)(d.e - p.E) * p.T : tp;
+    return (s >= 0 && s < p.T) ? s : -1;  // token ids outside [0, T) are padding
+  };
+  auto tp_ptr = [&](const ItemDesc& d, int r) -> const int32_t* {  // gate_up only
+    return p.tpid + ((d.e < p.E && r < d.nrows) ? d.slot0 + r : 0);
+  };
+  auto tp_read = [&](const ItemDesc& d, int r) -> long { return KIND == 0 ? (long)*tp_ptr(d, r) : 0; };
+  auto bias_ptr = [&](const ItemDesc& d) -> const float* {
+    const bool sh = d.e >= p.E;
+    const float* bb = sh ? p.bsh : p.bias;
+    return bb == nullptr ? nullptr : bb + (size_t)(sh ? d.e - p.E : d.e) * rows_w;
+  };
+  // rows behind the lane's activation loads (slot sl = wave NA + a: block kk = sl /
+  // AQ, rows 8 (sl % AQ) + lane / 8; sl >= KPS AQ: a spare load of row 0)
+  auto a_row = [&](int a) {
+    const int sl = wave * NA + a;
+    return ((sl < KPS * AQ) ? sl % AQ : 0) * 8 + (lane >> 3);
+  };
+  auto a_live = [&](int a) { return wave * NA + a < KPS * AQ; };
+  const int s_row = wave * 64 + lane;
+  const bool s_live = wave < NSQ && s_row < MT;
+  int aslot[NA], akk[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a) {
+    const int sl = wave * NA + a;
+    aslot[a] = (sl < KPS * AQ) ? sl : KPS * AQ;
+    akk[a] = (sl < KPS * AQ) ? sl / AQ : 0;
+  }
+  const int sslot = wave < NSQ ? wave : NSQ;
+  auto sources = [&](const ItemDesc& d, const long (&ta)[NA], long tsc) {
+    MxSrc<NA> s;
+    const bool sh = d.e >= p.E;
+    const int ej = sh ? d.e - p.E : d.e;
+    s.wb = (sh ? p.wsh : p.w) + (size_t)ej * rows_w * wrow_bytes;
+    s.wsb = (sh ? p.wssh : p.ws) + (size_t)ej * rows_w * KS;
+    // weight load i: rows 8 (i & 1) + l / 8 of column tile i / 2, stored chunk l % 8
+    // = logical chunk swz(row, l % 8) of the row's 128-byte segment
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int rr = (i & 1) * 8 + (lane >> 3);
-      boff[i] = (uint32_t)wrow_of(i >> 1, rr) * (uint32_t)wrow_bytes + (uint32_t)swz(rr, lane & 7) * 16;
+      s.boff[i] = (uint32_t)wrow_of(d, i >> 1, rr) * (uint32_t)wrow_bytes + (uint32_t)swz(rr, lane & 7) * 16;
     }
     // weight scale dword of row (j = l / 16, r = l % 16): byte offset of the row
-    const uint32_t bsoff = (uint32_t)wrow_of(lane >> 4, lane & 15) * (uint32_t)KS;
-    // activation load a of the wave: slot s = wave NA + a (s >= KPS AQ: a spare load
-    // of row 0 into slot KPS AQ); rows without a source read row 0 (never stored)
-    const uint8_t* aptr[NA];
-    int aslot[NA], akk[NA];
+    s.bsoff = (uint32_t)wrow_of(d, lane >> 4, lane & 15) * (uint32_t)KS;
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
-      const int sl = wave * NA + a;
-      const int q = (sl < KPS * AQ) ? sl % AQ : 0;
-      const int r = q * 8 + (lane >> 3);
-      long src = 0;
-      if (sl < KPS * AQ && sSrc[r] >= 0) src = sSrc[r];
-      aslot[a] = (sl < KPS * AQ) ? sl : KPS * AQ;
-      akk[a] = (sl < KPS * AQ) ? sl / AQ : 0;
-      aptr[a] = p.a + (size_t)src * Kdim + swz(r, lane & 7) * 16;
+      const long src = (a_live(a) && ta[a] >= 0) ? ta[a] : 0;  // no source: row 0, never stored
+      s.aptr[a] = p.a + (size_t)src * Kdim + swz(a_row(a), lane & 7) * 16;
     }
-    long ssrc = 0;
-    {
-      const int r = wave * 64 + lane;
-      if (wave < NSQ && r < MT && sSrc[r] >= 0) ssrc = sSrc[r];
-    }
-    const uint8_t* asp = p.as + (size_t)ssrc * KS;
-    const int sslot = wave < NSQ ? wave : NSQ;
-
-    // Loads of stage t (K blocks [KPS t, KPS t + KPS)).
-    auto issue = [&](Stage& S, int t) {
-      const size_t kb0 = (size_t)t * KPS;
+    s.asp = p.as + (size_t)(tsc >= 0 ? tsc : 0) * KS;
+    return s;
+  };
+  // Loads of stage t (K blocks [KPS t, KPS t + KPS)).
+  auto issue = [&](const MxSrc<NA>& s, Stage& S, int t) {
+    const size_t kb0 = (size_t)t * KPS;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) load_lds16(wb + boff[i] + (size_t)t * 128, &S.b[wave][i * 1024]);
-      if constexpr (!TBL) {
-#pragma unroll
-        for (int kk = 0; kk < KPS; ++kk)
-          load_lds4(wsb + bsoff + (kb0 + kk) * 4, (uint8_t*)&S.bs[wave][kk][0]);
-      }
-#pragma unroll
-      for (int a = 0; a < NA; ++a)
-        load_lds16(aptr[a] + (kb0 + akk[a]) * 128, &S.a[aslot[a]][0]);
+    for (int i = 0; i < 8; ++i) load_lds16(s.wb + s.boff[i] + (size_t)t * 128, &S.b[wave][i * 1024]);
+    if constexpr (!TBL) {
 #pragma unroll
       for (int kk = 0; kk < KPS; ++kk)
-        load_lds4(asp + (kb0 + kk) * 4, (uint8_t*)&S.as[kk][sslot][0]);
-    };
+        load_lds4(s.wsb + s.bsoff + (kb0 + kk) * 4, (uint8_t*)&S.bs[TBL ? 0 : wave][kk][0]);
+    }
+#pragma unroll
+    for (int a = 0; a < NA; ++a) load_lds16(s.aptr[a] + (kb0 + akk[a]) * 128, &S.a[aslot[a]][0]);
+#pragma unroll
+    for (int kk = 0; kk < KPS; ++kk) load_lds4(s.asp + (kb0 + kk) * 4, (uint8_t*)&S.as[kk][sslot][0]);
+  };
+  // The item's weight scale table (this wave's 64 rows): LDS chunk c = 64 i + lane
+  // of the wave's region is stored chunk c % 8 of row c / 8 and holds the row's
+  // scale bytes [16 pc, +16), pc = (c % 8) ^ (row % 8), so the 16 rows of a
+  // fragment read spread over the LDS banks (KS <= 128 and KS % 16 == 0, checked
+  // at launch; pieces past KS re-read piece 0 and are never read back).
+  auto load_table = [&](const ItemDesc& d, const MxSrc<NA>& s) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = 64 * i + lane, row = c >> 3, pc = (c & 7) ^ (row & 7);
+      const int off = (16 * pc < KS) ? 16 * pc : 0;
+      load_lds16(s.wsb + (size_t)wrow_of(d, row >> 4, row & 15) * KS + off, sTbl + wave * 8192 + i * 1024);
+    }
+  };
+  // bias of the lane's four weight rows (column tile j, row r16), loaded with
+  // gload_i32: the epilogue's use must not make the compiler wait for the ring's
+  // loads. The caller makes the loads complete (a wait) before bias_ready.
+  auto bias_issue = [&](const ItemDesc& d, int (&b)[4]) {
+    const float* bb = bias_ptr(d);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = bb != nullptr ? gload_i32(bb + wrow_of(d, j, r16)) : 0;
+  };
+  auto bias_ready = [&](int (&b)[4], float (&f)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      vm_ready(b[j]);
+      f[j] = __int_as_float(b[j]);
+    }
+  };
+
+  // ---- first item: plain loads, its tables, the ring's first stages
+  ItemDesc cd = desc(wi);
+  MxSrc<NA> cs;
+  float cbias[4];
+  {
+    long ta[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) ta[a] = a_live(a) ? row_src(cd, a_row(a), tp_read(cd, a_row(a))) : -1;
+    const long tsc = s_live ? row_src(cd, s_row, tp_read(cd, s_row)) : -1;
+    if (tid < MT) sSrc[0][tid] = row_src(cd, tid, tp_read(cd, tid));
+    cs = sources(cd, ta, tsc);
+  }
+  int cbi[4];
+  bias_issue(cd, cbi);
+  __syncthreads();  // the first item's token table (and its bias loads: vmcnt 0)
+  bias_ready(cbi, cbias);
+  if constexpr (TBL) load_table(cd, cs);
+#pragma unroll
+  for (int i = 0; i < PD - 1; ++i) issue(cs, st[i], min(i, NSTG - 1));
+
+  const int fr = (r16 >> 3) * 1024 + (r16 & 7) * 128;
+  auto cat = [](const v4i& lo, const v4i& hi) -> v8i {
+    return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  };
+
+  int sc = 0;   // ring stage of the stage being multiplied
+  int par = 0;  // parity of the current item's token table
+  for (;;) {
+    const int wn = wi + G;
+    const bool has_next = wn < total;
+    const bool xfer = stream && has_next;  // the ring runs into the next item
+    ItemDesc nd = cd;
+    MxSrc<NA> ns = cs;
+    float nbias[4] = {0.f, 0.f, 0.f, 0.f};
+    int mta[NA], mts = 0, mte = 0, mbi[4] = {0, 0, 0, 0};
+    if (xfer) nd = desc(wn);
+    const float* nbp = xfer ? bias_ptr(nd) : nullptr;
 
     v4f acc[MS][4];
 #pragma unroll
@@ -315,17 +428,57 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[ms][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    const int fr = (r16 >> 3) * 1024 + (r16 & 7) * 128;
-    auto cat = [](const v4i& lo, const v4i& hi) -> v8i {
-      return (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-    };
-    auto step = [&](int t, Stage& cur, Stage& nxt) {
+    for (int t = 0; t < NSTG; ++t) {
       __builtin_amdgcn_sched_barrier(0);
       wait_vm<(PD - 2) * NV>();      // this wave's share of stage t has landed
       __builtin_amdgcn_s_barrier();  // ... every wave's, and stage t - 1 is consumed
       __builtin_amdgcn_sched_barrier(0);
-      issue(nxt, min(t + PD - 1, NSTG - 1));
+      if (xfer && t == 0) {
+        // the next item's token ids and biases, ahead of this step's loads
+#pragma unroll
+        for (int a = 0; a < NA; ++a) mta[a] = KIND == 0 ? gload_i32(tp_ptr(nd, a_row(a))) : 0;
+        if (KIND == 0) {
+          mts = gload_i32(tp_ptr(nd, s_row));
+          mte = gload_i32(tp_ptr(nd, tid));
+        }
+        if (nbp != nullptr) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) mbi[j] = gload_i32(nbp + wrow_of(nd, j, r16));
+        }
+      }
+      const int kn = t + PD - 1;  // stage the ring loads now
+      Stage& nxt = st[sc == 0 ? PD - 1 : sc - 1];
+      // with the table and three stages, the ring's second stage of the next item
+      // waits until after this item's last multiply (see above)
+      const bool defer = TBL && PD == 3 && xfer && kn == NSTG + 1;
+      if (kn < NSTG) {
+        issue(cs, nxt, kn);
+      } else if (xfer) {
+        if (kn == NSTG) {
+          // the next item's sources and token table (its token loads have landed:
+          // at least one step's wait has passed since they were issued)
+          long nta[NA];
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            vm_ready(mta[a]);
+            nta[a] = a_live(a) ? row_src(nd, a_row(a), mta[a]) : -1;
+          }
+          vm_ready(mts);
+          vm_ready(mte);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            vm_ready(mbi[j]);
+            nbias[j] = nbp != nullptr ? __int_as_float(mbi[j]) : 0.f;
+          }
+          ns = sources(nd, nta, s_live ? row_src(nd, s_row, mts) : -1);
+          if (tid < MT) sSrc[par ^ 1][tid] = row_src(nd, tid, mte);
+        }
+        if (!defer) issue(ns, nxt, min(kn - NSTG, NSTG - 1));
+      } else {
+        issue(cs, nxt, NSTG - 1);  // keeps the counts exact; lands in a stage not read again
+      }
       __builtin_amdgcn_sched_barrier(0);
+      Stage& cur = st[sc];
       const uint32_t bw = lds_addr(&cur.b[wave][0]);
 #pragma unroll
       for (int kk = 0; kk < KPS; ++kk) {
@@ -373,51 +526,25 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-    };
-    wait_vm<0>();  // no earlier load is still landing in a stage buffer
-    if constexpr (TBL) {
-      // the item's weight scale table: LDS chunk c = 64 i + lane of the wave's
-      // region is stored chunk c % 8 of row c / 8 and holds the row's scale bytes
-      // [16 pc, +16), pc = (c % 8) ^ (row % 8), so the 16 rows of a fragment read
-      // spread over the LDS banks (KS <= 128 and KS % 16 == 0, checked at launch;
-      // pieces past KS re-read piece 0 and are never read back). The first step's
-      // wait covers these loads, which precede the ring's.
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int c = 64 * i + lane, row = c >> 3, pc = (c & 7) ^ (row & 7);
-        const int off = (16 * pc < KS) ? 16 * pc : 0;
-        load_lds16(wsb + (size_t)wrow_of(row >> 4, row & 15) * KS + off, sTbl + wave * 8192 + i * 1024);
-      }
+      sc = (sc == PD - 1) ? 0 : sc + 1;
     }
-    issue(st0, 0);
-    if (PD >= 3) issue(st1, min(1, NSTG - 1));
-    for (int t = 0; t < NSTG; t += PD) {
-      if (PD == 2) {
-        step(t, st0, st1);
-        if (t + 1 < NSTG) step(t + 1, st1, st0);
-      } else {
-        step(t, st0, st2);
-        if (t + 1 < NSTG) step(t + 1, st1, st0);
-        if (t + 2 < NSTG) step(t + 2, st2, st1);
-      }
+    if (xfer && TBL) {
+      // this wave has read its table rows for the last time in this item
+      load_table(nd, ns);
+      // the deferred second stage of the next item: global step s_last + 2, whose
+      // ring stage is (sc + 1) % 3 now that sc has moved past the last step
+      if (PD == 3) issue(ns, st[sc == PD - 1 ? 0 : sc + 1], min(1, NSTG - 1));
     }
-    wait_vm<0>();  // the tail's repeated loads land before the stages are reused
 
+    // Epilogue. Accumulator layout: lane l, register i holds D[4 * (l / 16) + i][l % 16]
+    // (row of the tile, weight row of the fragment).
+    const long row0 = cd.row0;
+    const int nt = cd.nt;
     int wrow[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wrow[j] = wrow_of(j, r16);
-    // Accumulator layout: lane l, register i holds D[4 * (l / 16) + i][l % 16]
-    // (row of the tile, weight row of the fragment).
+    for (int j = 0; j < 4; ++j) wrow[j] = wrow_of(cd, j, r16);
     if (KIND == 0) {
       const int GI = p.I / 32;
-      float bgate[2] = {0.f, 0.f}, bup[2] = {0.f, 0.f};
-      if (bb != nullptr) {
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          bgate[jj] = bb[wrow[jj]];
-          bup[jj] = bb[wrow[jj + 2]];
-        }
-      }
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
@@ -425,8 +552,8 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
           float m = 0.f;
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) {
-            const float gt = fminf(fmaxf(acc[ms][jj][i] + bgate[jj], p.gate_lo), p.gate_hi);
-            const float up = fminf(fmaxf(acc[ms][jj + 2][i] + bup[jj], p.up_lo), p.up_hi);
+            const float gt = fminf(fmaxf(acc[ms][jj][i] + cbias[jj], p.gate_lo), p.gate_hi);
+            const float up = fminf(fmaxf(acc[ms][jj + 2][i] + cbias[jj + 2], p.up_lo), p.up_hi);
             const float h = mx_act(gt, p.act) * up;
             acc[ms][jj][i] = h;
             m = fmaxf(m, fabsf(h));
@@ -435,7 +562,7 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
           m = group16_max_f32(m);
           const int row = ms * 16 + 4 * g + i;
           const int ex = mx_exponent(m);
-          if (sSrc[row] >= 0) {
+          if (sSrc[par][row] >= 0) {
             const float f = mx_inv_scale(ex);
             const uint32_t c2 = mx_e4m3x2(acc[ms][0][i], acc[ms][1][i], f);
             uint8_t* const hrow = p.hq + (size_t)(row0 + row) * p.I + nt * 128 + wave * 32 + r16;
@@ -446,27 +573,50 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
         }
       }
     } else {
-      float bd[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bb != nullptr) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bd[j] = bb[wrow[j]];
-      }
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int row = ms * 16 + 4 * g + i;
-          if (row < nrows) {
+          if (row < cd.nrows) {
             const long yrow = row0 + row;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-              p.y[(size_t)yrow * p.H + wrow[j]] = (uint16_t)bf16x2(acc[ms][j][i] + bd[j], 0.f);
+              p.y[(size_t)yrow * p.H + wrow[j]] = (uint16_t)bf16x2(acc[ms][j][i] + cbias[j], 0.f);
           }
         }
       }
     }
-    __syncthreads();
+
+    if (!has_next) break;
+    wi = wn;
+    par ^= 1;
+    if (xfer) {
+      cd = nd;
+      cs = ns;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) cbias[j] = nbias[j];
+    } else {
+      // drain mode: the ring's tail loads land, then the next item starts afresh
+      wait_vm<0>();
+      __syncthreads();
+      cd = desc(wi);
+      long ta[NA];
+#pragma unroll
+      for (int a = 0; a < NA; ++a) ta[a] = a_live(a) ? row_src(cd, a_row(a), tp_read(cd, a_row(a))) : -1;
+      const long tsc = s_live ? row_src(cd, s_row, tp_read(cd, s_row)) : -1;
+      if (tid < MT) sSrc[par][tid] = row_src(cd, tid, tp_read(cd, tid));
+      cs = sources(cd, ta, tsc);
+      bias_issue(cd, cbi);
+      __syncthreads();  // (and the bias loads: vmcnt 0)
+      bias_ready(cbi, cbias);
+      if constexpr (TBL) load_table(cd, cs);
+      sc = 0;
+#pragma unroll
+      for (int i = 0; i < PD - 1; ++i) issue(cs, st[i], min(i, NSTG - 1));
+    }
   }
+  wait_vm<0>();  // no load is still landing in LDS when the workgroup ends
 }
 
 // MXFP8 quantization of bf16 rows: lane q of a 4-lane group holds 8 consecutive
@@ -518,7 +668,9 @@ template <int KIND, int WFMT>
 static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
   const int NT = (KIND == 0) ? a.I / 128 : a.H / 256;
   const long items = (long)max_tiles * NT;
-  const int grid = (int)std::max(1L, std::min(items, 4096L));
+  // one persistent workgroup per CU (the ring's LDS allows one), each running
+  // every G-th work item
+  const int grid = (int)std::max(1L, std::min(items, (long)device_cu_count()));
   // the per-item scale table for K <= 4096 in whole 16-byte pieces per row
   // (K % 512 == 0), and for the tiles whose LDS has room
   const int Kdim = (KIND == 0) ? a.H : a.I;

@@ -34,6 +34,22 @@ int router_logits_topk(const void* x_bf16, const void* w_bf16, const float* bias
 // Rows per tile of the 256x256 expert GEMM kernels.
 constexpr int kBlockTileRows = 256;
 
+// Compute units of the current device (cached per device; 256 on MI355X), for
+// persistent grids of one workgroup per CU.
+inline int device_cu_count() {
+  constexpr int kMaxDev = 64;
+  static int cached[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 256;
+  int n = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    __atomic_store_n(&cached[dev], n, __ATOMIC_RELAXED);
+  }
+  return n;
+}
+
 // Tile list written by the mapping's scan kernel from the expert counts
 // (tiles == nullptr: none). Row tiles stay inside one block; block tiles
 // (span = 1) run across an expert's blocks and carry seg = (first tile of the
