@@ -50,7 +50,10 @@ constexpr int kBlkThreads = 512;
 constexpr int kStageA = kBM * kBK;  // 32 KB
 constexpr int kStageB = kBN * kBK;  // 32 KB
 constexpr int kDmaPerWave = (kStageA + kStageB) / 1024 / 8;  // 8 x 1 KB regions per wave
-constexpr int kStageSA = 2 * kBM * 4;  // activation scales of the stage's block, one copy per column half
+// Activation scales: two buffers x two copies (one per column half) x 256 rows x
+// four K blocks (fp32); every fourth step one 16-byte load per row brings the
+// next four blocks' scales.
+constexpr int kStageSA = 2 * 2 * kBM * 16;
 constexpr int kMaxKB = 128;  // K <= 16384
 
 struct BlkArgs {
@@ -83,6 +86,7 @@ struct BlkLds {
   uint8_t* ta;                     // A tile of the current block (one stage)
   uint8_t *tb0, *tb1, *tb2;        // B tiles: three-stage ring
   uint8_t* sa;                     // A scales (loaded two blocks ahead), one copy per column half
+  uint8_t* dummy;                  // 256 bytes per wave for loads that only keep the count
   float *r0, *r1;                  // scale ratios per (half, row) of even / odd blocks
   float* last;                     // last block scale per (half, row)
   int* src;                        // token (gate_up) or slot (down) of each tile row
@@ -178,6 +182,7 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   uint8_t* const sTB1 = s.tb1;
   uint8_t* const sTB2 = s.tb2;
   uint8_t* const sSA = s.sa;
+  uint8_t* const sDummy = s.dummy;
   float* const sR0 = s.r0;
   float* const sR1 = s.r1;
   float* const sLast = s.last;
@@ -235,7 +240,16 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
 #pragma unroll
   for (int i = 4; i < kDmaPerWave; ++i) load_lds16(wb + off[i], sTB0 + (4 * wave + i - 4) * 1024);
   const int srow = 64 * wm + lane, shalf = wn;  // the scale writer's row and half (below)
-  const int sa_dst = (wn * kBM + 64 * wm) * 4;
+  // Activation scale buffers. For gate_up with K blocks in multiples of four
+  // (sgrp), buffer (g & 1) holds blocks [4g, 4g + 4) as [half][row][4] fp32, loaded
+  // by one 16-byte load per row (gathered token rows: one 4-byte load per row and
+  // block makes every instruction touch 64 lines); otherwise (down's rows are
+  // consecutive) buffer (kb & 1) holds block kb as [half][row] fp32. Wave (wm, wn)
+  // fills rows 64 wm + lane of copy wn.
+  const bool sgrp = KIND == 0 && (KB & 3) == 0;
+  auto sa_dst_of = [&](int buf) -> uint8_t* {
+    return sSA + ((buf * 2 + wn) * kBM + 64 * wm) * (sgrp ? 16 : 4);
+  };
   if constexpr (KIND == 1) {
     // down: tile row r is h row rbase + r, so block 0's A tile and scales need no
     // lookup and join the first round trip
@@ -247,7 +261,10 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
       load_lds16(p.a + off[i], sTA + (4 * wave + i) * 1024);
     }
     const uint32_t rs = (uint32_t)(srow < nrows ? rbase + srow : rbase);
-    load_lds4((const uint8_t*)p.as + rs * (uint32_t)(KB * 4), sSA + sa_dst);
+    if (sgrp)
+      load_lds16((const uint8_t*)p.as + rs * (uint32_t)(KB * 4), sa_dst_of(0));
+    else
+      load_lds4((const uint8_t*)p.as + rs * (uint32_t)(KB * 4), sa_dst_of(0));
   }
   __builtin_amdgcn_sched_barrier(0);
   const int whf = tid < KB ? 0 : 1, wkb = min(tid, 2 * KB - 1) - whf * KB;
@@ -283,7 +300,11 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   const bool svalid = ssrc >= 0;
   // Byte offsets of operand rows fit 32 bits: the entry points reject larger operands.
   const uint32_t off_sa = (uint32_t)(svalid ? ssrc : 0) * (uint32_t)(KB * 4);
-  const uint32_t sa_own = lds_addr(sSA) + (uint32_t)((shalf * kBM + srow) * 4);
+  // the writer's own scale of block kb (its own wave loaded it)
+  auto sa_own = [&](int kb) -> uint32_t {
+    return sgrp ? lds_addr(sSA) + (uint32_t)((((((kb >> 2) & 1) * 2 + shalf) * kBM + srow) * 16) + (kb & 3) * 4)
+                : lds_addr(sSA) + (uint32_t)((((kb & 1) * 2 + shalf) * kBM + srow) * 4);
+  };
   float s_prev = 0.f;
   auto ratio = [&](float sa, float sw) {
     float s = svalid ? sa * sw : 1.f;
@@ -305,12 +326,20 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
     for (int i = 0; i < kAGroup; ++i)
       load_lds16(abase + off[i] + (size_t)kb * kBK, sTA + (4 * wave + i) * 1024);
   };
-  // Load i of block kb's B group into stage sb (i = 0: the scales).
+  // Load i of block kb's B group into stage sb (i = 0: the scales; grouped, only
+  // at a group's first block, otherwise a 4-byte load of one line into the
+  // wave's dummy area so every group has the same count).
   auto issue_b = [&](uint8_t* sb, int i, int kb) {
-    if (i == 0)
-      load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, sSA + sa_dst);
-    else
+    if (i == 0) {
+      if (!sgrp)
+        load_lds4((const uint8_t*)p.as + off_sa + (size_t)kb * 4, sa_dst_of(kb & 1));
+      else if ((kb & 3) == 0)
+        load_lds16((const uint8_t*)p.as + off_sa + (size_t)kb * 4, sa_dst_of((kb >> 2) & 1));
+      else
+        load_lds4((const uint8_t*)p.as, sDummy + wave * 256);
+    } else {
       load_lds16(wb + off[3 + i] + (size_t)kb * kBK, sb + (4 * wave + i - 1) * 1024);
+    }
   };
 
   // Accumulators: MF row tiles (16 rows) x 8 column tiles (16 columns).
@@ -377,7 +406,7 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
 
   // Ratios of block kb + 1 (scales of block kb + 1 landed) into sr.
   auto store_ratio = [&](float* sr, int kb) {
-    (shalf ? sr + kBM : sr)[srow] = ratio(lds_f32(sa_own), sW[shalf][kb]);
+    (shalf ? sr + kBM : sr)[srow] = ratio(lds_f32(sa_own(kb)), sW[shalf][kb]);
   };
 
   // One K step: the MFMAs of block kb (B tile in stage cb, ratios in cr). On entry
@@ -549,13 +578,14 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   __shared__ __attribute__((aligned(16))) uint8_t sTB1[kStageB];
   __shared__ __attribute__((aligned(16))) uint8_t sTB2[kStageB];
   __shared__ __attribute__((aligned(16))) uint8_t sSA[kStageSA];
+  __shared__ __attribute__((aligned(16))) uint8_t sDummy[8 * 256];
   __shared__ __attribute__((aligned(16))) float sR0[2 * kBM];
   __shared__ __attribute__((aligned(16))) float sR1[2 * kBM];
   __shared__ __attribute__((aligned(16))) float sLast[2 * kBM];
   __shared__ int sSrc[kBM];
   __shared__ float sRed[2][kBM];
   __shared__ float sW[2][kMaxKB];
-  const BlkLds s{sTA, sTB0, sTB1, sTB2, sSA, sR0, sR1, sLast, sSrc, sRed, sW};
+  const BlkLds s{sTA, sTB0, sTB1, sTB2, sSA, sDummy, sR0, sR1, sLast, sSrc, sRed, sW};
 
   // XCD-aware item index: workgroup b runs on XCD b % 8; XCD x takes the
   // contiguous item range [x * per, (x + 1) * per).
