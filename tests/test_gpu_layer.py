@@ -340,6 +340,19 @@ def test_layer_block_kernels(cuda, T, E, K, S):
     assert rel_l2(np_f32(out), np_f32(alt)) < 5e-3
 
 
+def test_block_kernels_k_blocks_not_multiple_of_four(cuda):
+    """Block kernels with H = 768 (6 K blocks for gate_up: the activation scales load
+    one block per step, not four) and I = 384 (3 K blocks for down), against the
+    oracle."""
+    cfg = MoEConfig(768, 384, 4, 2, n_shared=1, scoring="sigmoid", routed_scaling=1.0)
+    T = 1024
+    say("block kernels K blocks", cfg.hidden, cfg.intermediate)
+    assert ops.use_block_kernels(T, cfg.top_k, cfg.n_experts)
+    w = synthetic.make_weights(cfg, 77, device=cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, 77).to(cuda)
+    _check_layer(cfg, w, x, tag="block K blocks")
+
+
 def test_block_kernels_every_tile_height(cuda):
     """Block kernels on fixed expert counts whose tiles cover every row-group size
     (1-64, 65-128, 129-192 and 193-256 rows, full 256-row tiles before each

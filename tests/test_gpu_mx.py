@@ -153,6 +153,35 @@ def test_mx_experts_match_oracle(cuda, fmt, act, T, E, K):
     assert err <= TOL_REL_L2, err
 
 
+@pytest.mark.parametrize("fmt,T,E,K,H,I", [
+    ("fp4", 64, 64, 2, 1024, 2048),    # 16-row tiles, 3-stage ring, scale table, ~1000 items
+    ("fp4", 128, 16, 2, 1024, 2048),   # 32-row tiles, 2-stage ring, scale table
+    ("fp4", 2048, 8, 2, 1024, 2048),   # 64-row tiles, 2-stage ring, scale table
+    ("fp4", 4096, 8, 2, 4608, 512),    # gate_up K > 4096: per-stage scale loads
+    ("fp4", 2048, 8, 2, 4096, 256),    # down K = 256: fewer stages than the ring (drain)
+    ("fp8", 64, 64, 2, 1024, 1024)])   # MXFP8 weights: one K block per stage
+def test_mx_experts_persistent_grid(cuda, fmt, T, E, K, H, I):
+    """Shapes with more work items than CUs, so each persistent workgroup runs several
+    items and its load ring crosses from item to item (or drains between them when K
+    has fewer stages than the ring), with and without the per-item scale table."""
+    say("mx persistent", fmt, T, E, K, H, I)
+    w = make_mx_weights(E, H, I, 11 + T, cuda, fmt)
+    g = torch.Generator().manual_seed(3 * T + E)
+    x = (torch.randn(T, H, generator=g) * 2).to(torch.bfloat16).to(cuda)
+    ids = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    wts = torch.rand(T, K, generator=g)
+    gl, ul = (None, LIMIT), (1 - LIMIT, 1 + LIMIT)
+    out = ops.mx_experts(x, ids.to(cuda), wts.to(cuda), w, "swish", gl, ul)
+    ref = oracle_layer(x, ids.numpy(), wts.numpy(), w, "swish", gl, ul)
+    err = rel_l2(np_f32(out), ref)
+    say("rel_l2", err)
+    assert err <= TOL_REL_L2, err
+    # run to run the same bits
+    assert torch.equal(out, ops.mx_experts(x, ids.to(cuda), wts.to(cuda), w, "swish", gl, ul))
+    del w
+    torch.cuda.empty_cache()
+
+
 # ---------------------------------------------------------------- GPT-OSS-120B layer
 
 GPT_OSS = dict(E=128, H=3072, I=3072, h_real=2880, i_real=2880, K=4)   # hidden 2880 padded to 3072
