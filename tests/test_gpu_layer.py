@@ -121,13 +121,16 @@ def test_layer_row_tile_heights_agree(cuda):
     assert rel_l2(np_f32(ref), np_f32(outs[0])) < 5e-3
 
 
-@pytest.mark.parametrize("T,E", [(64, 64), (4096, 128), (1, 384), (7, 1024)])
+@pytest.mark.parametrize("T,E", [(64, 64), (4096, 128), (1, 384), (7, 1024), (100, 256),
+                                 (255, 384), (300, 256)])
 def test_layer_router_matches_op_path(cuda, T, E):
     """Inside the layer the top-k kernel sums the router's split-K partials itself (28
-    partials at 64 tokens and below; 8 from the 128-token wide tiles at 4096), a
-    workgroup's four tokens at a time (one token at T = 1, three in the last workgroup
-    at T = 7). Logits, ids and weights equal, bit for bit, those of ops.router_logits
-    (reduce kernel) followed by ops.router_topk."""
+    partials at 64 tokens and below; 8 from the 128-token wide tiles at 4096). Up to 256
+    tokens and 512 experts the top-k launch also builds the mapping (its last workgroup),
+    with one token per workgroup up to 64 tokens and ceil(T / 64) above (two at T = 100,
+    four at T = 255, three in the last workgroup); otherwise four tokens per workgroup
+    (T = 7 with 1024 experts: three in the last; T = 300). Logits, ids and weights equal,
+    bit for bit, those of ops.router_logits (reduce kernel) followed by ops.router_topk."""
     cfg = PRESETS["dsv3"].with_(n_experts=E, intermediate=128, n_group=8, topk_group=4)
     say("layer router vs op path", T, E)
     w = synthetic.make_weights(cfg, 30 + E, device=cuda)
@@ -137,6 +140,8 @@ def test_layer_router_matches_op_path(cuda, T, E):
     ids2, wts2 = ops.router_topk(lg2, cfg.top_k, ops.ORDER_GROUPED, cfg.scoring, cfg.n_group,
                                  cfg.topk_group, w.corr_bias, cfg.renorm, 1e-20, cfg.routed_scaling)
     assert torch.equal(lg, lg2) and torch.equal(ids, ids2) and torch.equal(wts, wts2)
+    if T in (100, 255):  # the mapping built by the top-k launch's last workgroup
+        _check_layer(cfg, w, x, tag=f"router op path T={T} E={E}")
 
 
 def test_layer_deterministic_and_module_api(cuda):

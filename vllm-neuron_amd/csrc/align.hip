@@ -16,71 +16,9 @@
 //                  expert_counts, block_to_expert and conditions.
 //  3. map_scatter: rebuilds the chunk bitmask; the rank of t inside its chunk
 //                  is a popcount of the bits below it; writes the slots.
-#include "moe_common.h"
-#include "moe_internal.h"
+#include "mapping.h"
 
 namespace moe {
-
-constexpr int kChunk = 256;    // tokens per chunk (256 bits = 8 words per expert)
-constexpr int kMapMaxE = 1024;  // LDS bitmask capacity
-
-struct MapWs {
-  int32_t* status;       // [4]: dropped pairs at [0]
-  int32_t* chunk_counts;  // [nchunks, E]
-  int32_t* chunk_base;    // [nchunks, E]
-  int32_t* block_off;     // [E]
-  int32_t* count_off;     // [E] exclusive prefix of the counts (compact rows)
-};
-
-static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-static inline MapWs carve_map_ws(void* ws, int T, int E) {
-  int nch = (T + kChunk - 1) / kChunk;
-  char* p = (char*)ws;
-  MapWs m;
-  m.status = (int32_t*)p;
-  p += 256;
-  m.chunk_counts = (int32_t*)p;
-  p += align256((size_t)nch * E * 4);
-  m.chunk_base = (int32_t*)p;
-  p += align256((size_t)nch * E * 4);
-  m.block_off = (int32_t*)p;
-  p += align256((size_t)E * 4);
-  m.count_off = (int32_t*)p;
-  return m;
-}
-
-static inline size_t map_ws_bytes(int T, int E) {
-  int nch = (T + kChunk - 1) / kChunk;
-  return 256 + 2 * align256((size_t)nch * E * 4) + 2 * align256((size_t)E * 4);
-}
-
-__device__ __forceinline__ void build_chunk_mask(uint32_t (*bm)[8], const int32_t* ids,
-                                                 const float* aff, int T, int K, int E, int t0,
-                                                 int32_t* status) {
-  for (int i = threadIdx.x; i < E * 8; i += blockDim.x) bm[i >> 3][i & 7] = 0u;
-  __syncthreads();
-  if (ids != nullptr) {
-    for (int i = threadIdx.x; i < kChunk * K; i += blockDim.x) {
-      int tl = i / K, t = t0 + tl;
-      if (t >= T) break;
-      int e = ids[(size_t)t * K + (i - tl * K)];
-      if (e >= 0 && e < E) {
-        atomicOr(&bm[e][tl >> 5], 1u << (tl & 31));
-      } else if (e >= E && status != nullptr) {
-        atomicAdd(status, 1);
-      }
-    }
-  } else {
-    for (int i = threadIdx.x; i < kChunk * E; i += blockDim.x) {
-      int tl = i / E, t = t0 + tl;
-      if (t >= T) break;
-      int e = i - tl * E;
-      if (aff[(size_t)t * E + e] != 0.f) atomicOr(&bm[e][tl >> 5], 1u << (tl & 31));
-    }
-  }
-  __syncthreads();
-}
 
 __global__ __launch_bounds__(256) void map_count_kernel(
     const int32_t* __restrict__ ids, const float* __restrict__ aff,
@@ -111,119 +49,6 @@ __global__ __launch_bounds__(256) void map_count_kernel(
     for (int w = 0; w < 8; ++w) c += __popc(bm[e][w]);
     ws.chunk_counts[(size_t)chunk * E + e] = c;
   }
-}
-
-// Inclusive sum over the 1024 threads of a workgroup (wave scans, then the
-// 16 wave totals); s_wave holds 16 ints.
-__device__ __forceinline__ int block_inclusive_sum(int v, int* s_wave) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
-  if (lane == 63) s_wave[wave] = v;
-  __syncthreads();
-  int add = 0;
-  for (int q = 0; q < wave; ++q) add += s_wave[q];
-  __syncthreads();
-  return v + add;
-}
-
-// Everything after the per-expert counts: block offsets (exclusive scan of
-// ceil(count/B)), expert_counts, block_to_expert, conditions and the optional tile
-// list. Thread tid < E holds run = count of expert tid. Leaves the inclusive
-// block scan in s_blk, the counts in s_cnt and, for compact rows, the exclusive
-// count scan in s_cex (and count_off); 1024 threads.
-__device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __restrict__ expert_counts,
-                               int32_t* __restrict__ block_to_expert, int32_t* __restrict__ conditions,
-                               int32_t* __restrict__ block_off, int32_t* __restrict__ count_off,
-                               const TileOut& to, int* s_blk, int* s_cnt, int* s_cex, int* s_tile,
-                               int* s_wave) {
-  const int tid = threadIdx.x;
-  int blk = 0;
-  if (tid < E) {
-    if (expert_counts != nullptr) expert_counts[tid] = run;
-    blk = (run + B - 1) / B;
-  }
-  const int cum = block_inclusive_sum(blk, s_wave);
-  if (tid < E) {
-    if (block_off != nullptr) block_off[tid] = cum - blk;  // exclusive
-    s_blk[tid] = cum;                                      // inclusive cumulative blocks
-    s_cnt[tid] = run;
-  }
-  if (to.compact) {  // workgroup-uniform
-    const int ccum = block_inclusive_sum(run, s_wave);
-    if (tid < E) {
-      s_cex[tid] = ccum - run;
-      if (count_off != nullptr) count_off[tid] = ccum - run;
-    }
-  }
-  __syncthreads();
-  const int total = s_blk[E - 1];
-  // block_to_expert[b] = #{ e < E-1 : cum[e] <= b }   (cum non-decreasing)
-  for (int b = tid; b < N; b += blockDim.x) {
-    int lo = 0, hi = E - 1;  // search in cum[0 .. E-2]
-    while (lo < hi) {
-      int mid = (lo + hi) >> 1;
-      if (s_blk[mid] <= b) lo = mid + 1;
-      else hi = mid;
-    }
-    block_to_expert[b] = lo;
-    if (conditions != nullptr) conditions[b] = (b < total) ? 1 : 0;
-  }
-  if (to.tiles == nullptr) return;  // workgroup-uniform
-  // Tile list from the counts. Expert e owns slots [off_e*B, off_e*B + c_e),
-  // so its tiles follow without reading token_position_to_id: per block
-  // ceil(rows/mt) tiles (row tiles), or ceil(c_e/mt) tiles running across the
-  // expert's blocks (block tiles, span = 1).
-  const int mt = to.mt, tpb = (B + mt - 1) / mt;
-  int nt = 0;
-  if (tid < E)
-    nt = to.span ? (run + mt - 1) / mt : (run / B) * tpb + (run % B + mt - 1) / mt;
-  const int tcum = block_inclusive_sum(nt, s_wave);
-  if (tid < E) s_tile[tid] = tcum;
-  __syncthreads();
-  const int ntiles = s_tile[E - 1];
-  for (int i = tid; i < ntiles && i < to.max_tiles; i += blockDim.x) {
-    int lo = 0, hi = E - 1;  // first e with s_tile[e] > i
-    while (lo < hi) {
-      int mid = (lo + hi) >> 1;
-      if (s_tile[mid] <= i) lo = mid + 1;
-      else hi = mid;
-    }
-    const int e = lo, first = (e > 0) ? s_tile[e - 1] : 0, loc = i - first;
-    const int c = s_cnt[e];
-    const long base = (long)(s_blk[e] - (c + B - 1) / B) * B;
-    if (to.span) {
-      // the expert's ceil(c / mt) tiles share its rows equally, so sibling tiles
-      // advance through K at the same rate and share each weight block in L2
-      const int ntl = s_tile[e] - first, h = (c + ntl - 1) / ntl;
-      const long in_e = (long)loc * h;  // first slot of the tile, relative to the expert
-      const long row = to.compact ? s_cex[e] + in_e : base + in_e;
-      to.tiles[i] = make_int4(e, (int)(base + in_e), min(h, c - loc * h), (int)row);
-      to.seg[i] = make_int2(first, ntl);
-    } else {
-      const int j = loc / tpb, m = loc - j * tpb;
-      const int rows = min(B, c - j * B);
-      const long in_e = (long)j * B + m * mt;
-      const long row = to.compact ? s_cex[e] + in_e : base + in_e;
-      to.tiles[i] = make_int4(e, (int)(base + in_e), min(mt, rows - m * mt), (int)row);
-    }
-  }
-  const int per = (T + mt - 1) / mt;
-  const int hsh = to.span ? (T + per - 1) / per : mt;  // equal block-tile heights
-  const long nb_total = (long)N * B;
-  const long row_sh = to.compact ? to.row_shared : nb_total;
-  for (int i = tid; i < to.n_shared * per; i += blockDim.x) {
-    const int j = i / per, m = i - j * per, idx = ntiles + i;
-    if (idx < to.max_tiles) {
-      const long in_sh = (long)j * T + (long)m * hsh;
-      to.tiles[idx] = make_int4(E + j, (int)(nb_total + in_sh), min(hsh, T - m * hsh), (int)(row_sh + in_sh));
-      if (to.span) to.seg[idx] = make_int2(ntiles + j * per, per);
-    }
-  }
-  if (tid == 0) to.num_tiles[0] = min(ntiles + to.n_shared * per, to.max_tiles);
 }
 
 __global__ __launch_bounds__(1024) void map_scan_kernel(int T, int E, int B, int N, int nchunks,
@@ -263,43 +88,8 @@ __global__ __launch_bounds__(1024) void map_small_kernel(
   __shared__ int s_cex[kMapMaxE];
   __shared__ int s_tile[kMapMaxE];
   __shared__ int s_wave[16];
-  const int tid = threadIdx.x;
-  const long nb_total = (long)N * B;
-  long filled = 0;
-  if (((uintptr_t)tpid & 15) == 0) {  // 16-byte stores while they fit
-    filled = nb_total & ~3L;
-    for (long i = tid; i < filled / 4; i += blockDim.x) ((int4*)tpid)[i] = make_int4(-1, -1, -1, -1);
-  }
-  for (long i = filled + tid; i < nb_total; i += blockDim.x) tpid[i] = -1;
-  if (tid == 0) ws.status[0] = 0;
-  __syncthreads();  // the fill and the status reset land before the scatter below
-  build_chunk_mask(bm, ids, nullptr, T, K, E, 0, ws.status);
-  int run = 0;
-  if (tid < E) {
-#pragma unroll
-    for (int w = 0; w < 8; ++w) run += __popc(bm[tid][w]);
-  }
-  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off,
-                 nullptr, to, s_blk, s_cnt, s_cex, s_tile, s_wave);
-  for (int i = tid; i < T * K; i += blockDim.x) {
-    const int t = i / K;
-    const int e = ids[i];
-    int out = -1;
-    if (e >= 0 && e < E) {
-      int rank = 0;
-      const int wq = t >> 5;
-      for (int w = 0; w < wq; ++w) rank += __popc(bm[e][w]);
-      rank += __popc(bm[e][wq] & ((1u << (t & 31)) - 1u));
-      const long slot = (long)(s_blk[e] - (s_cnt[e] + B - 1) / B) * B + rank;
-      if (slot < nb_total) {
-        tpid[slot] = t;
-        out = to.compact ? s_cex[e] + rank : (int)slot;
-      } else {
-        atomicAdd(ws.status, 1);
-      }
-    }
-    if (inv_pos != nullptr) inv_pos[i] = out;
-  }
+  map_small_body(ids, T, K, E, B, N, tpid, block_to_expert, conditions, expert_counts, inv_pos, ws,
+                 to, bm, s_blk, s_cnt, s_cex, s_tile, s_wave);
 }
 
 // inv_rows: inv_pos receives compact rows (count_off[e] + rank in the expert)

@@ -139,6 +139,22 @@ extern "C" size_t moe_layer_workspace_bytes(int T, int H, int I, int E, int K, i
   return carve(nullptr, T, H, I, E, K, n_shared, B, norm != 0).bytes;
 }
 
+// RouterFuse for the layer's mapping (no quantization).
+static RouterFuse map_fuse(const LayerWs& w, int B, int N, const TileOut& to) {
+  RouterFuse fz{};
+  fz.B = B;
+  fz.N = N;
+  fz.tpid = w.tpid;
+  fz.b2e = w.b2e;
+  fz.cond = w.cond;
+  fz.counts = w.counts;
+  fz.inv = w.inv;
+  fz.map_ws = w.map_ws;
+  fz.map_ws_bytes = w.map_ws_bytes;
+  fz.to = to;
+  return fz;
+}
+
 // The layer forward of both entry points: `workspace` is the caller's buffer or
 // this device's static scratch. _moe_fn names the entry point in error messages.
 static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const void* residual_bf16,
@@ -196,10 +212,7 @@ static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const voi
                                 residual_out_bf16, w.xq, w.xs, stream));
     xr = w.xn;
   }
-  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
-                              w.router_ws_bytes, corr_bias, K, order, scoring, n_group, topk_group,
-                              renorm, renorm_eps, routed_scale, ids, wts, stream));
-  // The mapping's scan kernel also writes the expert tile list, from the counts.
+  // The mapping also writes the expert tile list, from the counts.
   const bool block = use_block(T, K, E);
   const int mbt = block ? moe_max_block_tiles(T, K, E, N, B, n_shared) : 0;
   TileOut to{};
@@ -219,9 +232,20 @@ static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const voi
   to.n_shared = n_shared;
   to.compact = 1;  // hq / y hold only the routed and shared rows
   to.row_shared = R;
-  MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
-                             w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
-  if (!norm) MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
+  // Decode sizes: the quantization rides in the logits launch and the mapping ends
+  // the top-k launch (router_logits_topk says which it did).
+  RouterFuse fz = map_fuse(w, B, N, to);
+  if (!norm) {
+    fz.xq = w.xq;
+    fz.xs = w.xs;
+  }
+  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+                              w.router_ws_bytes, corr_bias, K, order, scoring, n_group, topk_group,
+                              renorm, renorm_eps, routed_scale, ids, wts, stream, &fz));
+  if (!fz.map_done)
+    MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
+                               w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
+  if (!norm && !fz.quant_done) MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
   if (block) {
     MOE_STEP(moe_expert_gate_up_block(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
                                       w13_shared_scale, n_shared, w.tpid, (int)NB, w.btiles,
@@ -391,9 +415,6 @@ extern "C" int moe_layer_forward_mx(
                                 residual_out_bf16, w.xq, w.xs, stream));
     xr = w.xn;
   }
-  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
-                              w.router_ws_bytes, nullptr, K, order, scoring, 1, 1, renorm,
-                              renorm_eps, routed_scale, ids, wts, stream));
   TileOut to{};
   to.tiles = (int4*)w.tiles;
   to.num_tiles = w.num_tiles;
@@ -401,8 +422,13 @@ extern "C" int moe_layer_forward_mx(
   to.mt = mt;
   to.compact = 1;
   to.row_shared = R;
-  MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
-                             w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
+  RouterFuse fz = map_fuse(w, B, N, to);  // the mapping ends the top-k launch at decode sizes
+  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+                              w.router_ws_bytes, nullptr, K, order, scoring, 1, 1, renorm,
+                              renorm_eps, routed_scale, ids, wts, stream, &fz));
+  if (!fz.map_done)
+    MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
+                               w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
   MOE_STEP(moe_act_quant_mx(xr, T, H, w.xq, xs, stream));
   MOE_STEP(moe_expert_gate_up_mx(w.xq, xs, T, H, I, E, wfmt, w13, w13_scale, b13, nullptr, nullptr,
                                  nullptr, 0, w.tpid, (int)NB, w.tiles, w.num_tiles, max_tiles, mt,

@@ -215,6 +215,36 @@ __device__ __forceinline__ void bf16x8_to_f32(const int4 c, float (&v)[8]) {
   }
 }
 
+// 1x128 quantization of `groups` consecutive bf16 groups (x 16-byte aligned, q
+// 8-byte aligned) by workgroup `blk` of `nblk` equal workgroups: lane l of a wave
+// takes the 16-byte chunk (l & 15) of group 4 * quad + l / 16, so a wave covers
+// four groups per load instruction; each wave keeps U quads of loads in flight.
+__device__ __forceinline__ void act_quant_vec_body(const uint16_t* __restrict__ x, long groups,
+                                                   uint8_t* __restrict__ q, float* __restrict__ s,
+                                                   int blk, int nblk) {
+  constexpr int U = 4;
+  const int lane = threadIdx.x & 63, wpb = blockDim.x >> 6;
+  const long quads = (groups + 3) / 4;
+  const long nwaves = (long)nblk * wpb;
+  for (long q0 = (long)blk * wpb + (threadIdx.x >> 6); q0 < quads; q0 += U * nwaves) {
+    int4 c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long gi = 4 * (q0 + u * nwaves) + (lane >> 4);
+      c[u] = (gi < groups) ? *(const int4*)(x + gi * MOE_GROUP + 8 * (lane & 15)) : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long gi = 4 * (q0 + u * nwaves) + (lane >> 4);  // whole 16-lane segments share gi
+      if (gi < groups) {
+        float v[8];
+        bf16x8_to_f32(c[u], v);
+        quant8_1x128(v, q + gi * MOE_GROUP + 8 * (lane & 15), s + gi, (lane & 15) == 0);
+      }
+    }
+  }
+}
+
 // The same, loading the group from x (bf16, 128 columns).
 __device__ __forceinline__ void quant_group_1x128(const uint16_t* x, uint8_t* q, float* s, int lane) {
   quant_pair_1x128(*(const uint32_t*)(x + 2 * lane), q, s, lane);

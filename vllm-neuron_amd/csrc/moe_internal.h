@@ -22,14 +22,6 @@ inline int router_logits_splits(int T, int H, int E) {
   return (int)std::max(1L, std::min(ks, kmax));
 }
 
-// moe_router_logits followed by moe_router_topk (no affinities output), with the
-// split-K reduce folded into the top-k kernel; for callers that already checked
-// the arguments of both.
-int router_logits_topk(const void* x_bf16, const void* w_bf16, const float* bias, int T, int H,
-                       int E, float* logits, void* workspace, size_t workspace_bytes,
-                       const float* corr_bias, int K, int order, int scoring, int n_group,
-                       int topk_group, int renorm, float renorm_eps, float routed_scale,
-                       int32_t* ids, float* weights, void* stream);
 
 // Rows per tile of the 256x256 expert GEMM kernels.
 constexpr int kBlockTileRows = 256;
@@ -70,6 +62,31 @@ struct TileOut {
   int compact;
   long row_shared;
 };
+
+// Work that router_logits_topk may fold into its launches for the layer: the 1x128
+// quantization of x into xq / xs (when xq is set) and blockwise_mapping of the ids
+// it selects (when tpid is set; ids only, no padding mask, inv_pos = inv, workspace
+// map_ws, tile list `to`). On return quant_done / map_done say which it did; the
+// caller runs the rest itself.
+struct RouterFuse {
+  uint8_t* xq;
+  float* xs;
+  int B, N;
+  int32_t *tpid, *b2e, *cond, *counts, *inv;
+  void* map_ws;
+  size_t map_ws_bytes;
+  TileOut to;
+  bool quant_done, map_done;
+};
+
+// moe_router_logits followed by moe_router_topk (no affinities output), with the
+// split-K reduce folded into the top-k kernel; for callers that already checked
+// the arguments of both.
+int router_logits_topk(const void* x_bf16, const void* w_bf16, const float* bias, int T, int H,
+                       int E, float* logits, void* workspace, size_t workspace_bytes,
+                       const float* corr_bias, int K, int order, int scoring, int n_group,
+                       int topk_group, int renorm, float renorm_eps, float routed_scale,
+                       int32_t* ids, float* weights, void* stream, RouterFuse* fuse = nullptr);
 
 // moe_blockwise_mapping plus an optional tile list (same checks and errors).
 int blockwise_mapping(const int32_t* ids, const float* affinities, const uint8_t* padding_mask,

@@ -30,33 +30,11 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   }
 }
 
-// Vector form for 16-byte aligned x and 8-byte aligned q: lane l of a wave takes
-// the 16-byte chunk (l & 15) of group 4 * quad + l / 16, so a wave covers four
-// groups per load instruction; each wave keeps U quads of loads in flight.
+// Vector form for 16-byte aligned x and 8-byte aligned q (act_quant_vec_body).
 __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __restrict__ x, long groups,
                                                             uint8_t* __restrict__ q,
                                                             float* __restrict__ s) {
-  constexpr int U = 4;
-  const int lane = threadIdx.x & 63;
-  const long quads = (groups + 3) / 4;
-  const long nwaves = (long)gridDim.x * 4;
-  for (long q0 = (long)blockIdx.x * 4 + (threadIdx.x >> 6); q0 < quads; q0 += U * nwaves) {
-    int4 c[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const long gi = 4 * (q0 + u * nwaves) + (lane >> 4);
-      c[u] = (gi < groups) ? *(const int4*)(x + gi * MOE_GROUP + 8 * (lane & 15)) : make_int4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const long gi = 4 * (q0 + u * nwaves) + (lane >> 4);  // whole 16-lane segments share gi
-      if (gi < groups) {
-        float v[8];
-        bf16x8_to_f32(c[u], v);
-        quant8_1x128(v, q + gi * MOE_GROUP + 8 * (lane & 15), s + gi, (lane & 15) == 0);
-      }
-    }
-  }
+  act_quant_vec_body(x, groups, q, s, blockIdx.x, gridDim.x);
 }
 
 // out[t] = sum_s w[t,s] * y[inv[t,s]] (inv >= 0) + sum_j y[NB + j*T + t], fp32 accumulation,

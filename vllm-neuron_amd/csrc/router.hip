@@ -4,10 +4,23 @@
 // Reference behaviour: vllm_neuron/functional/moe/router.py:384-566 (torch
 // fallback orders), moe_block_tkg.py:153-205 (router_pre_norm / norm_topk_prob),
 // plus DeepSeek-V3 grouped sigmoid routing with a selection-only correction bias.
-#include "moe_common.h"
-#include "moe_internal.h"
+#include "mapping.h"
 
 namespace moe {
+
+// Side jobs of the logits launch, for the layer: `zero` (when set) is cleared by
+// workgroup 0 before the top-k launch counts workgroups on it, and workgroups
+// [qblk0, qblk0 + qnblk) quantize x (1x128 groups, act_quant_vec_body) instead of
+// computing logits: the quantization does not depend on the routing, so it needs
+// no launch of its own.
+struct LogitsSide {
+  int* zero;
+  const uint16_t* qx;
+  long qgroups;
+  uint8_t* qq;
+  float* qs;
+  int qblk0, qnblk;
+};
 
 // ---------------------------------------------------------------------------
 // logits[t, e] = sum_h x[t, h] * w[e, h]   (bf16 operands, fp32 accumulation)
@@ -26,7 +39,7 @@ namespace moe {
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const float* __restrict__ bias, int T, int H, int E, int kchunk, int ks,
-    float* __restrict__ out) {
+    float* __restrict__ out, LogitsSide side) {
   // x tile: 64 rows x 256 columns (four 64-column K steps), rows padded by 8.
   constexpr int KW = 256, LDX = KW + 8;
   __shared__ __attribute__((aligned(16))) uint16_t sx[64][LDX];
@@ -38,6 +51,11 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   const int nct = (E + 63) / 64;
   const long total = (long)nct * ((T + 63) / 64) * ks;
   const long per = (total + 7) / 8;
+  if (side.qnblk > 0 && (int)blockIdx.x >= side.qblk0) {  // whole workgroup
+    act_quant_vec_body(side.qx, side.qgroups, side.qq, side.qs, blockIdx.x - side.qblk0, side.qnblk);
+    return;
+  }
+  if (side.zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *side.zero = 0;
   const long L = (long)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
   if (L >= total) return;  // whole workgroup
   const int ct = (int)(L % nct);
@@ -143,7 +161,7 @@ template <int EF>
 __global__ __launch_bounds__(1024) void router_logits_wide_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const float* __restrict__ bias, int T, int H, int E, int kchunk, int ks,
-    float* __restrict__ out) {
+    float* __restrict__ out, int* __restrict__ zero) {
   constexpr int KW = 128, LDX = KW + 8;
   __shared__ __attribute__((aligned(16))) uint16_t sx[128][LDX];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -153,6 +171,7 @@ __global__ __launch_bounds__(1024) void router_logits_wide_kernel(
   const int nrt = (T + 127) / 128;
   const long total = (long)nrt * ks;
   const long per = (total + 7) / 8;
+  if (zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *zero = 0;
   const long L = (long)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
   if (L >= total) return;  // whole workgroup
   const int kz = (int)(L / nrt), rt = (int)(L % nrt);
@@ -247,23 +266,30 @@ static RouterPlan router_plan(int T, int H, int E) {
 
 // The logits product into out (ks == 1: the logits with bias) or into the
 // partials [ks, T, E].
+// Workgroups of the 64 x 64 form (a multiple of 8, for the XCD mapping).
+static long logits_blocks(const RouterPlan& pl, int T, int E) {
+  const long tiles = (long)((T + 63) / 64) * ((E + 63) / 64) * pl.ks;
+  return ((tiles + 7) / 8) * 8;
+}
+
+// side.qnblk > 0 only with the 64 x 64 form (qblk0 = logits_blocks).
 static void launch_router_logits(const RouterPlan& pl, const void* x_bf16, const void* w_bf16,
                                  const float* bias, int T, int H, int E, float* out,
-                                 hipStream_t st) {
+                                 hipStream_t st, const LogitsSide& side = LogitsSide{}) {
   if (pl.wide) {
     const long tiles = (long)((T + 127) / 128) * pl.ks;
     const dim3 grid((unsigned)(((tiles + 7) / 8) * 8));
     const dim3 block((unsigned)(64 * (E / (16 * pl.ef))));
 #define MOE_WIDE(EFV)                                                                              \
   hipLaunchKernelGGL(router_logits_wide_kernel<EFV>, grid, block, 0, st, (const uint16_t*)x_bf16, \
-                     (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk, pl.ks, out)
+                     (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk, pl.ks, out, side.zero)
     MOE_WIDE(1);
 #undef MOE_WIDE
   } else {
-    const long tiles = (long)((T + 63) / 64) * ((E + 63) / 64) * pl.ks;
-    hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)(((tiles + 7) / 8) * 8)), dim3(256), 0,
-                       st, (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E,
-                       pl.kchunk, pl.ks, out);
+    const long blocks = logits_blocks(pl, T, E) + std::max(side.qnblk, 0);
+    hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk,
+                       pl.ks, out, side);
   }
 }
 
@@ -360,17 +386,26 @@ __device__ __forceinline__ void top2_step(float& t1, float& t2) {
   t2 = fmaxf(lo, fmaxf(t2, b2));
 }
 
-template <int PM>
-__global__ __launch_bounds__(256) void router_topk_kernel(
+// The mapping that the top-k launch ends in (MAP): blockwise_mapping's outputs
+// and workspace for the ids the launch selects.
+struct MapJob {
+  int B, N;
+  int32_t *tpid, *b2e, *cond, *counts, *inv;
+  MapWs ws;
+  TileOut to;
+};
+
+template <int PM, bool MAP>
+__global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     const float* __restrict__ logits, const float* __restrict__ corr_bias, int T, int E, int K,
     int order, int scoring, int n_group, int topk_group, int renorm, float eps, float scale,
     int32_t* __restrict__ ids, float* __restrict__ weights, float* __restrict__ aff,
     const float* __restrict__ part, int ksplit, const float* __restrict__ lbias,
-    float* __restrict__ logits_out) {
+    float* __restrict__ logits_out, int tpb, MapJob mj) {
   __shared__ float s_act[4][PM * 64];
   __shared__ float s_key[4][PM * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wave;
+  const int t0 = blockIdx.x * tpb, t = t0 + wave;
   const int P = (E + 63) / 64;
   const float NEG_INF = -__builtin_inff();
   const bool need_act = order != MOE_ORDER_TOPK_ACT;
@@ -384,8 +419,8 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   }
 
   if (part != nullptr) {
-    // Split-K partials [ksplit, T, E] summed by the whole workgroup for its (up to)
-    // four tokens, in split order and then + bias, exactly as router_logits_reduce
+    // Split-K partials [ksplit, T, E] summed by the whole workgroup for its tpb
+    // (at most four) tokens, in split order and then + bias, exactly as router_logits_reduce
     // does; the sums are also written to logits_out. A thread owns (token, expert)
     // pairs and keeps up to 32 partial loads in flight, so a single token (decode)
     // costs one memory round trip per pair for up to 32 splits (H / 256 splits up
@@ -394,9 +429,8 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     // writes activations there.
     constexpr int Q = 32;
     const size_t TE = (size_t)T * E;
-    const int t0 = blockIdx.x * 4;
-    const int npairs = min(4, T - t0) * E;
-    for (int q = threadIdx.x; q < npairs; q += 256) {
+    const int npairs = min(tpb, T - t0) * E;
+    for (int q = threadIdx.x; q < npairs; q += blockDim.x) {
       const int tl = q / E, e = q - tl * E;
       const float* src = part + (size_t)(t0 + tl) * E + e;
       const float bv = (lbias != nullptr) ? lbias[e] : 0.f;
@@ -415,206 +449,232 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     }
     __syncthreads();
   }
-  if (t >= T) return;  // wave-uniform; no workgroup barrier below
-
-  float lg[PM];
-  if (part == nullptr) {
-    const float* row = logits + (size_t)t * E;
-#pragma unroll
-    for (int j = 0; j < PM; ++j) {
-      int e = lane + 64 * j;
-      lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < PM; ++j) {
-      int e = lane + 64 * j;
-      lg[j] = (j < P && e < E) ? s_act[wave][e] : NEG_INF;
-    }
-  }
-
-  if (need_act) {
-    if (scoring == MOE_SCORING_SIGMOID) {
+  if (wave < tpb && t < T) {  // wave-uniform: one wave per token
+    float lg[PM];
+    if (part == nullptr) {
+      const float* row = logits + (size_t)t * E;
 #pragma unroll
       for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
-        if (j < P && e < E) s_act[wave][e] = det_sigmoid_f32(lg[j]);
+        lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
       }
     } else {
-      float m = NEG_INF;
-#pragma unroll
-      for (int j = 0; j < PM; ++j) m = fmaxf(m, lg[j]);
-      m = wave_max_f32(m);
 #pragma unroll
       for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
-        if (j < P && e < E) s_act[wave][e] = det_exp_f32(lg[j] - m);
-      }
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      float sum = 0.f;
-      for (int e = 0; e < E; ++e) sum += s_act[wave][e];
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int j = 0; j < PM; ++j) {
-        int e = lane + 64 * j;
-        if (j < P && e < E) s_act[wave][e] = s_act[wave][e] / sum;
+        lg[j] = (j < P && e < E) ? s_act[wave][e] : NEG_INF;
       }
     }
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 
-  // Selection keys (kept in registers, mirrored in LDS for the group scan).
-  float key[PM];
-  bool valid[PM];
+    if (need_act) {
+      if (scoring == MOE_SCORING_SIGMOID) {
 #pragma unroll
-  for (int j = 0; j < PM; ++j) {
-    int e = lane + 64 * j;
-    valid[j] = (j < P && e < E);
-    float kv = NEG_INF;
-    if (valid[j]) {
-      if (order == MOE_ORDER_TOPK_ACT || (order == MOE_ORDER_ACT_TOPK && scoring == MOE_SCORING_SOFTMAX)) {
-        kv = lg[j];
-      } else if (order == MOE_ORDER_ACT_TOPK) {
-        kv = s_act[wave][e];
+        for (int j = 0; j < PM; ++j) {
+          int e = lane + 64 * j;
+          if (j < P && e < E) s_act[wave][e] = det_sigmoid_f32(lg[j]);
+        }
       } else {
-        kv = s_act[wave][e] + cb[j];
+        float m = NEG_INF;
+#pragma unroll
+        for (int j = 0; j < PM; ++j) m = fmaxf(m, lg[j]);
+        m = wave_max_f32(m);
+#pragma unroll
+        for (int j = 0; j < PM; ++j) {
+          int e = lane + 64 * j;
+          if (j < P && e < E) s_act[wave][e] = det_exp_f32(lg[j] - m);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        float sum = 0.f;
+        for (int e = 0; e < E; ++e) sum += s_act[wave][e];
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < PM; ++j) {
+          int e = lane + 64 * j;
+          if (j < P && e < E) s_act[wave][e] = s_act[wave][e] / sum;
+        }
       }
-      s_key[wave][e] = kv;
     }
-    key[j] = kv;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
 
-  if (order == MOE_ORDER_GROUPED && n_group > 1 && topk_group < n_group) {
-    const int gs = E / n_group;
-    float gscore = NEG_INF;
-    int gidx = 0x7fffffff;
-    if (gs == 32 && P * 64 == E) {
-      // Groups of 32: group 2j + lane / 32 is register j of one 32-lane half,
-      // so its top 2 is a DPP reduction within the half (lane 31 / 63 gets it).
-      // NaN keys count as -inf, as in the sequential scan, which skips them.
+    // Selection keys (kept in registers, mirrored in LDS for the group scan).
+    float key[PM];
+    bool valid[PM];
+#pragma unroll
+    for (int j = 0; j < PM; ++j) {
+      int e = lane + 64 * j;
+      valid[j] = (j < P && e < E);
+      float kv = NEG_INF;
+      if (valid[j]) {
+        if (order == MOE_ORDER_TOPK_ACT || (order == MOE_ORDER_ACT_TOPK && scoring == MOE_SCORING_SOFTMAX)) {
+          kv = lg[j];
+        } else if (order == MOE_ORDER_ACT_TOPK) {
+          kv = s_act[wave][e];
+        } else {
+          kv = s_act[wave][e] + cb[j];
+        }
+        s_key[wave][e] = kv;
+      }
+      key[j] = kv;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+
+    if (order == MOE_ORDER_GROUPED && n_group > 1 && topk_group < n_group) {
+      const int gs = E / n_group;
+      float gscore = NEG_INF;
+      int gidx = 0x7fffffff;
+      if (gs == 32 && P * 64 == E) {
+        // Groups of 32: group 2j + lane / 32 is register j of one 32-lane half,
+        // so its top 2 is a DPP reduction within the half (lane 31 / 63 gets it).
+        // NaN keys count as -inf, as in the sequential scan, which skips them.
+#pragma unroll
+        for (int j = 0; j < PM; ++j) {
+          if (j < P) {
+            float t1 = (key[j] == key[j]) ? key[j] : NEG_INF, t2 = NEG_INF;
+            top2_step<0xB1, 0xF>(t1, t2);
+            top2_step<0x4E, 0xF>(t1, t2);
+            top2_step<0x141, 0xF>(t1, t2);
+            top2_step<0x140, 0xF>(t1, t2);
+            top2_step<0x142, 0xA>(t1, t2);
+            const float g_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1 + t2), 31));
+            const float g_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1 + t2), 63));
+            if (lane == 2 * j) {
+              gscore = g_lo;
+              gidx = lane;
+            }
+            if (lane == 2 * j + 1) {
+              gscore = g_hi;
+              gidx = lane;
+            }
+          }
+        }
+      } else if (lane < n_group) {
+        float t1 = NEG_INF, t2 = NEG_INF;
+        for (int q = 0; q < gs; ++q) {
+          float v = s_key[wave][lane * gs + q];
+          if (v > t1) {
+            t2 = t1;
+            t1 = v;
+          } else if (v > t2) {
+            t2 = v;
+          }
+        }
+        gscore = (gs == 1) ? t1 : t1 + t2;
+        gidx = lane;
+      }
+      // A NaN group score (+inf + -inf) ranks below every number, -inf included,
+      // lower group first: it competes as -inf with its index moved past 63.
+      if (gidx < n_group && gscore != gscore) {
+        gscore = NEG_INF;
+        gidx += 64;
+      }
+      uint64_t keep = 0;
+      for (int q = 0; q < topk_group; ++q) {
+        KeyIdx b = wave_argmax(gscore, gidx);
+        if (b.i < 128) keep |= 1ull << (b.i & 63);
+        if (lane == (b.i & 63)) {
+          gscore = NEG_INF;
+          gidx = 0x7fffffff;
+        }
+      }
 #pragma unroll
       for (int j = 0; j < PM; ++j) {
-        if (j < P) {
-          float t1 = (key[j] == key[j]) ? key[j] : NEG_INF, t2 = NEG_INF;
-          top2_step<0xB1, 0xF>(t1, t2);
-          top2_step<0x4E, 0xF>(t1, t2);
-          top2_step<0x141, 0xF>(t1, t2);
-          top2_step<0x140, 0xF>(t1, t2);
-          top2_step<0x142, 0xA>(t1, t2);
-          const float g_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1 + t2), 31));
-          const float g_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1 + t2), 63));
-          if (lane == 2 * j) {
-            gscore = g_lo;
-            gidx = lane;
-          }
-          if (lane == 2 * j + 1) {
-            gscore = g_hi;
-            gidx = lane;
-          }
+        int e = lane + 64 * j;
+        if (valid[j] && !((keep >> (e / gs)) & 1ull)) valid[j] = false;
+      }
+    }
+
+    // K rounds of wave argmax; lane k keeps the k-th winner.
+    int my_id = -1;
+    float my_key = 0.f;
+    int taken[PM];
+#pragma unroll
+    for (int j = 0; j < PM; ++j) taken[j] = -1;
+    for (int k = 0; k < K; ++k) {
+      float bv = NEG_INF;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int j = 0; j < PM; ++j) {
+        int e = lane + 64 * j;
+        if (valid[j] && taken[j] < 0 && better(key[j], e, bv, bi)) {
+          bv = key[j];
+          bi = e;
         }
       }
-    } else if (lane < n_group) {
-      float t1 = NEG_INF, t2 = NEG_INF;
-      for (int q = 0; q < gs; ++q) {
-        float v = s_key[wave][lane * gs + q];
-        if (v > t1) {
-          t2 = t1;
-          t1 = v;
-        } else if (v > t2) {
-          t2 = v;
-        }
-      }
-      gscore = (gs == 1) ? t1 : t1 + t2;
-      gidx = lane;
-    }
-    // A NaN group score (+inf + -inf) ranks below every number, -inf included,
-    // lower group first: it competes as -inf with its index moved past 63.
-    if (gidx < n_group && gscore != gscore) {
-      gscore = NEG_INF;
-      gidx += 64;
-    }
-    uint64_t keep = 0;
-    for (int q = 0; q < topk_group; ++q) {
-      KeyIdx b = wave_argmax(gscore, gidx);
-      if (b.i < 128) keep |= 1ull << (b.i & 63);
-      if (lane == (b.i & 63)) {
-        gscore = NEG_INF;
-        gidx = 0x7fffffff;
-      }
-    }
+      KeyIdx b = wave_argmax(bv, bi);
 #pragma unroll
-    for (int j = 0; j < PM; ++j) {
-      int e = lane + 64 * j;
-      if (valid[j] && !((keep >> (e / gs)) & 1ull)) valid[j] = false;
+      for (int j = 0; j < PM; ++j)
+        if (lane + 64 * j == b.i) taken[j] = k;
+      if (lane == k) {
+        my_id = (b.i < E) ? b.i : -1;  // no valid candidate left (NaN keys): id -1
+        my_key = b.v;
+      }
     }
-  }
 
-  // K rounds of wave argmax; lane k keeps the k-th winner.
-  int my_id = -1;
-  float my_key = 0.f;
-  int taken[PM];
-#pragma unroll
-  for (int j = 0; j < PM; ++j) taken[j] = -1;
-  for (int k = 0; k < K; ++k) {
-    float bv = NEG_INF;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < PM; ++j) {
-      int e = lane + 64 * j;
-      if (valid[j] && taken[j] < 0 && better(key[j], e, bv, bi)) {
-        bv = key[j];
-        bi = e;
+    // Weights for the K selections (lane k holds selection k).
+    float wv = 0.f;
+    if (order == MOE_ORDER_TOPK_ACT) {
+      if (scoring == MOE_SCORING_SOFTMAX) {
+        float m0 = __shfl(my_key, 0, 64);
+        float ex = (lane < K) ? det_exp_f32(my_key - m0) : 0.f;
+        float sum = 0.f;
+        for (int k = 0; k < K; ++k) sum += __shfl(ex, k, 64);
+        wv = ex / sum;
+      } else {
+        wv = (lane < K) ? det_sigmoid_f32(my_key) : 0.f;
       }
-    }
-    KeyIdx b = wave_argmax(bv, bi);
-#pragma unroll
-    for (int j = 0; j < PM; ++j)
-      if (lane + 64 * j == b.i) taken[j] = k;
-    if (lane == k) {
-      my_id = (b.i < E) ? b.i : -1;  // no valid candidate left (NaN keys): id -1
-      my_key = b.v;
-    }
-  }
-
-  // Weights for the K selections (lane k holds selection k).
-  float wv = 0.f;
-  if (order == MOE_ORDER_TOPK_ACT) {
-    if (scoring == MOE_SCORING_SOFTMAX) {
-      float m0 = __shfl(my_key, 0, 64);
-      float ex = (lane < K) ? det_exp_f32(my_key - m0) : 0.f;
-      float sum = 0.f;
-      for (int k = 0; k < K; ++k) sum += __shfl(ex, k, 64);
-      wv = ex / sum;
     } else {
-      wv = (lane < K) ? det_sigmoid_f32(my_key) : 0.f;
+      wv = (lane < K && my_id >= 0) ? s_act[wave][my_id] : 0.f;
     }
-  } else {
-    wv = (lane < K && my_id >= 0) ? s_act[wave][my_id] : 0.f;
-  }
-  if (renorm) {
-    float sum = 0.f;
-    for (int k = 0; k < K; ++k) sum += __shfl(wv, k, 64);
-    float den = sum + eps;
-    wv = wv / den;
-  }
-  wv = wv * scale;
+    if (renorm) {
+      float sum = 0.f;
+      for (int k = 0; k < K; ++k) sum += __shfl(wv, k, 64);
+      float den = sum + eps;
+      wv = wv / den;
+    }
+    wv = wv * scale;
 
-  if (lane < K) {
-    ids[(size_t)t * K + lane] = my_id;
-    weights[(size_t)t * K + lane] = wv;
-  }
-  if (aff != nullptr) {
-#pragma unroll
-    for (int j = 0; j < PM; ++j) {
-      int e = lane + 64 * j;
-      int k = taken[j];
-      float v = __shfl(wv, k < 0 ? 0 : k, 64);  // all lanes take part in the shuffle
-      if (j < P && e < E) aff[(size_t)t * E + e] = (k >= 0) ? v : 0.f;
+    if (lane < K) {
+      ids[(size_t)t * K + lane] = my_id;
+      weights[(size_t)t * K + lane] = wv;
     }
+    if (aff != nullptr) {
+#pragma unroll
+      for (int j = 0; j < PM; ++j) {
+        int e = lane + 64 * j;
+        int k = taken[j];
+        float v = __shfl(wv, k < 0 ? 0 : k, 64);  // all lanes take part in the shuffle
+        if (j < P && e < E) aff[(size_t)t * E + e] = (k >= 0) ? v : 0.f;
+      }
+    }
+  }
+  if constexpr (MAP) {
+    // The last workgroup to finish builds the mapping from every token's ids
+    // (the decode form of blockwise_mapping, map_small_body). After the barrier
+    // (every wave's stores done) one thread per workgroup releases them at device
+    // scope and takes a ticket; the last one acquires every workgroup's ids. One
+    // fence per workgroup: a device-scope fence writes back (release) or
+    // invalidates (acquire) the whole L2 of its XCD. mj.ws.status[1] was cleared
+    // by the logits launch.
+    __shared__ uint32_t s_bm[PM * 64][8];
+    __shared__ int s_blk[PM * 64], s_cnt[PM * 64], s_cex[PM * 64], s_tile[PM * 64];
+    __shared__ int s_wave[16];
+    __shared__ int s_last;
+    __syncthreads();
+    if (gridDim.x > 1) {  // workgroup-uniform
+      if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const bool last = atomicAdd(mj.ws.status + 1, 1) == (int)gridDim.x - 1;
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        s_last = last;
+      }
+      __syncthreads();
+      if (!s_last) return;  // whole workgroup
+    }
+    map_small_body(ids, T, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond, mj.counts, mj.inv, mj.ws,
+                   mj.to, s_bm, s_blk, s_cnt, s_cex, s_tile, s_wave);
   }
 }
 
@@ -684,9 +744,10 @@ extern "C" int moe_router_topk(const float* logits, const float* corr_bias, int 
   // that covers E, so the per-chunk loops unroll without dead iterations.
   const int P = (E + 63) / 64;
 #define MOE_TOPK_LAUNCH(PMV)                                                                   \
-  hipLaunchKernelGGL(router_topk_kernel<PMV>, dim3((T + 3) / 4), dim3(256), 0, (hipStream_t)stream, \
-                     logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,     \
-                     renorm_eps, routed_scale, ids, weights, affinities, nullptr, 0, nullptr, nullptr)
+  hipLaunchKernelGGL((router_topk_kernel<PMV, false>), dim3((T + 3) / 4), dim3(256), 0,            \
+                     (hipStream_t)stream, logits, corr_bias, T, E, K, order, scoring, n_group,     \
+                     topk_group, renorm, renorm_eps, routed_scale, ids, weights, affinities,       \
+                     nullptr, 0, nullptr, nullptr, 4, MapJob{})
   if (P <= 1)
     MOE_TOPK_LAUNCH(1);
   else if (P <= 2)
@@ -704,16 +765,19 @@ extern "C" int moe_router_topk(const float* logits, const float* corr_bias, int 
 // Router logits and top-k for the layer: with a split-K logits product the top-k
 // kernel sums the partials itself (same order and values as router_logits_reduce,
 // written to logits), one launch fewer than moe_router_logits + moe_router_topk.
+// With `fuse` the logits launch also quantizes x and, for up to 256 tokens and
+// 512 experts, the top-k launch ends in the mapping (see RouterFuse).
 // Arguments are those of the two entry points, already checked by the caller.
 int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float* bias, int T, int H,
                             int E, float* logits, void* workspace, size_t workspace_bytes,
                             const float* corr_bias, int K, int order, int scoring, int n_group,
                             int topk_group, int renorm, float renorm_eps, float routed_scale,
-                            int32_t* ids, float* weights, void* stream) {
+                            int32_t* ids, float* weights, void* stream, RouterFuse* fuse) {
+  if (fuse != nullptr) fuse->quant_done = fuse->map_done = false;
   const RouterPlan pl = router_plan(T, H, E);
   const int ks = pl.ks;
-  if (ks == 1 || T == 0 || E > kTopkMaxE || workspace == nullptr ||
-      workspace_bytes < (size_t)ks * T * E * sizeof(float)) {
+  if (T == 0 || E > kTopkMaxE ||
+      (ks > 1 && (workspace == nullptr || workspace_bytes < (size_t)ks * T * E * sizeof(float)))) {
     int rc = moe_router_logits(x_bf16, w_bf16, bias, T, H, E, logits, workspace, workspace_bytes,
                                stream);
     if (rc != MOE_OK) return rc;
@@ -738,23 +802,90 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
                   "topk_group * group size must be >= top_k");
   }
   hipStream_t st = (hipStream_t)stream;
-  float* part = (float*)workspace;
-  launch_router_logits(pl, x_bf16, w_bf16, bias, T, H, E, part, st);
   const int P = (E + 63) / 64;
-#define MOE_TOPK_FUSED(PMV)                                                                       \
-  hipLaunchKernelGGL(router_topk_kernel<PMV>, dim3((T + 3) / 4), dim3(256), 0, st, nullptr, corr_bias, \
-                     T, E, K, order, scoring, n_group, topk_group, renorm, renorm_eps,             \
-                     routed_scale, ids, weights, nullptr, part, ks, bias, logits)
-  if (P <= 1)
-    MOE_TOPK_FUSED(1);
-  else if (P <= 2)
-    MOE_TOPK_FUSED(2);
-  else if (P <= 4)
-    MOE_TOPK_FUSED(4);
-  else if (P <= 8)
-    MOE_TOPK_FUSED(8);
-  else
-    MOE_TOPK_FUSED(kTopkMaxP);
+  LogitsSide side{};
+  MapJob mj{};
+  // The mapping in the top-k launch: ids only, one 256-token chunk (the decode form
+  // of blockwise_mapping), E <= 512 (the top-k kernel at 1024 threads keeps its
+  // per-lane arrays in registers); otherwise the caller runs blockwise_mapping.
+  const bool do_map =
+      fuse != nullptr && fuse->tpid != nullptr && fuse->b2e != nullptr && fuse->map_ws != nullptr &&
+      T <= kChunk && P <= 8 && fuse->B > 0 && fuse->N == moe_num_blocks(T, K, E, fuse->B) &&
+      fuse->map_ws_bytes >= map_ws_bytes(T, E) &&
+      (fuse->to.tiles == nullptr ||
+       (fuse->to.num_tiles && fuse->to.mt > 0 && fuse->to.max_tiles > 0 && fuse->to.n_shared >= 0 &&
+        (!fuse->to.span || fuse->to.seg))) &&
+      (!fuse->to.compact || (fuse->to.tiles != nullptr && fuse->to.row_shared >= 0));
+  if (do_map) {
+    mj.B = fuse->B;
+    mj.N = fuse->N;
+    mj.tpid = fuse->tpid;
+    mj.b2e = fuse->b2e;
+    mj.cond = fuse->cond;
+    mj.counts = fuse->counts;
+    mj.inv = fuse->inv;
+    mj.ws = carve_map_ws(fuse->map_ws, T, E);
+    mj.to = fuse->to;
+    side.zero = mj.ws.status + 1;  // the top-k launch's workgroup counter
+  }
+  // The quantization in the logits launch (the 64 x 64 form, moe_act_quant_1x128's
+  // vector path).
+  const bool do_quant = fuse != nullptr && fuse->xq != nullptr && fuse->xs != nullptr && !pl.wide &&
+                        H % MOE_GROUP == 0 && ((uintptr_t)fuse->xq & 7) == 0;
+  if (do_quant) {
+    const long groups = (long)T * (H / MOE_GROUP);
+    side.qx = (const uint16_t*)x_bf16;
+    side.qgroups = groups;
+    side.qq = fuse->xq;
+    side.qs = fuse->xs;
+    side.qblk0 = (int)logits_blocks(pl, T, E);
+    side.qnblk = (int)std::max(1L, std::min<long>((groups + 15) / 16, 2048));
+  }
+  float* part = ks > 1 ? (float*)workspace : nullptr;
+  launch_router_logits(pl, x_bf16, w_bf16, bias, T, H, E, part ? part : logits, st, side);
+  // Split-K: the top-k kernel sums the partials (+ bias) and writes the logits;
+  // one split: the logits kernel wrote them with the bias.
+  const float* lin = part ? nullptr : logits;
+  const float* lbias = part ? bias : nullptr;
+  float* lout = part ? logits : nullptr;
+  if (do_map) {
+    // One token per workgroup up to 64 tokens, so the partial sums of a token take
+    // one memory round trip on 1024 threads; at most four tokens per workgroup above.
+    const int tpb = T <= 64 ? 1 : (T + 63) / 64;
+    const dim3 grid((T + tpb - 1) / tpb);
+#define MOE_TOPK_MAP(PMV)                                                                          \
+  hipLaunchKernelGGL((router_topk_kernel<PMV, true>), grid, dim3(1024), 0, st, lin, corr_bias, T, E, \
+                     K, order, scoring, n_group, topk_group, renorm, renorm_eps, routed_scale, ids,  \
+                     weights, nullptr, part, ks, lbias, lout, tpb, mj)
+    if (P <= 1)
+      MOE_TOPK_MAP(1);
+    else if (P <= 2)
+      MOE_TOPK_MAP(2);
+    else if (P <= 4)
+      MOE_TOPK_MAP(4);
+    else
+      MOE_TOPK_MAP(8);
+#undef MOE_TOPK_MAP
+  } else {
+#define MOE_TOPK_FUSED(PMV)                                                                        \
+  hipLaunchKernelGGL((router_topk_kernel<PMV, false>), dim3((T + 3) / 4), dim3(256), 0, st, lin,    \
+                     corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm, renorm_eps,   \
+                     routed_scale, ids, weights, nullptr, part, ks, lbias, lout, 4, MapJob{})
+    if (P <= 1)
+      MOE_TOPK_FUSED(1);
+    else if (P <= 2)
+      MOE_TOPK_FUSED(2);
+    else if (P <= 4)
+      MOE_TOPK_FUSED(4);
+    else if (P <= 8)
+      MOE_TOPK_FUSED(8);
+    else
+      MOE_TOPK_FUSED(kTopkMaxP);
 #undef MOE_TOPK_FUSED
+  }
+  if (fuse != nullptr) {
+    fuse->quant_done = do_quant;
+    fuse->map_done = do_map;
+  }
   MOE_API_END();
 }
