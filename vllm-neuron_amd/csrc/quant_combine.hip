@@ -37,12 +37,11 @@ __global__ __launch_bounds__(256) void act_quant_vec_kernel(const uint16_t* __re
   act_quant_vec_body(x, groups, q, s, blockIdx.x, gridDim.x);
 }
 
-// out[t] = sum_s w[t,s] * y[inv[t,s]] (inv >= 0) + sum_j y[NB + j*T + t], fp32 accumulation,
-// one workgroup per token, 8 bf16 (16 B) per thread per step.
-// One workgroup per (token, column chunk). The token's live rows are listed in
-// slot order (ballot compaction, so the order and the fp32 sums are the same as a
-// sequential scan), then each thread sums its 8 columns over the rows, with the
-// loads of up to eight rows in flight.
+// out[t] = sum_s w[t,s] * y[inv[t,s]] (inv >= 0) + sum_j y[NB + j*T + t], fp32 accumulation.
+// One workgroup per (token, column chunk), 8 bf16 (16 B) per thread. The token's live
+// rows are listed in slot order (ballot compaction, so the order and the fp32 sums
+// are the same as a sequential scan), then each thread sums its 8 columns over the
+// rows, with the loads of up to 16 rows in flight.
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y,
                                                       const int32_t* __restrict__ inv,
                                                       const float* __restrict__ w, int S, int T,
@@ -80,7 +79,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-    // Rows r0 .. r0 + NR - 1, all NR loads in flight, then summed in row order.
+    // Rows r0 .. r0 + NR - 1, all NR loads in flight (unconditional: a load under a
+    // branch would be waited for at the join), then summed in row order.
     auto rows = [&](auto nr, int r0) {
       constexpr int NR = decltype(nr)::value;
       int4 v[NR];
@@ -97,12 +97,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
         }
       }
     };
-    // Groups of 8, then 4, 2 and 1 rows (workgroup-uniform counts, no repeated loads).
-    int r0 = 0;
-    for (; r0 + 8 <= n; r0 += 8) rows(std::integral_constant<int, 8>{}, r0);
-    if (n - r0 >= 4) { rows(std::integral_constant<int, 4>{}, r0); r0 += 4; }
-    if (n - r0 >= 2) { rows(std::integral_constant<int, 2>{}, r0); r0 += 2; }
-    if (n - r0 >= 1) rows(std::integral_constant<int, 1>{}, r0);
+    // Up to 16 rows at a time, all their loads in flight (workgroup-uniform counts,
+    // no repeated loads): one memory round trip for a token's top-8 plus shared rows.
+    for (int r0 = 0; r0 < n; r0 += 16) {
+      switch (min(16, n - r0)) {
+#define MOE_ROWS(NRV)                                     \
+  case NRV:                                               \
+    rows(std::integral_constant<int, NRV>{}, r0);         \
+    break;
+        MOE_ROWS(1) MOE_ROWS(2) MOE_ROWS(3) MOE_ROWS(4) MOE_ROWS(5) MOE_ROWS(6) MOE_ROWS(7)
+        MOE_ROWS(8) MOE_ROWS(9) MOE_ROWS(10) MOE_ROWS(11) MOE_ROWS(12) MOE_ROWS(13)
+        MOE_ROWS(14) MOE_ROWS(15) MOE_ROWS(16)
+#undef MOE_ROWS
+      }
+    }
     int4 o;
     o.x = (int)bf16x2(acc[0], acc[1]);
     o.y = (int)bf16x2(acc[2], acc[3]);

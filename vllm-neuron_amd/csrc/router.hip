@@ -4,15 +4,18 @@
 // Reference behaviour: vllm_neuron/functional/moe/router.py:384-566 (torch
 // fallback orders), moe_block_tkg.py:153-205 (router_pre_norm / norm_topk_prob),
 // plus DeepSeek-V3 grouped sigmoid routing with a selection-only correction bias.
+#include <type_traits>
+
 #include "mapping.h"
 
 namespace moe {
 
 // Side jobs of the logits launch, for the layer: `zero` (when set) is cleared by
-// workgroup 0 before the top-k launch counts workgroups on it, and workgroups
-// [qblk0, qblk0 + qnblk) quantize x (1x128 groups, act_quant_vec_body) instead of
-// computing logits: the quantization does not depend on the routing, so it needs
-// no launch of its own.
+// workgroup 0 before the top-k launch counts workgroups on it, and x is quantized
+// (1x128 groups into qq / qs) since the quantization does not depend on the routing
+// and needs no launch of its own: by the extra workgroups [qblk0, qblk0 + qnblk)
+// (act_quant_vec_body) in the 64 x 64 form, by the wide form as it loads x (qq set,
+// qnblk 0).
 struct LogitsSide {
   int* zero;
   const uint16_t* qx;
@@ -161,7 +164,7 @@ template <int EF>
 __global__ __launch_bounds__(1024) void router_logits_wide_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const float* __restrict__ bias, int T, int H, int E, int kchunk, int ks,
-    float* __restrict__ out, int* __restrict__ zero) {
+    float* __restrict__ out, LogitsSide side) {
   constexpr int KW = 128, LDX = KW + 8;
   __shared__ __attribute__((aligned(16))) uint16_t sx[128][LDX];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(1024) void router_logits_wide_kernel(
   const int nrt = (T + 127) / 128;
   const long total = (long)nrt * ks;
   const long per = (total + 7) / 8;
-  if (zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *zero = 0;
+  if (side.zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *side.zero = 0;
   const long L = (long)(blockIdx.x & 7) * per + (blockIdx.x >> 3);
   if (L >= total) return;  // whole workgroup
   const int kz = (int)(L / nrt), rt = (int)(L % nrt);
@@ -199,6 +202,21 @@ __global__ __launch_bounds__(1024) void router_logits_wide_kernel(
       const int tr = min(t0 + row, T - 1);  // rows past T load row T-1 and are zeroed
       xv[c] = (idx < 2048) ? *(const int4*)(x + (size_t)tr * H + k0 + col) : make_int4(0, 0, 0, 0);
       if (t0 + row >= T) xv[c] = make_int4(0, 0, 0, 0);
+    }
+    if (side.qq != nullptr) {
+      // Every x element is loaded once (one token tile per K chunk); the 16 lanes of a
+      // row chunk (idx >> 4) hold one 1x128 group, so they quantize it here.
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int idx = tid + c * nthreads, row = idx >> 4, col = (idx & 15) * 8;
+        if (idx < 2048 && t0 + row < T) {  // whole 16-lane segments
+          float v[8];
+          bf16x8_to_f32(xv[c], v);
+          const size_t t = (size_t)(t0 + row);
+          quant8_1x128(v, side.qq + t * H + k0 + col, side.qs + t * (H / MOE_GROUP) + k0 / MOE_GROUP,
+                       (lane & 15) == 0);
+        }
+      }
     }
     v8bf b[EF][4];
 #pragma unroll
@@ -272,7 +290,8 @@ static long logits_blocks(const RouterPlan& pl, int T, int E) {
   return ((tiles + 7) / 8) * 8;
 }
 
-// side.qnblk > 0 only with the 64 x 64 form (qblk0 = logits_blocks).
+// side.qnblk > 0 only with the 64 x 64 form (qblk0 = logits_blocks); the wide form
+// quantizes inline (side.qq set).
 static void launch_router_logits(const RouterPlan& pl, const void* x_bf16, const void* w_bf16,
                                  const float* bias, int T, int H, int E, float* out,
                                  hipStream_t st, const LogitsSide& side = LogitsSide{}) {
@@ -282,7 +301,7 @@ static void launch_router_logits(const RouterPlan& pl, const void* x_bf16, const
     const dim3 block((unsigned)(64 * (E / (16 * pl.ef))));
 #define MOE_WIDE(EFV)                                                                              \
   hipLaunchKernelGGL(router_logits_wide_kernel<EFV>, grid, block, 0, st, (const uint16_t*)x_bf16, \
-                     (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk, pl.ks, out, side.zero)
+                     (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk, pl.ks, out, side)
     MOE_WIDE(1);
 #undef MOE_WIDE
   } else {
@@ -427,25 +446,63 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     // to H = 8192) instead of one per pair of splits. The sums are staged in
     // s_act[token], which each wave reads back for its own token below before it
     // writes activations there.
-    constexpr int Q = 32;
     const size_t TE = (size_t)T * E;
     const int npairs = min(tpb, T - t0) * E;
-    for (int q = threadIdx.x; q < npairs; q += blockDim.x) {
+    auto finish = [&](int q, float sum) {
       const int tl = q / E, e = q - tl * E;
-      const float* src = part + (size_t)(t0 + tl) * E + e;
-      const float bv = (lbias != nullptr) ? lbias[e] : 0.f;
-      float sum = 0.f;
-      for (int k0 = 0; k0 < ksplit; k0 += Q) {
-        float v[Q];
-#pragma unroll
-        for (int u = 0; u < Q; ++u) v[u] = src[(size_t)min(k0 + u, ksplit - 1) * TE];
-#pragma unroll
-        for (int u = 0; u < Q; ++u)
-          if (k0 + u < ksplit) sum += v[u];
-      }
-      const float lgv = (lbias != nullptr) ? sum + bv : sum;
+      const float lgv = (lbias != nullptr) ? sum + lbias[e] : sum;
       if (logits_out != nullptr) logits_out[(size_t)(t0 + tl) * E + e] = lgv;
       s_act[tl][e] = lgv;
+    };
+    // Up to 16 splits: Q >= ksplit loads per pair and 32 / Q pairs per thread at a
+    // time (32 loads in flight). Pairs past the end reload the last pair.
+    auto sum_few = [&](auto qc) {
+      constexpr int Q = decltype(qc)::value, PB = 32 / Q;
+      for (int q0 = threadIdx.x; q0 < npairs; q0 += PB * (int)blockDim.x) {
+        float v[PB][Q];
+#pragma unroll
+        for (int p = 0; p < PB; ++p) {
+          const int q = min(q0 + p * (int)blockDim.x, npairs - 1);
+          const int tl = q / E;
+          const float* src = part + (size_t)(t0 + tl) * E + (q - tl * E);
+#pragma unroll
+          for (int u = 0; u < Q; ++u) v[p][u] = src[(size_t)min(u, ksplit - 1) * TE];
+        }
+#pragma unroll
+        for (int p = 0; p < PB; ++p) {
+          const int q = q0 + p * (int)blockDim.x;
+          if (q < npairs) {
+            float sum = 0.f;
+#pragma unroll
+            for (int u = 0; u < Q; ++u)
+              if (u < ksplit) sum += v[p][u];
+            finish(q, sum);
+          }
+        }
+      }
+    };
+    if (ksplit <= 4) {
+      sum_few(std::integral_constant<int, 4>{});
+    } else if (ksplit <= 8) {
+      sum_few(std::integral_constant<int, 8>{});
+    } else if (ksplit <= 16) {
+      sum_few(std::integral_constant<int, 16>{});
+    } else {
+      constexpr int Q = 32;  // 32 splits at a time, one pair per thread
+      for (int q = threadIdx.x; q < npairs; q += blockDim.x) {
+        const int tl = q / E;
+        const float* src = part + (size_t)(t0 + tl) * E + (q - tl * E);
+        float sum = 0.f;
+        for (int k0 = 0; k0 < ksplit; k0 += Q) {
+          float v[Q];
+#pragma unroll
+          for (int u = 0; u < Q; ++u) v[u] = src[(size_t)min(k0 + u, ksplit - 1) * TE];
+#pragma unroll
+          for (int u = 0; u < Q; ++u)
+            if (k0 + u < ksplit) sum += v[u];
+        }
+        finish(q, sum);
+      }
     }
     __syncthreads();
   }
@@ -828,18 +885,19 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
     mj.to = fuse->to;
     side.zero = mj.ws.status + 1;  // the top-k launch's workgroup counter
   }
-  // The quantization in the logits launch (the 64 x 64 form, moe_act_quant_1x128's
-  // vector path).
-  const bool do_quant = fuse != nullptr && fuse->xq != nullptr && fuse->xs != nullptr && !pl.wide &&
+  // The quantization in the logits launch (codes as moe_act_quant_1x128's).
+  const bool do_quant = fuse != nullptr && fuse->xq != nullptr && fuse->xs != nullptr &&
                         H % MOE_GROUP == 0 && ((uintptr_t)fuse->xq & 7) == 0;
   if (do_quant) {
-    const long groups = (long)T * (H / MOE_GROUP);
-    side.qx = (const uint16_t*)x_bf16;
-    side.qgroups = groups;
     side.qq = fuse->xq;
     side.qs = fuse->xs;
-    side.qblk0 = (int)logits_blocks(pl, T, E);
-    side.qnblk = (int)std::max(1L, std::min<long>((groups + 15) / 16, 2048));
+    if (!pl.wide) {  // extra workgroups; the wide form quantizes as it loads x
+      const long groups = (long)T * (H / MOE_GROUP);
+      side.qx = (const uint16_t*)x_bf16;
+      side.qgroups = groups;
+      side.qblk0 = (int)logits_blocks(pl, T, E);
+      side.qnblk = (int)std::max(1L, std::min<long>((groups + 15) / 16, 2048));
+    }
   }
   float* part = ks > 1 ? (float*)workspace : nullptr;
   launch_router_logits(pl, x_bf16, w_bf16, bias, T, H, E, part ? part : logits, st, side);
