@@ -12,10 +12,13 @@
 // Work decomposition: a work item is (row tile, N tile). A row tile holds up
 // to MT consecutive slots of one expert (moe_build_tiles) and names the first
 // row of hq / y its slots use (the slot itself, or a compacted row in the
-// layer, whose buffers hold only the routed rows). Each workgroup
-// (4 waves) owns 256 weight rows: for gate_up, 128 gate rows and the matching
-// 128 up rows (so one workgroup sees a whole 128-column quantization group of
-// h); for down, 256 output columns. Wave w owns four 16-row MFMA column tiles.
+// layer, whose buffers hold only the routed rows). Each wave owns 64 weight
+// rows (four 16-row MFMA column tiles). gate_up workgroups (4 waves) own 256
+// weight rows: 128 gate rows and the matching 128 up rows, so one workgroup sees
+// a whole 128-column quantization group of h. down workgroups own 256 output
+// columns (4 waves), or 128 (2 waves) for tiles of up to 32 rows: two of those
+// fit a CU, so one workgroup's start-up (tile metadata, the first blocks' round
+// trip) and epilogue overlap the other's weight stream.
 //
 // K loop: one v_mfma_f32_16x16x128_f8f6f4 per 128-wide K block (exactly one
 // scale block), accumulated in fp32 as acc += mfma(a, b) * (s_a[row] * s_w).
@@ -124,22 +127,24 @@ __device__ __forceinline__ void lds_read_a(uint32_t a_lo, uint32_t a_hi, uint32_
 // One pipeline stage. Each stage is its own LDS object: the compiler then tells
 // the fragment reads of one stage from the direct-to-LDS loads in flight into the
 // others (it tracks such loads per LDS object) and does not drain them all.
-template <int MT>
+template <int MT, int NW>
 struct RowTileStage {
-  uint8_t b[4][8192];                       // wave w's 64 weight rows x 128 bytes
+  uint8_t b[NW][8192];                      // wave w's 64 weight rows x 128 bytes
   uint8_t a[MT / 8 + 1][1024];              // activation rows, 8 per slot (+ a spare slot)
   float as[(MT + 63) / 64 + 1][64];         // activation scales (+ a spare slot)
 };
 
-template <int MT, int KIND, int PD>
-__global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
+template <int MT, int KIND, int PD, int NW>
+__global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
   constexpr int MS = MT / 16;
   constexpr int AQ = MT / 8;                // activation loads (8 rows) per stage
-  constexpr int NA = (AQ + 3) / 4;          // ... per wave (spare ones go to slot AQ)
+  constexpr int NA = (AQ + NW - 1) / NW;    // ... per wave (spare ones go to slot AQ)
   constexpr int NSQ = (MT + 63) / 64;       // scale loads (64 rows) per stage
   constexpr int NV = 8 + NA + 1;            // direct-to-LDS loads per wave per stage
   static_assert(PD >= 2 && PD <= 4 && (PD - 2) * NV < 64, "pipeline depth");
-  using Stage = RowTileStage<MT>;
+  using Stage = RowTileStage<MT, NW>;
+  static_assert(NW == 4 || (KIND == 1 && NW == 2), "waves per workgroup");
+  static_assert(NW * 64 >= MT, "one thread per tile row");
   __shared__ __attribute__((aligned(1024))) Stage st0;
   __shared__ __attribute__((aligned(1024))) Stage st1;
   __shared__ __attribute__((aligned(1024))) Stage st2;
@@ -152,7 +157,7 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
   const int g = lane >> 4, r16 = lane & 15;
   const int Kdim = (KIND == 0) ? p.H : p.I;
   const int KB = Kdim / MOE_GROUP;
-  const int NT = (KIND == 0) ? p.I / 128 : p.H / 256;
+  const int NT = (KIND == 0) ? p.I / 128 : p.H / (64 * NW);
   const int total = p.num_tiles[0] * NT;
 
   for (int wi = blockIdx.x; wi < total; wi += gridDim.x) {
@@ -189,9 +194,9 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
     }
     // weight block scales of the tile's two 128-row halves: gate / up blocks
     // (gate_up) or the two output blocks (down)
-    for (int i = tid; i < 2 * KB; i += 256) {
+    for (int i = tid; i < (KIND == 0 ? 2 : NW / 2) * KB; i += 64 * NW) {
       const int h = i / KB, kb = i - h * KB;
-      const int rb = (KIND == 0) ? (h == 0 ? nt : p.I / 128 + nt) : nt * 2 + h;
+      const int rb = (KIND == 0) ? (h == 0 ? nt : p.I / 128 + nt) : nt * (NW / 2) + h;
       sWs[h][kb] = wsb[(size_t)rb * KB + kb];
     }
     __syncthreads();
@@ -208,7 +213,7 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
         row = (j < 2) ? nt * 128 + wave * 32 + j * 16 + rr
                       : p.I + nt * 128 + wave * 32 + (j - 2) * 16 + rr;
       else
-        row = nt * 256 + wave * 64 + j * 16 + rr;
+        row = nt * 64 * NW + wave * 64 + j * 16 + rr;
       boff[i] = (uint32_t)row * (uint32_t)Kdim + (uint32_t)swz(rr, lane & 7) * 16;
     }
     // Activation load a of wave w: tile rows [8q, 8q + 8), q = w NA + a (q >= AQ:
@@ -364,7 +369,7 @@ __global__ __launch_bounds__(256) void expert_gemm_kernel(GemmArgs p) {
             const long yrow = row0 + row;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const int col = nt * 256 + wave * 64 + j * 16 + r16;
+              const int col = nt * 64 * NW + wave * 64 + j * 16 + r16;
               p.y[(size_t)yrow * p.H + col] = (uint16_t)bf16x2(acc[ms][j][i], 0.f);
             }
           }
@@ -408,21 +413,25 @@ __global__ void selftest_mfma_kernel(const uint8_t* a, const uint8_t* b, float* 
 
 template <int KIND>
 static int launch_gemm(const GemmArgs& a, int max_tiles, int mt, hipStream_t st) {
-  const int NT = (KIND == 0) ? a.I / 128 : a.H / 256;
+  // down at 16 and 32 rows: 128 weight rows per workgroup (2 waves), so two
+  // workgroups share a CU and one's start-up overlaps the other's weight stream
+  constexpr int NWD = (KIND == 1) ? 2 : 4;
+  const int nw = (mt <= 32) ? NWD : 4;
+  const int NT = (KIND == 0) ? a.I / 128 : a.H / (64 * nw);
   const long items = (long)max_tiles * NT;
-  const int grid = (int)std::max(1L, std::min(items, 4096L));
+  const int grid = (int)std::max(1L, std::min(items, 4096L * 4 / nw));
   switch (mt) {
     case 16:
-      hipLaunchKernelGGL((expert_gemm_kernel<16, KIND, 3>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((expert_gemm_kernel<16, KIND, 3, NWD>), dim3(grid), dim3(64 * NWD), 0, st, a);
       break;
     case 32:
-      hipLaunchKernelGGL((expert_gemm_kernel<32, KIND, 3>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((expert_gemm_kernel<32, KIND, 3, NWD>), dim3(grid), dim3(64 * NWD), 0, st, a);
       break;
     case 64:
-      hipLaunchKernelGGL((expert_gemm_kernel<64, KIND, 3>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((expert_gemm_kernel<64, KIND, 3, 4>), dim3(grid), dim3(256), 0, st, a);
       break;
     case 128:
-      hipLaunchKernelGGL((expert_gemm_kernel<128, KIND, 2>), dim3(grid), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((expert_gemm_kernel<128, KIND, 2, 4>), dim3(grid), dim3(256), 0, st, a);
       break;
     default:
       return MOE_ERR_ARG;
