@@ -422,14 +422,19 @@ extern "C" int moe_layer_forward_mx(
   to.mt = mt;
   to.compact = 1;
   to.row_shared = R;
-  RouterFuse fz = map_fuse(w, B, N, to);  // the mapping ends the top-k launch at decode sizes
+  // Decode sizes: the MXFP8 quantization rides in the logits launch and the
+  // mapping ends the top-k launch (router_logits_topk says which it did).
+  RouterFuse fz = map_fuse(w, B, N, to);
+  fz.xq = w.xq;
+  fz.xs = xs;
+  fz.quant_mx = 1;
   MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
                               w.router_ws_bytes, nullptr, K, order, scoring, 1, 1, renorm,
                               renorm_eps, routed_scale, ids, wts, stream, &fz));
   if (!fz.map_done)
     MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
                                w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
-  MOE_STEP(moe_act_quant_mx(xr, T, H, w.xq, xs, stream));
+  if (!fz.quant_done) MOE_STEP(moe_act_quant_mx(xr, T, H, w.xq, xs, stream));
   MOE_STEP(moe_expert_gate_up_mx(w.xq, xs, T, H, I, E, wfmt, w13, w13_scale, b13, nullptr, nullptr,
                                  nullptr, 0, w.tpid, (int)NB, w.tiles, w.num_tiles, max_tiles, mt,
                                  act, gate_lo, gate_hi, up_lo, up_hi, w.hq, hs, stream));

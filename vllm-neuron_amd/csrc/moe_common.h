@@ -215,6 +215,52 @@ __device__ __forceinline__ void bf16x8_to_f32(const int4 c, float (&v)[8]) {
   }
 }
 
+// E8M0 exponent e of an MX block with magnitude maximum amax (OCP MX v1.0 6.3):
+// floor(log2(amax)) - 8 (8 = emax of e4m3), at least -127; the scale byte is
+// e + 127 and the elements are v * 2^-e (a power of two: exact), clamped to +-448
+// and rounded to nearest even. amax = 0 or subnormal gives e = -127.
+__device__ __forceinline__ int mx_exponent(float amax) {
+  const int ef = (int)((__float_as_uint(amax) >> 23) & 0xffu);
+  return max(ef - 135, -127);
+}
+
+// 2^-e for e in [-127, 119] (the range mx_exponent returns for finite input).
+__device__ __forceinline__ float mx_inv_scale(int e) { return __uint_as_float((uint32_t)(127 - e) << 23); }
+
+__device__ __forceinline__ uint32_t mx_e4m3x2(float a, float b, float f) {
+  return e4m3x2(fminf(fmaxf(a * f, -448.0f), 448.0f), fminf(fmaxf(b * f, -448.0f), 448.0f));
+}
+
+// MXFP8 quantization of `chunks` 8-value chunks of bf16 rows (chunks % 4 == 0) by
+// workgroup `blk` of `nblk` equal workgroups: lane q of a 4-lane group holds 8
+// consecutive values of one 32-value block (one 16-byte load), the block amax is
+// combined over the group, and the group writes 32 codes and one scale byte.
+__device__ __forceinline__ void mx_act_quant_body(const uint16_t* __restrict__ x, long chunks,
+                                                  uint8_t* __restrict__ q, uint8_t* __restrict__ s,
+                                                  int blk, int nblk) {
+  const long stride = (long)nblk * blockDim.x;
+  for (long c0 = (long)blk * blockDim.x; c0 < chunks; c0 += stride) {
+    const long c = c0 + threadIdx.x;  // whole 4-lane groups share the bound (chunks % 4 == 0)
+    float v[8];
+    float a = 0.f;
+    if (c < chunks) {
+      bf16x8_to_f32(*(const int4*)(x + c * 8), v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
+    }
+    a = fmaxf(a, __shfl_xor(a, 1, MOE_WAVE));
+    a = fmaxf(a, __shfl_xor(a, 2, MOE_WAVE));
+    if (c < chunks) {
+      const int ex = mx_exponent(a);
+      const float f = mx_inv_scale(ex);
+      const uint32_t lo = mx_e4m3x2(v[0], v[1], f) | (mx_e4m3x2(v[2], v[3], f) << 16);
+      const uint32_t hi = mx_e4m3x2(v[4], v[5], f) | (mx_e4m3x2(v[6], v[7], f) << 16);
+      *(uint2*)(q + c * 8) = make_uint2(lo, hi);
+      if ((c & 3) == 0) s[c >> 2] = (uint8_t)(ex + 127);
+    }
+  }
+}
+
 // 1x128 quantization of `groups` consecutive bf16 groups (x 16-byte aligned, q
 // 8-byte aligned) by workgroup `blk` of `nblk` equal workgroups: lane l of a wave
 // takes the 16-byte chunk (l & 15) of group 4 * quad + l / 16, so a wave covers

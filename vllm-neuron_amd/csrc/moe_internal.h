@@ -63,14 +63,16 @@ struct TileOut {
   long row_shared;
 };
 
-// Work that router_logits_topk may fold into its launches for the layer: the 1x128
-// quantization of x into xq / xs (when xq is set) and blockwise_mapping of the ids
-// it selects (when tpid is set; ids only, no padding mask, inv_pos = inv, workspace
-// map_ws, tile list `to`). On return quant_done / map_done say which it did; the
-// caller runs the rest itself.
+// Work that router_logits_topk may fold into its launches for the layer: the
+// quantization of x into xq / xs (when xq is set: 1x128 fp8 codes and fp32 scales,
+// or with quant_mx MXFP8 codes and E8M0 scale bytes) and blockwise_mapping of the
+// ids it selects (when tpid is set; ids only, no padding mask, inv_pos = inv,
+// workspace map_ws, tile list `to`). On return quant_done / map_done say which it
+// did; the caller runs the rest itself.
 struct RouterFuse {
   uint8_t* xq;
-  float* xs;
+  void* xs;
+  int quant_mx;
   int B, N;
   int32_t *tpid, *b2e, *cond, *counts, *inv;
   void* map_ws;

@@ -12,17 +12,18 @@ namespace moe {
 
 // Side jobs of the logits launch, for the layer: `zero` (when set) is cleared by
 // workgroup 0 before the top-k launch counts workgroups on it, and x is quantized
-// (1x128 groups into qq / qs) since the quantization does not depend on the routing
-// and needs no launch of its own: by the extra workgroups [qblk0, qblk0 + qnblk)
-// (act_quant_vec_body) in the 64 x 64 form, by the wide form as it loads x (qq set,
-// qnblk 0).
+// (1x128 groups into qq / qs, or MXFP8 32-value blocks with E8M0 scale bytes when
+// qmx is set) since the quantization does not depend on the routing and needs no
+// launch of its own: by the extra workgroups [qblk0, qblk0 + qnblk)
+// (act_quant_vec_body / mx_act_quant_body) in the 64 x 64 form, by the wide form
+// as it loads x (1x128 only: qq set, qnblk 0).
 struct LogitsSide {
   int* zero;
   const uint16_t* qx;
-  long qgroups;
+  long qgroups;  // 1x128 groups, or 8-value chunks (qmx)
   uint8_t* qq;
-  float* qs;
-  int qblk0, qnblk;
+  void* qs;
+  int qblk0, qnblk, qmx;
 };
 
 // ---------------------------------------------------------------------------
@@ -55,7 +56,12 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   const long total = (long)nct * ((T + 63) / 64) * ks;
   const long per = (total + 7) / 8;
   if (side.qnblk > 0 && (int)blockIdx.x >= side.qblk0) {  // whole workgroup
-    act_quant_vec_body(side.qx, side.qgroups, side.qq, side.qs, blockIdx.x - side.qblk0, side.qnblk);
+    if (side.qmx)
+      mx_act_quant_body(side.qx, side.qgroups, side.qq, (uint8_t*)side.qs, blockIdx.x - side.qblk0,
+                        side.qnblk);
+    else
+      act_quant_vec_body(side.qx, side.qgroups, side.qq, (float*)side.qs, blockIdx.x - side.qblk0,
+                         side.qnblk);
     return;
   }
   if (side.zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *side.zero = 0;
@@ -213,8 +219,8 @@ __global__ __launch_bounds__(1024) void router_logits_wide_kernel(
           float v[8];
           bf16x8_to_f32(xv[c], v);
           const size_t t = (size_t)(t0 + row);
-          quant8_1x128(v, side.qq + t * H + k0 + col, side.qs + t * (H / MOE_GROUP) + k0 / MOE_GROUP,
-                       (lane & 15) == 0);
+          quant8_1x128(v, side.qq + t * H + k0 + col,
+                       (float*)side.qs + t * (H / MOE_GROUP) + k0 / MOE_GROUP, (lane & 15) == 0);
         }
       }
     }
@@ -885,18 +891,27 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
     mj.to = fuse->to;
     side.zero = mj.ws.status + 1;  // the top-k launch's workgroup counter
   }
-  // The quantization in the logits launch (codes as moe_act_quant_1x128's).
+  // The quantization in the logits launch (codes as moe_act_quant_1x128's, or as
+  // moe_act_quant_mx's; the MX form only as extra workgroups of the 64 x 64 form).
   const bool do_quant = fuse != nullptr && fuse->xq != nullptr && fuse->xs != nullptr &&
-                        H % MOE_GROUP == 0 && ((uintptr_t)fuse->xq & 7) == 0;
+                        ((uintptr_t)fuse->xq & 7) == 0 &&
+                        (fuse->quant_mx ? H % 32 == 0 && !pl.wide : H % MOE_GROUP == 0);
   if (do_quant) {
     side.qq = fuse->xq;
     side.qs = fuse->xs;
+    side.qmx = fuse->quant_mx;
     if (!pl.wide) {  // extra workgroups; the wide form quantizes as it loads x
-      const long groups = (long)T * (H / MOE_GROUP);
       side.qx = (const uint16_t*)x_bf16;
-      side.qgroups = groups;
+      if (fuse->quant_mx) {
+        const long chunks = (long)T * H / 8;
+        side.qgroups = chunks;
+        side.qnblk = (int)std::max(1L, std::min<long>((chunks + 255) / 256, 4096));
+      } else {
+        const long groups = (long)T * (H / MOE_GROUP);
+        side.qgroups = groups;
+        side.qnblk = (int)std::max(1L, std::min<long>((groups + 15) / 16, 2048));
+      }
       side.qblk0 = (int)logits_blocks(pl, T, E);
-      side.qnblk = (int)std::max(1L, std::min<long>((groups + 15) / 16, 2048));
     }
   }
   float* part = ks > 1 ? (float*)workspace : nullptr;
