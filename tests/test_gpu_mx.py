@@ -159,11 +159,16 @@ def test_mx_experts_match_oracle(cuda, fmt, act, T, E, K):
     ("fp4", 2048, 8, 2, 1024, 2048),   # 64-row tiles, 2-stage ring, scale table
     ("fp4", 4096, 8, 2, 4608, 512),    # gate_up K > 4096: per-stage scale loads
     ("fp4", 2048, 8, 2, 4096, 256),    # down K = 256: fewer stages than the ring (drain)
-    ("fp8", 64, 64, 2, 1024, 1024)])   # MXFP8 weights: one K block per stage
+    ("fp8", 64, 64, 2, 1024, 1024),    # MXFP8 weights: one K block per stage
+    ("fp4", 1, 64, 2, 1024, 2048),     # one token: 2-wave half-width items, scale table
+    ("fp8", 1, 64, 2, 1024, 1024),     # ... MXFP8 weights
+    ("fp4", 1, 8, 2, 4608, 512)])      # ... gate_up without the scale table (K > 4096)
 def test_mx_experts_persistent_grid(cuda, fmt, T, E, K, H, I):
     """Shapes with more work items than CUs, so each persistent workgroup runs several
     items and its load ring crosses from item to item (or drains between them when K
-    has fewer stages than the ring), with and without the per-item scale table."""
+    has fewer stages than the ring), with and without the per-item scale table; and
+    one-token shapes, whose items run on 2-wave workgroups of half the width (one
+    item per CU)."""
     say("mx persistent", fmt, T, E, K, H, I)
     w = make_mx_weights(E, H, I, 11 + T, cuda, fmt)
     g = torch.Generator().manual_seed(3 * T + E)

@@ -19,9 +19,10 @@
 // no per-block fp32 multiply is left for the VALU.
 //
 // Work decomposition as in gemm_fp8.hip: a work item is (row tile, N tile); a
-// row tile holds up to MT consecutive slots of one expert; a workgroup (4 waves)
-// owns 256 weight rows (gate_up: 128 gate rows + the matching 128 up rows, so a
-// wave holds 32 h columns = one MX block of h; down: 256 output columns). Weight
+// row tile holds up to MT consecutive slots of one expert; a workgroup (NW = 4
+// waves, or 2 for one-token decode, which would otherwise leave CUs idle) owns
+// 64 NW weight rows (gate_up: 32 NW gate rows + the matching up rows, so a wave
+// holds 32 h columns = one MX block of h; down: 64 NW output columns). Weight
 // fragments stream from HBM into registers through a PD-deep ring (each weight
 // byte is read by exactly one lane); activation rows and their scale bytes are
 // gathered into LDS (double buffered).
@@ -95,13 +96,13 @@ __device__ __forceinline__ float mx_act(float g, int act) {
 // so the wait for the oldest stage is a compile-time vmcnt; the fragment reads
 // are asm statements that wait for their own data (see gemm_fp8.hip).
 // ---------------------------------------------------------------------------
-template <int MT, int WFMT, bool TBL>
+template <int MT, int WFMT, bool TBL, int NW>
 struct MxStage {
   static constexpr int KPS = (WFMT == kFmtFp4) ? 2 : 1;  // 128-K blocks per stage
   static constexpr int AQ = MT / 8;                     // activation loads per K block
   static constexpr int NSQ = (MT + 63) / 64;            // activation scale loads per K block
-  uint8_t b[4][8192];                  // wave w's 64 weight rows x 128 bytes
-  uint32_t bs[TBL ? 1 : 4][KPS][64];   // their scale dwords (row 16 j + r of the wave; unused
+  uint8_t b[NW][8192];                 // wave w's 64 weight rows x 128 bytes
+  uint32_t bs[TBL ? 1 : NW][KPS][64];   // their scale dwords (row 16 j + r of the wave; unused
                                        // with the per-item scale table)
   uint8_t a[KPS * AQ + 1][1024];       // activation rows: slot kk * AQ + q = rows 8q.. of block kk
   uint32_t as[KPS][NSQ + 1][64];       // activation scale dwords per 64-row group (+ a spare)
@@ -213,16 +214,17 @@ __device__ __forceinline__ void vm_ready(int& v) { asm volatile("" : "+v"(v)); }
 // reads them); with three stages the ring's second block of item j + 1 is issued
 // after that reload, so the first step's wait covers the table as well. Items
 // with fewer stages than the ring depth drain between items instead.
-template <int MT, int KIND, int PD, int WFMT, bool TBL>
-__global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
-  using Stage = MxStage<MT, WFMT, TBL>;
+template <int MT, int KIND, int PD, int WFMT, bool TBL, int NW>
+__global__ __launch_bounds__(64 * NW) void expert_gemm_mx_kernel(MxArgs p) {
+  using Stage = MxStage<MT, WFMT, TBL, NW>;
+  static_assert(NW == 4 || NW == 2, "waves per workgroup");
   constexpr int MS = MT / 16;
   constexpr int KPS = Stage::KPS, AQ = Stage::AQ, NSQ = Stage::NSQ;
-  constexpr int NA = (KPS * AQ + 3) / 4;       // activation loads per wave per stage
+  constexpr int NA = (KPS * AQ + NW - 1) / NW;  // activation loads per wave per stage
   constexpr int NV = 8 + (TBL ? 0 : KPS) + NA + KPS;  // direct-to-LDS loads per wave per stage
   static_assert(PD >= 2 && PD <= 3 && (PD - 2) * NV < 64, "pipeline depth");
   __shared__ __attribute__((aligned(1024))) Stage st[PD];
-  __shared__ __attribute__((aligned(16))) uint8_t sTbl[TBL ? 4 * 64 * 128 : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t sTbl[TBL ? NW * 64 * 128 : 16];
   __shared__ long sSrc[2][MT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -230,7 +232,7 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
   const int Kdim = (KIND == 0) ? p.H : p.I;
   const int KS = Kdim / 32;               // scale bytes per row
   const int NSTG = Kdim / (128 * KPS);    // stages (K % (128 KPS) == 0, checked by the entry points)
-  const int NT = (KIND == 0) ? p.I / 128 : p.H / 256;
+  const int NT = (KIND == 0) ? p.I / (32 * NW) : p.H / (64 * NW);
   const int total = p.num_tiles[0] * NT;
   const int G = gridDim.x;
   const std::integral_constant<int, WFMT> wfmt{};
@@ -264,8 +266,9 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
   // weight row of column tile j, row r of the tile, for this wave
   auto wrow_of = [&](const ItemDesc& d, int j, int r) -> int {
     if (KIND == 0)
-      return (j < 2) ? d.nt * 128 + wave * 32 + j * 16 + r : p.I + d.nt * 128 + wave * 32 + (j - 2) * 16 + r;
-    return d.nt * 256 + wave * 64 + j * 16 + r;
+      return (j < 2) ? d.nt * 32 * NW + wave * 32 + j * 16 + r
+                     : p.I + d.nt * 32 * NW + wave * 32 + (j - 2) * 16 + r;
+    return d.nt * 64 * NW + wave * 64 + j * 16 + r;
   };
   // token (gate_up) or h row (down) of tile row r; -1 for padding. tp: the
   // token-position entry (gate_up, routed experts).
@@ -549,10 +552,10 @@ __global__ __launch_bounds__(256) void expert_gemm_mx_kernel(MxArgs p) {
           if (sSrc[par][row] >= 0) {
             const float f = mx_inv_scale(ex);
             const uint32_t c2 = mx_e4m3x2(acc[ms][0][i], acc[ms][1][i], f);
-            uint8_t* const hrow = p.hq + (size_t)(row0 + row) * p.I + nt * 128 + wave * 32 + r16;
+            uint8_t* const hrow = p.hq + (size_t)(row0 + row) * p.I + nt * 32 * NW + wave * 32 + r16;
             hrow[0] = (uint8_t)c2;
             hrow[16] = (uint8_t)(c2 >> 8);
-            if (r16 == 0) p.hs[(size_t)(row0 + row) * GI + nt * 4 + wave] = (uint8_t)(ex + 127);
+            if (r16 == 0) p.hs[(size_t)(row0 + row) * GI + nt * NW + wave] = (uint8_t)(ex + 127);
           }
         }
       }
@@ -628,40 +631,53 @@ __global__ void selftest_mfma_mx_kernel(const uint8_t* a, const uint8_t* sa, con
 
 template <int KIND, int WFMT>
 static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
-  const int NT = (KIND == 0) ? a.I / 128 : a.H / 256;
-  const long items = (long)max_tiles * NT;
   // one persistent workgroup per CU (the ring's LDS allows one), each running
-  // every G-th work item
-  const int grid = (int)std::max(1L, std::min(items, (long)device_cu_count()));
+  // every G-th work item; 16-row tiles whose 2-wave half-width items still fit one
+  // per CU (one token) run those instead, twice as many workgroups
+  const int cus = device_cu_count();
+  const int nt4 = (KIND == 0) ? a.I / 128 : a.H / 256;
+  const bool half = mt == 16 && 2L * max_tiles * nt4 <= cus;
+  const int NT = half ? 2 * nt4 : nt4;
+  const long items = (long)max_tiles * NT;
+  const int grid = (int)std::max(1L, std::min(items, (long)cus));
   // the per-item scale table for K <= 4096 in whole 16-byte pieces per row
   // (K % 512 == 0), and for the tiles whose LDS has room
   const int Kdim = (KIND == 0) ? a.H : a.I;
   const bool tbl = Kdim <= kMxTblMaxK && Kdim % 512 == 0;
+#define MOE_MX(MTV, PDV, TBLV, NWV) \
+  hipLaunchKernelGGL((expert_gemm_mx_kernel<MTV, KIND, PDV, WFMT, TBLV, NWV>), dim3(grid), dim3(64 * NWV), 0, st, a)
   switch (mt) {
     case 16:
-      if (tbl)
-        hipLaunchKernelGGL((expert_gemm_mx_kernel<16, KIND, 3, WFMT, true>), dim3(grid), dim3(256), 0, st, a);
-      else
-        hipLaunchKernelGGL((expert_gemm_mx_kernel<16, KIND, 3, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
+      if (half) {
+        if (tbl)
+          MOE_MX(16, 3, true, 2);
+        else
+          MOE_MX(16, 3, false, 2);
+      } else if (tbl) {
+        MOE_MX(16, 3, true, 4);
+      } else {
+        MOE_MX(16, 3, false, 4);
+      }
       break;
     case 32:
       if (tbl)
-        hipLaunchKernelGGL((expert_gemm_mx_kernel<32, KIND, 2, WFMT, true>), dim3(grid), dim3(256), 0, st, a);
+        MOE_MX(32, 2, true, 4);
       else
-        hipLaunchKernelGGL((expert_gemm_mx_kernel<32, KIND, 3, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
+        MOE_MX(32, 3, false, 4);
       break;
     case 64:
       if (tbl)
-        hipLaunchKernelGGL((expert_gemm_mx_kernel<64, KIND, 2, WFMT, true>), dim3(grid), dim3(256), 0, st, a);
+        MOE_MX(64, 2, true, 4);
       else
-        hipLaunchKernelGGL((expert_gemm_mx_kernel<64, KIND, 2, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
+        MOE_MX(64, 2, false, 4);
       break;
     case 128:
-      hipLaunchKernelGGL((expert_gemm_mx_kernel<128, KIND, 2, WFMT, false>), dim3(grid), dim3(256), 0, st, a);
+      MOE_MX(128, 2, false, 4);
       break;
     default:
       return MOE_ERR_ARG;
   }
+#undef MOE_MX
   return MOE_OK;
 }
 
