@@ -76,13 +76,22 @@ static __device__ __forceinline__ void build_chunk_mask(uint32_t (*bm)[8], const
 
 // Inclusive sum over the 1024 threads of a workgroup (wave scans, then the
 // 16 wave totals); s_wave holds 16 ints.
+// Wave-inclusive part by DPP moves (no LDS round trips): row_shr 1, 2, 4, 8 within
+// each row of 16 lanes (lanes shifted in from outside the row add 0), then row 0's
+// total into row 1 and row 2's into row 3 (row_bcast:15), and the total of rows 0-1
+// into rows 2-3 (row_bcast:31).
+template <int CTRL, int ROW_MASK>
+static __device__ __forceinline__ int dpp_add_in(int v) {
+  return v + __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, true);
+}
 static __device__ __forceinline__ int block_inclusive_sum(int v, int* s_wave) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
-  }
+  v = dpp_add_in<0x111, 0xF>(v);
+  v = dpp_add_in<0x112, 0xF>(v);
+  v = dpp_add_in<0x114, 0xF>(v);
+  v = dpp_add_in<0x118, 0xF>(v);
+  v = dpp_add_in<0x142, 0xA>(v);
+  v = dpp_add_in<0x143, 0xC>(v);
   if (lane == 63) s_wave[wave] = v;
   __syncthreads();
   int add = 0;

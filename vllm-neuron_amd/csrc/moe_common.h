@@ -91,7 +91,7 @@ __device__ __forceinline__ float div_by(float x, float d, float rd) {
 // Cody-Waite reduction with C1 = 355/512 (exact), degree-7 Taylor (Horner),
 // scale by 2^n. Argument clamped to [-80, 80] (no subnormal intermediates).
 // ---------------------------------------------------------------------------
-__device__ __attribute__((noinline)) float det_exp_f32(float x) {
+__device__ __forceinline__ float det_exp_f32(float x) {
 #pragma clang fp contract(off)
   x = fminf(fmaxf(x, -80.0f), 80.0f);
   float n = __builtin_rintf(x * 0x1.715476p+0f);          // log2(e)

@@ -402,6 +402,11 @@ __device__ __forceinline__ KeyIdx wave_argmax(float v, int i) {
           __builtin_amdgcn_readlane(i, 63)};
 }
 
+// Value of lane k (k wave-uniform): a scalar read, no LDS round trip.
+__device__ __forceinline__ float lane_f32(float v, int k) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k));
+}
+
 // Top-2 values of (t1, t2) pairs under fmaxf/fminf (inputs never NaN).
 template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ void top2_step(float& t1, float& t2) {
@@ -680,10 +685,10 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     float wv = 0.f;
     if (order == MOE_ORDER_TOPK_ACT) {
       if (scoring == MOE_SCORING_SOFTMAX) {
-        float m0 = __shfl(my_key, 0, 64);
+        float m0 = lane_f32(my_key, 0);
         float ex = (lane < K) ? det_exp_f32(my_key - m0) : 0.f;
         float sum = 0.f;
-        for (int k = 0; k < K; ++k) sum += __shfl(ex, k, 64);
+        for (int k = 0; k < K; ++k) sum += lane_f32(ex, k);
         wv = ex / sum;
       } else {
         wv = (lane < K) ? det_sigmoid_f32(my_key) : 0.f;
@@ -693,7 +698,7 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     }
     if (renorm) {
       float sum = 0.f;
-      for (int k = 0; k < K; ++k) sum += __shfl(wv, k, 64);
+      for (int k = 0; k < K; ++k) sum += lane_f32(wv, k);
       float den = sum + eps;
       wv = wv / den;
     }
