@@ -330,3 +330,40 @@ def test_gpt_oss_moe_block_tkg_mx_api(cuda, gpt_oss_weights):
     err = rel_l2(np_f32(out.reshape(T, -1))[sel], ref)
     say("moe_block_tkg mx rel_l2", err)
     assert err <= TOL_REL_L2, err
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_gpt_oss_layer_captures_in_hip_graph(cuda, gpt_oss_weights, T):
+    """The GPT-OSS layer forward (norm with the residual add, router with the MXFP8
+    quantization in its launch, top-k ending in the mapping, MX experts, combine)
+    recorded into a HIP graph: three replays on new inputs, with eager work and
+    synchronizations between them, each equal to an eager run bit for bit."""
+    from vllm_neuron_amd import MXFP4MoE
+    c = GPT_OSS
+    say("gpt-oss hip graph", T)
+    g = torch.Generator().manual_seed(40 + T)
+    gamma = torch.zeros(c["H"])
+    gamma[:c["h_real"]] = 1 + 0.1 * torch.randn(c["h_real"], generator=g)
+    layer = MXFP4MoE(gpt_oss_weights, c["K"], norm_weight=gamma.to(cuda), eps=1e-5,
+                     hidden_actual=c["h_real"])
+    sx = _padded_hidden(T, 300 + T, cuda)
+    sr = _padded_hidden(T, 400 + T, cuda)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):  # warm up the allocator and the library outside the capture
+            layer(sx, None, False, None, residual=sr)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout, gsum = layer(sx, None, False, None, residual=sr)
+    for i in range(3):
+        x = _padded_hidden(T, 500 + 10 * T + i, cuda)
+        r = _padded_hidden(T, 600 + 10 * T + i, cuda)
+        ref_out, ref_sum = layer(x, None, False, None, residual=r)
+        torch.cuda.synchronize()
+        sx.copy_(x)
+        sr.copy_(r)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, ref_out) and torch.equal(gsum, ref_sum), i
