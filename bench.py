@@ -18,8 +18,10 @@ Phases:
      (64 tokens, hidden 1024, 8 experts, top-2), Kimi-K2 over 1..16384 tokens
      (1 token also with 32 inputs cycled so the weights do not stay in the 256 MB
      MALL), GLM-4.5 with Zipf-skewed routing, and the GPT-OSS-120B layer with
-     MXFP4 experts; and under "cpu_extra" the oracle timed on the small layer in
-     the reference's dense all-experts form and on token samples of each layer.
+     MXFP4 experts (up to 64 tokens also "graph_ms_per_step": the same call replayed
+     from a HIP graph, timed on the GPU's clock without the host's launch cost); and under
+     "cpu_extra" the oracle timed on the small layer in the reference's dense
+     all-experts form and on token samples of each layer.
 Prints one JSON line.
 """
 import argparse
@@ -123,22 +125,58 @@ def time_layer(x, w, cfg, steps, warmup, torch, ops):
     return (time.perf_counter() - t0) / steps
 
 
+def graph_ms(fn, reps, torch):
+    """Device time per call of fn replayed from a HIP graph: two warm-up calls on a
+    side stream, one capture, then `reps` replays queued behind a short spin kernel
+    (so the host's launch cost stays off the GPU's timeline) and timed with HIP
+    events on the replay stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(20_000_000)  # ~10 ms of GPU spin while the replays are queued
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del g
+    torch.cuda.empty_cache()
+    return round(ms, 4)
+
+
 def workload_report(name, x, w, cfg, steps, torch, ops):
-    """Whole-layer timing of one extra workload with its algorithmic roofline."""
+    """Whole-layer timing of one extra workload with its algorithmic roofline (and, up to
+    64 tokens, the device time of the same call replayed from a HIP graph)."""
     T = x.shape[0]
     H, I, E = cfg.hidden, cfg.intermediate, cfg.n_experts
     sec = time_layer(x, w, cfg, steps, 2, torch, ops)
+    gms = graph_ms(lambda: ops.layer_forward(x, w, cfg), max(steps, 20), torch) if T <= 64 else None
     ids = ops.layer_forward(x, w, cfg, return_routing=True)[1]
     active, rows = layer_counts(ids, E)
     flops = 2 * (rows + T * cfg.n_shared) * 3 * H * I + 2 * T * H * E
     nbytes = ((active + cfg.n_shared) * (expert_bytes(H, I, "gate_up") + expert_bytes(H, I, "down"))
               + E * H * 2 + T * H * 2 * 2)
-    return {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
-            "tokens_per_s": round(T / sec, 1), "active_experts": active,
-            "alg_bytes": nbytes, "alg_flops": flops,
-            "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
-            "mfma_frac": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4),
-            "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
+    rep = {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
+           "tokens_per_s": round(T / sec, 1), "active_experts": active,
+           "alg_bytes": nbytes, "alg_flops": flops,
+           "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "mfma_frac": round(flops / sec / 1e12 / FP8_PEAK_TFLOPS, 4),
+           "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9), flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
+    if gms is not None:
+        rep["graph_ms_per_step"] = gms
+        rep["graph_hbm_frac"] = round(nbytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    return rep
 
 
 def run_prologue(calls, torch, ops, dev, H=7168):
@@ -199,6 +237,7 @@ def mx_report(name, layer, x, steps, torch):
         layer(x, None, True, None)
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
+    gms = graph_ms(lambda: layer(x, None, True, None), max(steps, 20), torch) if T <= 64 else None
     from vllm_neuron_amd import ops
     ids = ops.layer_forward_mx(x, w, layer.top_k, layer.act, layer.limits[:2], layer.limits[2:],
                                return_routing=True, gamma=layer.norm_weight, eps=layer.rms_norm_eps,
@@ -208,12 +247,16 @@ def mx_report(name, layer, x, steps, torch):
     per_expert = 3 * H * I // 2 + 3 * H * I // 32 + 4 * (2 * I + H)
     nbytes = active * per_expert + E * H * 2 + T * H * 2 * 2
     flops = 2 * rows * 3 * hr * hr + 2 * T * H * E
-    return {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
-            "tokens_per_s": round(T / sec, 1), "active_experts": active,
-            "alg_bytes": nbytes, "alg_flops": flops,
-            "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
-            "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9),
-                                       flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
+    rep = {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
+           "tokens_per_s": round(T / sec, 1), "active_experts": active,
+           "alg_bytes": nbytes, "alg_flops": flops,
+           "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "roofline_frac": round(max(nbytes / (HBM_PEAK_GBS * 1e9),
+                                      flops / (FP8_PEAK_TFLOPS * 1e12)) / sec, 4)}
+    if gms is not None:
+        rep["graph_ms_per_step"] = gms
+        rep["graph_hbm_frac"] = round(nbytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    return rep
 
 
 def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev, cpu_tokens):
