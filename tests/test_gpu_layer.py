@@ -50,6 +50,33 @@ def _check_layer(cfg, w, x, tokens=None, tag=""):
     return out
 
 
+def _op_path(cfg, w, x):
+    """The layer of a grouped-routing config run op by op through the C-ABI entry points
+    (router logits with their own reduce, top-k, the chunked or one-launch mapping, the
+    1x128 quantizer, the expert kernels the layer picks, combine). The layer fuses the
+    quantization into its router launch and, at decode sizes, the mapping into its top-k
+    launch; every output must be the same bits."""
+    T = x.shape[0]
+    E, K, B = cfg.n_experts, cfg.top_k, cfg.block_size
+    lg = ops.router_logits(x, w.router_w, w.router_bias)
+    ids, wts = ops.router_topk(lg, K, ops.ORDER_GROUPED, cfg.scoring, cfg.n_group, cfg.topk_group,
+                               w.corr_bias, cfg.renorm, 1e-20, cfg.routed_scaling)
+    m = ops.blockwise_mapping(ids=ids, n_experts=E, block_size=B)
+    tpid, b2e = m["token_position_to_id"], m["block_to_expert"]
+    NB = tpid.numel()
+    xq, xs = ops.act_quant(x)
+    if ops.use_block_kernels(T, K, E):
+        tiles, num, mbt = ops.build_block_tiles(tpid, b2e, B, T, K, E, cfg.n_shared)
+        hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mbt)
+        y = ops.expert_down_block(hq, hs, w, T, NB, tiles, num, mbt)
+    else:
+        mt = ops.choose_mt(T, K, E)
+        tiles, num, mx = ops.build_tiles(tpid, b2e, B, T, K, E, cfg.n_shared, mt)
+        hq, hs = ops.expert_gate_up(xq, xs, w, tpid, NB, tiles, num, mx, mt)
+        y = ops.expert_down(hq, hs, w, T, NB, tiles, num, mx, mt)
+    return ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, cfg.n_shared)
+
+
 def test_layer_small_config(cuda):
     """64 tokens, H 1024, I 512, 8 experts, softmax top-2, no shared expert."""
     cfg = PRESETS["small"]
@@ -180,7 +207,9 @@ def test_layer_dsv3_full_size(cuda, T, idx, tokens):
     ids = ops.layer_forward(x, w, cfg, return_routing=True)[1].cpu().numpy()
     tokens, experts = _tile_tokens(ids, cfg.n_experts, extra=tokens)
     say("dsv3 tokens", tokens, "experts", experts)
-    _check_layer(cfg, w, x, tokens=tokens, tag=f"dsv3 T={T}")
+    out = _check_layer(cfg, w, x, tokens=tokens, tag=f"dsv3 T={T}")
+    if T <= 256:  # every token: the op-by-op path gives the same bits
+        assert torch.equal(out, _op_path(cfg, w, x))
     del w
     torch.cuda.empty_cache()
 
@@ -295,14 +324,17 @@ def test_layer_kimi_k2_full_size(cuda, kimi_weights, T):
     its whole token sweep: 1 and 16 tokens (16-row tiles), 256 (32-row tiles), 2048
     (block kernels on mostly one partial tile per expert, ~43 rows) and 16384 (block
     kernels, ~341 rows per expert). The oracle checks the first and last token and the
-    tokens in the last slot of experts whose last tiles cover every 64-row band."""
+    tokens in the last slot of experts whose last tiles cover every 64-row band; up to
+    2048 tokens every token also equals the op-by-op path bit for bit."""
     cfg = PRESETS["kimi_k2"]
     say("layer kimi-k2 full", T)
     x = synthetic.hidden_states(T, cfg.hidden, 3).to(cuda)
     ids = ops.layer_forward(x, kimi_weights, cfg, return_routing=True)[1].cpu().numpy()
     tokens, experts = _tile_tokens(ids, cfg.n_experts, extra=(0, T - 1))
     say("kimi tokens", tokens, "experts", experts)
-    _check_layer(cfg, kimi_weights, x, tokens=tokens, tag=f"kimi T={T}")
+    out = _check_layer(cfg, kimi_weights, x, tokens=tokens, tag=f"kimi T={T}")
+    if T <= 2048:  # every token: the op-by-op path gives the same bits
+        assert torch.equal(out, _op_path(cfg, kimi_weights, x))
 
 
 def test_layer_glm45_full_size_zipf(cuda):
