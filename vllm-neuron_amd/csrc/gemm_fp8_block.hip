@@ -210,8 +210,9 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
     wb = (is_sh ? p.wsh : p.w) + (size_t)ej * p.H * p.I;
     wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (p.H / 128) * KB;
   }
-  // Loader: 64 regions of 1 KB (A: 32, B: 32), 8 per wave: A regions 4w..4w+3
-  // and B regions 4w..4w+3. Lane l writes region byte l*16 = row l/8, stored
+  // Loader: regions of 1 KB, B: 32 (regions 4w..4w+3 of wave w), A: 8 MF (the
+  // tile's 64 MF rows, regions MF w..MF w + MF - 1; a partial tile loads no rows
+  // its row groups do not read). Lane l writes region byte l*16 = row l/8, stored
   // chunk l%8.
   uint32_t off[kDmaPerWave];
 #pragma unroll
@@ -254,11 +255,11 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
     // down: tile row r is h row rbase + r, so block 0's A tile and scales need no
     // lookup and join the first round trip
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 8 * (4 * wave + i) + (lane >> 3);
+    for (int i = 0; i < MF; ++i) {
+      const int row = 8 * (MF * wave + i) + (lane >> 3);
       const uint32_t rs = (uint32_t)(row < nrows ? rbase + row : rbase);
       off[i] = rs * (uint32_t)Kdim + (uint32_t)(swz(row, lane & 7) * 16);
-      load_lds16(p.a + off[i], sTA + (4 * wave + i) * 1024);
+      load_lds16(p.a + off[i], sTA + (MF * wave + i) * 1024);
     }
     const uint32_t rs = (uint32_t)(srow < nrows ? rbase + srow : rbase);
     if (sgrp)
@@ -280,8 +281,8 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   lds_barrier();
   if constexpr (KIND == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 8 * (4 * wave + i) + (lane >> 3);
+    for (int i = 0; i < MF; ++i) {
+      const int row = 8 * (MF * wave + i) + (lane >> 3);
       const int rs = __float_as_int(lds_f32(lds_addr(sSrc) + 4 * row));
       off[i] = (uint32_t)(rs >= 0 ? rs : 0) * (uint32_t)Kdim + (uint32_t)(swz(row, lane & 7) * 16);
     }
@@ -318,13 +319,13 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // rows past the tile's end re-read row 0, never stored) and the B group (the
   // block's activation scales, then the B tile: exactly kBGroup loads per wave).
   // Fixed counts keep every vmcnt wait exact.
-  constexpr int kAGroup = 4;
+  constexpr int kAGroup = MF;  // the tile's 64 MF rows: MF 1 KB loads per wave
   constexpr int kBLoads = kDmaPerWave - 4;
   constexpr int kBGroup = kBLoads + 1;
   auto issue_a = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < kAGroup; ++i)
-      load_lds16(abase + off[i] + (size_t)kb * kBK, sTA + (4 * wave + i) * 1024);
+      load_lds16(abase + off[i] + (size_t)kb * kBK, sTA + (MF * wave + i) * 1024);
   };
   // Load i of block kb's B group into stage sb (i = 0: the scales; grouped, only
   // at a group's first block, otherwise a 4-byte load of one line into the
