@@ -406,8 +406,24 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   };
 
   // Ratios of block kb + 1 (scales of block kb + 1 landed) into sr.
+  // Grouped scales: the writer's row holds four blocks' scales in one 16-byte piece;
+  // the piece is read whole at each group's first block (64 lanes, 1 KB contiguous:
+  // conflict-free) and kept, instead of one 4-byte read per block (16-byte lane
+  // stride: four lanes per bank).
+  v4i s4 = {0, 0, 0, 0};
   auto store_ratio = [&](float* sr, int kb) {
-    (shalf ? sr + kBM : sr)[srow] = ratio(lds_f32(sa_own(kb)), sW[shalf][kb]);
+    float sa;
+    if (sgrp) {
+      if ((kb & 3) == 0) {
+        lds_v4_issue<0>(sa_own(kb), s4);
+        lds_v4_wait(s4);
+      }
+      const int k3 = kb & 3;
+      sa = __int_as_float(k3 == 0 ? s4.x : k3 == 1 ? s4.y : k3 == 2 ? s4.z : s4.w);
+    } else {
+      sa = lds_f32(sa_own(kb));
+    }
+    (shalf ? sr + kBM : sr)[srow] = ratio(sa, sW[shalf][kb]);
   };
 
   // One K step: the MFMAs of block kb (B tile in stage cb, ratios in cr). On entry
