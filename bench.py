@@ -480,7 +480,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "expert_gemm_kernel gate_up (decode)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("expert_gemm_kernel<16,0,3>", "decode64"),
+                     "traffic": measured_traffic("expert_gemm_kernel<16,0,3,4>", "decode64"),
                      "alg_bytes_per_launch": gu_bytes, "avg_launch_ms": round(gu_ms, 4)},
         "layer": {"alg_bytes": layer_bytes, "alg_flops": layer_flops,
                   "hbm_GBs": round(layer_bytes / sec / 1e9, 1),
