@@ -88,8 +88,8 @@ __global__ __launch_bounds__(1024) void map_small_kernel(
   __shared__ int s_cex[kMapMaxE];
   __shared__ int s_tile[kMapMaxE];
   __shared__ int s_wave[16];
-  map_small_body(ids, T, K, E, B, N, tpid, block_to_expert, conditions, expert_counts, inv_pos, ws,
-                 to, bm, s_blk, s_cnt, s_cex, s_tile, s_wave);
+  map_small_body(ids, nullptr, T, K, E, B, N, tpid, block_to_expert, conditions, expert_counts,
+                 inv_pos, ws, to, bm, s_blk, s_cnt, s_cex, s_tile, s_wave);
 }
 
 // inv_rows: inv_pos receives compact rows (count_off[e] + rank in the expert)

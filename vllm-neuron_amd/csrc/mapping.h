@@ -198,26 +198,66 @@ static __device__ void finish_mapping(int T, int E, int B, int N, int run, int32
 
 // The whole mapping in one workgroup of 1024 threads, for ids and at most one
 // 256-token chunk (decode): fill, bitmask, counts, scan, tiles and scatter. The LDS
-// arrays hold E entries (bm: E rows of 8 words); s_wave holds 16.
-static __device__ void map_small_body(const int32_t* __restrict__ ids, int T, int K, int E, int B,
-                                      int N, int32_t* __restrict__ tpid,
+// arrays hold E entries (bm: E rows of 8 words); s_wave holds 16. s_ids (optional):
+// the T*K ids already in this workgroup's LDS.
+static __device__ void map_small_body(const int32_t* __restrict__ ids, const int* s_ids, int T, int K,
+                                      int E, int B, int N, int32_t* __restrict__ tpid,
                                       int32_t* __restrict__ block_to_expert,
                                       int32_t* __restrict__ conditions,
                                       int32_t* __restrict__ expert_counts,
                                       int32_t* __restrict__ inv_pos, const MapWs& ws,
                                       const TileOut& to, uint32_t (*bm)[8], int* s_blk, int* s_cnt,
                                       int* s_cex, int* s_tile, int* s_wave) {
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int TK = T * K;
   const long nb_total = (long)N * B;
-  long filled = 0;
-  if (((uintptr_t)tpid & 15) == 0) {  // 16-byte stores while they fit
-    filled = nb_total & ~3L;
-    for (long i = tid; i < filled / 4; i += blockDim.x) ((int4*)tpid)[i] = make_int4(-1, -1, -1, -1);
+  // Up to 2 pairs per thread (i = tid + u * nthr) the ids live in registers, loaded
+  // before this body stores anything: every later wait for them would also wait
+  // for the stores issued before it (stores count in vmcnt), and no global load
+  // follows the fill.
+  const bool reg = TK <= 2 * nthr;  // workgroup-uniform
+  int my_e[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int i = tid + u * nthr;
+    my_e[u] = -1;
+    if (reg && i < TK) my_e[u] = (s_ids != nullptr) ? s_ids[i] : ids[i];
   }
-  for (long i = filled + tid; i < nb_total; i += blockDim.x) tpid[i] = -1;
-  if (tid == 0) ws.status[0] = 0;
-  __syncthreads();  // the fill and the status reset land before the scatter below
-  build_chunk_mask(bm, ids, nullptr, T, K, E, 0, ws.status);
+  auto fill = [&]() {
+    long filled = 0;
+    if (((uintptr_t)tpid & 15) == 0) {  // 16-byte stores while they fit
+      filled = nb_total & ~3L;
+      for (long i = tid; i < filled / 4; i += nthr) ((int4*)tpid)[i] = make_int4(-1, -1, -1, -1);
+    }
+    for (long i = filled + tid; i < nb_total; i += nthr) tpid[i] = -1;
+  };
+  if (reg) {
+    // bitmask and count of ids >= E from the registers, then the fill; the
+    // barriers below order the fill and the status store before the scatter
+    for (int i = tid; i < E * 8; i += nthr) bm[i >> 3][i & 7] = 0u;
+    if (tid == 0) s_wave[0] = 0;
+    __syncthreads();
+    int drop = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + u * nthr, e = my_e[u];
+      if (i < TK) {
+        const int tl = i / K;
+        if (e >= 0 && e < E) atomicOr(&bm[e][tl >> 5], 1u << (tl & 31));
+        else if (e >= E) ++drop;
+      }
+    }
+    if (drop != 0) atomicAdd(&s_wave[0], drop);
+    fill();
+    __syncthreads();
+    // s_wave[0] is next written by lane 63 of this same wave (the scans below)
+    if (tid == 0) ws.status[0] = s_wave[0];
+  } else {
+    fill();
+    if (tid == 0) ws.status[0] = 0;
+    __syncthreads();  // the fill and the status reset land before the scatter below
+    build_chunk_mask(bm, ids, nullptr, T, K, E, 0, ws.status);
+  }
   int run = 0;
   if (tid < E) {
 #pragma unroll
@@ -225,9 +265,8 @@ static __device__ void map_small_body(const int32_t* __restrict__ ids, int T, in
   }
   finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off,
                  nullptr, to, s_blk, s_cnt, s_cex, s_tile, s_wave);
-  for (int i = tid; i < T * K; i += blockDim.x) {
+  auto scatter = [&](int i, int e) {
     const int t = i / K;
-    const int e = ids[i];
     int out = -1;
     if (e >= 0 && e < E) {
       int rank = 0;
@@ -243,6 +282,13 @@ static __device__ void map_small_body(const int32_t* __restrict__ ids, int T, in
       }
     }
     if (inv_pos != nullptr) inv_pos[i] = out;
+  };
+  if (reg) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (tid + u * nthr < TK) scatter(tid + u * nthr, my_e[u]);
+  } else {
+    for (int i = tid; i < TK; i += nthr) scatter(i, ids[i]);
   }
 }
 

@@ -434,6 +434,9 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     float* __restrict__ logits_out, int tpb, MapJob mj) {
   __shared__ float s_act[4][PM * 64];
   __shared__ float s_key[4][PM * 64];
+  // one workgroup (one token) ending in the mapping: its ids also go to LDS
+  __shared__ int s_ids[MAP ? 64 : 1];
+  const bool lds_ids = MAP && gridDim.x == 1 && T * K <= 64;  // workgroup-uniform
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t0 = blockIdx.x * tpb, t = t0 + wave;
   const int P = (E + 63) / 64;
@@ -707,6 +710,7 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     if (lane < K) {
       ids[(size_t)t * K + lane] = my_id;
       weights[(size_t)t * K + lane] = wv;
+      if (lds_ids) s_ids[t * K + lane] = my_id;
     }
     if (aff != nullptr) {
 #pragma unroll
@@ -741,8 +745,8 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
       __syncthreads();
       if (!s_last) return;  // whole workgroup
     }
-    map_small_body(ids, T, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond, mj.counts, mj.inv, mj.ws,
-                   mj.to, s_bm, s_blk, s_cnt, s_cex, s_tile, s_wave);
+    map_small_body(ids, lds_ids ? s_ids : nullptr, T, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond,
+                   mj.counts, mj.inv, mj.ws, mj.to, s_bm, s_blk, s_cnt, s_cex, s_tile, s_wave);
   }
 }
 
