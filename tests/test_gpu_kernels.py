@@ -180,7 +180,8 @@ def test_router_grouped_nonfinite_group_scores(cuda, gs):
 
 
 MAP_CASES = [(1, 8, 256, 256), (7, 2, 8, 4), (64, 2, 8, 256), (64, 8, 256, 256), (300, 8, 160, 16),
-             (4096, 8, 160, 256), (8192, 8, 256, 256), (1000, 6, 384, 64), (513, 1, 5, 1)]
+             (4096, 8, 160, 256), (8192, 8, 256, 256), (1000, 6, 384, 64), (513, 1, 5, 1),
+             (256, 16, 64, 32), (200, 12, 96, 8)]  # one chunk, more than 2 ids per thread
 
 
 @pytest.mark.parametrize("T,K,E,B", MAP_CASES)
