@@ -124,7 +124,7 @@ def test_opcheck_layer_and_operators(cuda):
                           test_utils=utils)
 
 
-@pytest.mark.parametrize("T", [64, 2048])
+@pytest.mark.parametrize("T", [1, 64, 2048])  # 1: the one-workgroup top-k and mapping
 def test_layer_captures_in_hip_graph(cuda, T):
     """The layer forward (norm, residual add, router, mapping, experts, combine)
     recorded into a HIP graph: three replays on new inputs, with eager work and
