@@ -34,11 +34,11 @@ def test_noalloc_matches_workspace_entry(cuda):
 
 
 def test_noalloc_dsv3_decode_and_limit(cuda):
-    """DeepSeek-V3 decode (64 tokens, then 8) on the static scratch; a call whose
+    """DeepSeek-V3 decode (64 tokens, then 8, then 1) on the static scratch; a call whose
     workspace exceeds the scratch is refused before any work is queued."""
     cfg = PRESETS["dsv3"]
     w = synthetic.make_weights(cfg, 1, device=cuda, experts_device=cuda)
-    for T in (64, 8):
+    for T in (64, 8, 1):
         say("noalloc dsv3", T)
         x = synthetic.hidden_states(T, cfg.hidden, 1).to(cuda)
         _same(ops.layer_forward_noalloc(x, w, cfg, return_routing=True),
