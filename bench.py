@@ -13,13 +13,16 @@ Phases:
   B  K steps of the same kernels launched one by one, with HIP events around the
      two expert GEMMs on the launch stream, for the per-kernel roofline.
   C  the same layer at prefill (8192 tokens), reported under "prefill8k".
-  D  the CPU oracle on a bounded token sample (rank 0, N = 1 only).
+  D  the CPU oracle on a bounded token sample (rank 0, N = 1 only): median of 3
+     timed runs after one warm-up.
   E  (unless --no-extra) the other workloads, under "extra": the small layer
      (64 tokens, hidden 1024, 8 experts, top-2), Kimi-K2 over 1..16384 tokens
      (1 token also with 32 inputs cycled so the weights do not stay in the 256 MB
      MALL), GLM-4.5 with Zipf-skewed routing, and the GPT-OSS-120B layer with
      MXFP4 experts (up to 64 tokens also "graph_ms_per_step": the same call replayed
-     from a HIP graph, timed on the GPU's clock without the host's launch cost); and under
+     from a HIP graph, timed on the GPU's clock without the host's launch cost, and
+     "flushed_ms_per_step": each call after a 1 GiB fill that evicts the weights from
+     L2 and the MALL, timed with HIP events); and under
      "cpu_extra" the oracle timed on the small layer in the reference's dense
      all-experts form and on token samples of each layer.
 Prints one JSON line.
@@ -155,6 +158,31 @@ def graph_ms(fn, reps, torch):
     return round(ms, 4)
 
 
+def flushed_ms(fn, steps, torch):
+    """Device time per call of fn with the caches cold: before each call a 1 GiB fill
+    evicts the weights from L2 and the 256 MB MALL, then a short spin kernel lets the
+    host queue the call, which HIP events on the launch stream bracket. Median over
+    `steps` calls."""
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    fn()
+    torch.cuda.synchronize()
+    ev = []
+    for i in range(steps):
+        buf.fill_(i & 0xFF)
+        torch.cuda._sleep(400_000)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        ev.append((e0, e1))
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in ev)
+    del buf
+    torch.cuda.empty_cache()
+    return round(ts[len(ts) // 2], 4)
+
+
 def workload_report(name, x, w, cfg, steps, torch, ops):
     """Whole-layer timing of one extra workload with its algorithmic roofline (and, up to
     64 tokens, the device time of the same call replayed from a HIP graph)."""
@@ -162,6 +190,7 @@ def workload_report(name, x, w, cfg, steps, torch, ops):
     H, I, E = cfg.hidden, cfg.intermediate, cfg.n_experts
     sec = time_layer(x, w, cfg, steps, 2, torch, ops)
     gms = graph_ms(lambda: ops.layer_forward(x, w, cfg), max(steps, 20), torch) if T <= 64 else None
+    fms = flushed_ms(lambda: ops.layer_forward(x, w, cfg), max(steps, 20), torch) if T <= 64 else None
     ids = ops.layer_forward(x, w, cfg, return_routing=True)[1]
     active, rows = layer_counts(ids, E)
     flops = 2 * (rows + T * cfg.n_shared) * 3 * H * I + 2 * T * H * E
@@ -176,6 +205,9 @@ def workload_report(name, x, w, cfg, steps, torch, ops):
     if gms is not None:
         rep["graph_ms_per_step"] = gms
         rep["graph_hbm_frac"] = round(nbytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if fms is not None:
+        rep["flushed_ms_per_step"] = fms
+        rep["flushed_hbm_frac"] = round(nbytes / (fms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     return rep
 
 
@@ -238,6 +270,7 @@ def mx_report(name, layer, x, steps, torch):
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
     gms = graph_ms(lambda: layer(x, None, True, None), max(steps, 20), torch) if T <= 64 else None
+    fms = flushed_ms(lambda: layer(x, None, True, None), max(steps, 20), torch) if T <= 64 else None
     from vllm_neuron_amd import ops
     ids = ops.layer_forward_mx(x, w, layer.top_k, layer.act, layer.limits[:2], layer.limits[2:],
                                return_routing=True, gamma=layer.norm_weight, eps=layer.rms_norm_eps,
@@ -256,6 +289,9 @@ def mx_report(name, layer, x, steps, torch):
     if gms is not None:
         rep["graph_ms_per_step"] = gms
         rep["graph_hbm_frac"] = round(nbytes / (gms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if fms is not None:
+        rep["flushed_ms_per_step"] = fms
+        rep["flushed_hbm_frac"] = round(nbytes / (fms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     return rep
 
 
@@ -334,20 +370,22 @@ def _route_cpu(cfg, lg, w):
     return R.route_topk_act(lg, cfg.top_k, sc, cfg.renorm, 1e-20, cfg.routed_scaling)
 
 
-def cpu_baseline(x, w, cfg, n_tokens):
+def cpu_baseline(x, w, cfg, n_tokens, reps=3):
     """The oracle (numpy, fp32; sparse per-expert form: router, top-k, each routed
     expert's weights dequantized and applied to its tokens, weighted combine) on
-    the first n_tokens tokens of the workload. Returns (tokens/s, experts, seconds)."""
+    the first n_tokens tokens of the workload, the weights already in host memory.
+    One warm-up run, then the median of `reps` timed runs.
+    Returns (tokens/s, experts, median seconds, all timed seconds)."""
     import numpy as np
     import torch
     from oracle import router as R
     from oracle.moe import moe_sparse_fp8
     xs = x[:n_tokens].float().cpu().numpy()
-    t0 = time.perf_counter()
     rb = None if w.router_bias is None else w.router_bias.float().cpu().numpy()
-    lg = R.router_logits(xs, w.router_w.float().cpu().numpy(), rb)
-    ids, wts = _route_cpu(cfg, lg, w)
-    experts = sorted(set(np.unique(ids).tolist()))
+    rw = w.router_w.float().cpu().numpy()
+    lg = R.router_logits(xs, rw, rb)
+    ids0, _ = _route_cpu(cfg, lg, w)
+    experts = sorted(set(np.unique(ids0).tolist()))
     q13 = {e: w.w13[e].view(torch.uint8).cpu().numpy() for e in experts}
     s13 = {e: w.w13_scale[e].cpu().numpy() for e in experts}
     q2 = {e: w.w2[e].view(torch.uint8).cpu().numpy() for e in experts}
@@ -360,16 +398,27 @@ def cpu_baseline(x, w, cfg, n_tokens):
     class _D(dict):
         shape = (cfg.n_experts,)
 
-    moe_sparse_fp8(xs, ids, wts, _D(q13), _D(s13), _D(q2), _D(s2), shared=sh, experts=experts)
-    dt = time.perf_counter() - t0
-    return n_tokens / dt, len(experts), dt
+    def run():
+        lg = R.router_logits(xs, rw, rb)
+        ids, wts = _route_cpu(cfg, lg, w)
+        moe_sparse_fp8(xs, ids, wts, _D(q13), _D(s13), _D(q2), _D(s2), shared=sh, experts=experts)
+
+    run()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[len(times) // 2]
+    return n_tokens / dt, len(experts), dt, times
 
 
 def oracle_sample(name, x, w, cfg, n_tokens):
     print(f"[bench] cpu: {name}, {n_tokens} tokens", file=sys.stderr, flush=True)
-    tps, nexp, dt = cpu_baseline(x, w, cfg, n_tokens)
+    tps, nexp, dt, times = cpu_baseline(x, w, cfg, n_tokens)
     return {"workload": name, "form": "sparse per-expert (oracle)", "tokens": n_tokens,
             "routed_experts": nexp, "seconds": round(dt, 3), "tokens_per_s": round(tps, 3),
+            "runs_s": [round(t, 3) for t in times], "timing": "median of 3 after 1 warm-up",
             "cores": cpu_threads()}
 
 
@@ -416,7 +465,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--cpu-tokens", type=int, default=2)
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the other workloads (small, Kimi-K2 sweep, GLM-4.5 Zipf, GPT-OSS "
                          "MXFP4) and the CPU samples of them")
@@ -516,12 +565,14 @@ def main():
     # ---- D: CPU oracle on a bounded sample
     if args.cpu_tokens > 0:
         print("[bench] phase D: CPU oracle sample", file=sys.stderr, flush=True)
-        tps, nexp, dt = cpu_baseline(x, w, cfg, args.cpu_tokens)
+        tps, nexp, dt, times = cpu_baseline(x, w, cfg, args.cpu_tokens)
         cores = cpu_threads()
         result["cpu_baseline"] = {
             "value": round(tps, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"first {args.cpu_tokens} of the 64 decode tokens ({nexp} routed experts + shared, "
-                      f"full layer math incl. per-expert dequant), numpy fp32 BLAS, {dt:.1f} s"}
+                      f"full layer math incl. per-expert dequant), numpy fp32 BLAS; median of 3 "
+                      f"timed runs after 1 warm-up: {dt:.2f} s (runs "
+                      f"{', '.join(f'{t:.2f}' for t in times)} s)"}
     if not args.no_extra:
         del w
         torch.cuda.empty_cache()

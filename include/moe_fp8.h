@@ -252,8 +252,10 @@ int moe_layer_forward(const void* x_bf16, const void* residual_bf16, const float
 /* moe_layer_forward without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops that
  * forbid allocation). No counterpart in the reference. Its workspace is a static
- * device array of MOE_NOALLOC_SCRATCH_BYTES, one per GPU, held from the first
- * call on that GPU until the process ends; the call allocates nothing. Calls
+ * device array of MOE_NOALLOC_SCRATCH_BYTES, one per GPU, reserved when the
+ * library's code object loads on that GPU (whether or not this entry is ever
+ * called, so it costs 64 MiB per GPU also to callers that only use the workspace
+ * entry points) and held until the process ends; the call allocates nothing. Calls
  * whose moe_layer_workspace_bytes exceeds it return MOE_ERR_UNSUPPORTED (64 MiB
  * covers the DeepSeek-V3 / Kimi-K2 layers up to about 320 tokens). All calls on
  * one GPU share the array: calls that overlap on one GPU (unordered streams,
@@ -296,7 +298,8 @@ int moe_layer_forward_noalloc(const void* x_bf16, const void* residual_bf16, con
 int moe_act_quant_mx(const void* x_bf16, int rows, int cols, uint8_t* q, uint8_t* scales,
                      void* stream);
 
-/* MX gate_up over row tiles (tiles as moe_build_tiles): gate = clamp(x W_g^T + b_g,
+/* MX gate_up over row tiles (tiles as moe_build_tiles, mt in {16, 32, 64}; 128
+ * returns MOE_ERR_UNSUPPORTED): gate = clamp(x W_g^T + b_g,
  * gate_lo, gate_hi), up = clamp(x W_u^T + b_u, up_lo, up_hi) (NaN limit = none),
  * h = act(gate) * up, written MXFP8-quantized per 32 columns (hq [rows, I] codes,
  * hs [rows, I/32] scale bytes). Replaces the gate/up half of nkilib's
@@ -311,7 +314,8 @@ int moe_expert_gate_up_mx(const uint8_t* xq, const uint8_t* xs, int T, int H, in
                           float gate_hi, float up_lo, float up_hi, uint8_t* hq, uint8_t* hs,
                           void* stream);
 
-/* MX down: y[row, :H] = bf16(h W_d^T + b_d) per tile row (unweighted). Replaces the
+/* MX down: y[row, :H] = bf16(h W_d^T + b_d) per tile row (unweighted; mt as the MX
+ * gate_up). Replaces the
  * down projection and its bias of moe_cte (moe_cte.py:585-591). */
 int moe_expert_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E, int wfmt,
                        const uint8_t* w2, const uint8_t* w2_scale, const float* b2,
@@ -375,15 +379,15 @@ int moe_selftest_bf16_encode(uint32_t first, uint32_t count, uint32_t* out, int 
  * the quantizer's scale max(amax, 1e-10) / 448 as divisor. Mode 1: u seeds a
  * random fp32 amax in [2^-40, 2^40) and a value of magnitude at most amax.
  * Output as moe_selftest_fp8_encode. No reference counterpart. */
+int moe_selftest_quant_div(int mode, uint32_t first, uint32_t count, uint32_t* out, int blocks,
+                           void* stream);
+
 /* One scaled MFMA with the MX GEMMs' lane mapping: c[16,16] = A . B^T with A
  * [16,128] fp8 codes and scale bytes sa [16,4], B [16,128] values as fp4 (packed
  * [16,64] bytes) or fp8 ([16,128]) with sb [16,4]. No reference counterpart: it
  * pins the gfx950 scaled-MFMA data and scale layout for the tests. */
 int moe_selftest_mfma_mx(const uint8_t* a, const uint8_t* sa, const uint8_t* b, const uint8_t* sb,
                          int wfmt, float* c, void* stream);
-
-int moe_selftest_quant_div(int mode, uint32_t first, uint32_t count, uint32_t* out, int blocks,
-                           void* stream);
 
 #ifdef __cplusplus
 }

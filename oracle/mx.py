@@ -140,12 +140,14 @@ def expert_mlp_mx(xhat, w13hat, b13, w2hat, b2, act="swish", gate_limits=(None, 
 
 
 def moe_sparse_mx(x, ids, w, w13_packed, w13_scale, b13, w2_packed, w2_scale, b2,
-                  act="swish", gate_limits=(None, None), up_limits=(None, None), experts=None):
+                  act="swish", gate_limits=(None, None), up_limits=(None, None), experts=None,
+                  requant_h=True):
     """Layer output (fp32, before the final cast) with MXFP4 experts and MXFP8
     activations: x [T, H] float32 holding bf16 values; ids / w [T, K]; w13_packed
     [E, 2I, H/2] (gate rows, then up rows), w13_scale [E, 2I, H/32]; w2_packed
     [E, H, I/2], w2_scale [E, H, I/32]; biases [E, 2I] / [E, H] or None. POST_SCALE
-    sum per token in expert order."""
+    sum per token in expert order (moe_cte.py:603-606): the down bias is part of each
+    expert's output and so is weighted by its affinity (:590-591)."""
     x = np.asarray(x, F)
     T, H = x.shape
     xhat = dequant_mxfp8(*quant_mxfp8(x))
@@ -161,7 +163,7 @@ def moe_sparse_mx(x, ids, w, w13_packed, w13_scale, b13, w2_packed, w2_scale, b2
         y = expert_mlp_mx(xhat[rows], dequant_mxfp4(w13_packed[e], w13_scale[e]),
                           None if b13 is None else b13[e],
                           dequant_mxfp4(w2_packed[e], w2_scale[e]),
-                          None if b2 is None else b2[e], act, gate_limits, up_limits)
+                          None if b2 is None else b2[e], act, gate_limits, up_limits, requant_h)
         out[rows] = (out[rows] + y * wt[:, None]).astype(F)
     return out
 

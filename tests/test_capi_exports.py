@@ -115,6 +115,15 @@ def test_argument_errors_raise_reference_exception_types():
     rc = lib.moe_expert_down_block(p, p, 4, 7168, 2048, 256, p, p, None, None, 0, 1 << 21, p, p,
                                    1, p, None)
     assert rc == _lib.MOE_ERR_UNSUPPORTED and b"exceeds 4 GiB" in lib.moe_last_error()
+    # MX expert tiles stop at 64 rows: mt = 128 is refused before any launch
+    rc = lib.moe_expert_gate_up_mx(p, p, 4, 3072, 3072, 128, 1, p, p, None, None, None, None, 0, p,
+                                   0, p, p, 1, 128, 1, ctypes.c_float(float("nan")),
+                                   ctypes.c_float(7.0), ctypes.c_float(-6.0), ctypes.c_float(8.0),
+                                   p, p, None)
+    assert rc == _lib.MOE_ERR_UNSUPPORTED and b"64 rows" in lib.moe_last_error()
+    rc = lib.moe_expert_down_mx(p, p, 4, 3072, 3072, 128, 1, p, p, None, None, None, None, 0, 0,
+                                p, p, 1, 128, p, None)
+    assert rc == _lib.MOE_ERR_UNSUPPORTED and b"64 rows" in lib.moe_last_error()
 
 
 def test_ops_reject_cpu_tensors():

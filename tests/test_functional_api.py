@@ -147,3 +147,50 @@ def test_converted_weight_cache_follows_its_sources():
         del gu, dn, w13, w2
         gc.collect()
         assert len(_experts._CACHE) == 0
+
+
+def _nf_weights(E=2, H=256, I=128, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    gu = torch.randn(E, H, 2 * I, generator=g).to(FP8)   # a parameter stored [E, H, 2I]
+    dn = torch.randn(E, I, H, generator=g).to(FP8)
+    return gu, dn
+
+
+def test_operator_layout_cache_hits_fresh_views_of_one_parameter():
+    """The reference's decode passes a fresh `.reshape` view of each expert parameter
+    on every call (model_bf16.py:1278). The re-layout to the kernels' stacking runs
+    once for all of them: the cache follows the storage, not the view object."""
+    from vllm_neuron_amd.functional.moe import _experts
+    gu, dn = _nf_weights()
+    E, H, I2 = gu.shape
+    before = _experts.BUILDS[0]
+    outs = [_experts.routed_weights(gu.reshape(E, H, 2, I2 // 2), dn.reshape(E, I2 // 2, H))
+            for _ in range(3)]
+    assert _experts.BUILDS[0] == before + 1
+    assert all(o[0] is outs[0][0] and o[2] is outs[0][2] for o in outs)
+    ref = gu.reshape(E, H, 2, I2 // 2).permute(0, 2, 3, 1).reshape(E, I2, H)
+    assert torch.equal(outs[0][0].view(torch.uint8), ref.contiguous().view(torch.uint8))
+    # an in-place write through the parameter (a weight reload) bumps the shared
+    # version counter: the next call rebuilds
+    gu.view(torch.uint8)[0, 0, 0] ^= 1
+    _experts.routed_weights(gu.reshape(E, H, 2, I2 // 2), dn.reshape(E, I2 // 2, H))
+    assert _experts.BUILDS[0] == before + 2
+
+
+def test_operator_layout_cache_drops_freed_weights():
+    """A freed weight's entry goes with its storage owner, so a tensor allocated later
+    (possibly at the same address) is converted afresh, never served stale bytes."""
+    import gc
+    from vllm_neuron_amd.functional.moe import _experts
+    gu, dn = _nf_weights(seed=1)
+    E, H, I2 = gu.shape
+    a = _experts.routed_weights(gu.reshape(E, H, 2, I2 // 2), dn.reshape(E, I2 // 2, H))[0].clone()
+    n = len(_experts._CACHE)
+    del gu, dn
+    gc.collect()
+    assert len(_experts._CACHE) == n - 1
+    before = _experts.BUILDS[0]
+    gu2, dn2 = _nf_weights(seed=2)
+    b = _experts.routed_weights(gu2.reshape(E, H, 2, I2 // 2), dn2.reshape(E, I2 // 2, H))[0]
+    assert _experts.BUILDS[0] == before + 1
+    assert not torch.equal(a.view(torch.uint8), b.view(torch.uint8))

@@ -351,3 +351,27 @@ def test_moe_block_tkg_fused_residual(cuda):
     only = M.moe_block_tkg(x, gamma, w.router_w.t(), gu, dn, residual=res, skip_router_logits=True,
                            **kw)
     assert len(only) == 2 and torch.equal(only[0], out) and torch.equal(only[1], s)
+
+
+def test_moe_block_tkg_fresh_weight_views_convert_once(cuda):
+    """The reference's decode hands moe_block_tkg a fresh `.reshape` view of the
+    gate_up parameter on every step (model_bf16.py:1278). Three calls with fresh views
+    of one stored parameter re-layout the experts once and give equal outputs."""
+    say("moe_block_tkg fresh views")
+    cfg, w = _small(cuda, 5)
+    E, K, H, I = cfg.n_experts, cfg.top_k, cfg.hidden, cfg.intermediate
+    gu, gs, dn, ds = _nf(w)
+    gate_up_param = gu.reshape(E, H, 2 * I).clone()      # stored flat, as the model's parameter
+    x = synthetic.hidden_states(8, H, 5).to(cuda).reshape(1, 8, H)
+    gamma = torch.ones(1, H, device=cuda)
+    kw = dict(top_k=K, expert_gate_up_weights_scale=gs, expert_down_weights_scale=ds,
+              router_act_fn=M.RouterActFnType.SOFTMAX, router_pre_norm=False,
+              expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.POST_SCALE)
+    before = _experts.BUILDS[0]
+    outs = [M.moe_block_tkg(x, gamma, w.router_w.t(), gate_up_param.reshape(E, H, 2, I), dn, **kw)[0]
+            for _ in range(3)]
+    torch.cuda.synchronize()
+    assert _experts.BUILDS[0] == before + 1
+    assert torch.equal(outs[1], outs[0]) and torch.equal(outs[2], outs[0])
+    ref = M.moe_block_tkg(x, gamma, w.router_w.t(), gu, dn, **kw)[0]
+    assert torch.equal(ref, outs[0])

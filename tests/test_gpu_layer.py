@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+from _routing_audit import audit
 from _util import np_f32, np_u8, oracle_shared, oracle_weights, rel_l2, say
 from oracle import router as R
 from oracle.moe import bf16_round, moe_sparse_fp8
@@ -25,6 +26,19 @@ def _route_oracle(cfg, lg, w):
     return R.route_topk_act(lg, cfg.top_k, sc, cfg.renorm, 1e-20, cfg.routed_scaling)
 
 
+def _routing_audit(cfg, w, ref_lg, lg, ids, tag):
+    """The oracle end to end (its own logits -> its own ids) against the GPU's ids:
+    every token that differs must be a near-tie within the logits tolerance."""
+    oi, _ = _route_oracle(cfg, ref_lg, w)
+    sc = R.SOFTMAX if cfg.scoring == "softmax" else R.SIGMOID
+    rep = audit(ref_lg, lg, ids, oi, cfg.top_k, sc, cfg.grouped,
+                None if (not cfg.grouped or w.corr_bias is None) else np_f32(w.corr_bias),
+                cfg.n_group if cfg.grouped else 1, cfg.topk_group if cfg.grouped else 1)
+    say(tag, "routing audit", {k: v for k, v in rep.items() if k != "unexplained"},
+        "unexplained", rep["unexplained"][:10])
+    assert not rep["unexplained"], (tag, rep["unexplained"][:10])
+
+
 def _check_layer(cfg, w, x, tokens=None, tag=""):
     out, ids, wts, lg = ops.layer_forward(x, w, cfg, return_routing=True)
     torch.cuda.synchronize()
@@ -37,6 +51,7 @@ def _check_layer(cfg, w, x, tokens=None, tag=""):
     oi, ow = _route_oracle(cfg, lg, w)
     assert np.array_equal(ids, oi), tag
     assert np.array_equal(wts, ow), tag
+    _routing_audit(cfg, w, ref_lg, lg, ids, tag)
     sel = np.arange(x.shape[0]) if tokens is None else np.asarray(tokens)
     experts = set(np.unique(ids[sel]).tolist())
     q13, s13, q2, s2 = oracle_weights(w, experts if tokens is not None else None)
@@ -214,20 +229,11 @@ def test_layer_dsv3_full_size(cuda, T, idx, tokens):
     torch.cuda.empty_cache()
 
 
-def test_dsv3_prefill_every_row_of_chosen_experts(cuda):
-    """DeepSeek-V3 prefill (8192 tokens) through the block kernels: every slot row of y
-    (the unweighted expert outputs) of several whole experts against the oracle's expert
-    MLP on the same fp8 operands: experts whose second 256-row tile is partial (1-64 and
-    65-128 rows), the most loaded one, one below 256 rows, and the shared expert's last
-    two tiles. The same routing through the row-tile kernels (128-row tiles) agrees
-    with the block kernels on the whole layer output."""
-    from oracle.fp8 import dequant_act_1x128, dequant_weight_128x128, quant_act_1x128
-    from oracle.moe import expert_mlp
-    cfg = PRESETS["dsv3"]
-    T, E, K, B = 8192, cfg.n_experts, cfg.top_k, cfg.block_size
-    say("dsv3 prefill every row", T)
-    w = _big_weights(cfg, 2, cuda)
-    x = synthetic.hidden_states(T, cfg.hidden, 2).to(cuda)
+def _block_op_path(cfg, w, x):
+    """The grouped-routing layer op by op through the block kernels: the routing, the
+    mapping, the operands and y (unweighted expert outputs per slot row) besides the
+    combined output."""
+    T, E, K, B = x.shape[0], cfg.n_experts, cfg.top_k, cfg.block_size
     lg = ops.router_logits(x, w.router_w, w.router_bias)
     ids, wts = ops.router_topk(lg, K, ops.ORDER_GROUPED, cfg.scoring, cfg.n_group, cfg.topk_group,
                                w.corr_bias, cfg.renorm, 1e-20, cfg.routed_scaling)
@@ -235,13 +241,53 @@ def test_dsv3_prefill_every_row_of_chosen_experts(cuda):
     tpid, b2e = m["token_position_to_id"], m["block_to_expert"]
     NB = tpid.numel()
     xq, xs = ops.act_quant(x)
-    tiles, num, mbt = ops.build_block_tiles(tpid, b2e, B, T, K, E, 1)
+    tiles, num, mbt = ops.build_block_tiles(tpid, b2e, B, T, K, E, cfg.n_shared)
     hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mbt)
     y = ops.expert_down_block(hq, hs, w, T, NB, tiles, num, mbt)
-    out_blk = ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, 1)
-    counts = m["expert_counts"].cpu().numpy()
-    tp = tpid.cpu().numpy()
-    b2 = b2e.cpu().numpy()
+    out = ops.combine(y, m["inv_pos"], wts, T, cfg.hidden, NB, cfg.n_shared)
+    return dict(ids=ids, wts=wts, m=m, tpid=tpid, b2e=b2e, NB=NB, xq=xq, xs=xs, y=y, out=out,
+                tiles=(tiles, num, mbt))
+
+
+def _check_expert_rows(cfg, w, x, p, experts, tag):
+    """Every slot row of y of each expert in `experts` against the oracle's expert MLP
+    on the same fp8 operands (slots hold an expert's tokens in ascending order)."""
+    from oracle.fp8 import dequant_act_1x128, dequant_weight_128x128, quant_act_1x128
+    from oracle.moe import expert_mlp
+    counts = p["m"]["expert_counts"].cpu().numpy()
+    tp, b2 = p["tpid"].cpu().numpy(), p["b2e"].cpu().numpy()
+    xhat = dequant_act_1x128(*quant_act_1x128(np_f32(x)))
+    for e in experts:
+        first = int(np.nonzero(b2 == e)[0][0]) * cfg.block_size
+        slots = np.arange(first, first + counts[e])
+        toks = tp[slots]
+        assert np.all(toks >= 0) and np.all(np.diff(toks) > 0)
+        w13 = dequant_weight_128x128(np_u8(w.w13[e]), np_f32(w.w13_scale[e]))
+        w2 = dequant_weight_128x128(np_u8(w.w2[e]), np_f32(w.w2_scale[e]))
+        ref = expert_mlp(xhat[toks], w13, w2)
+        got = np_f32(p["y"][torch.from_numpy(slots).to(x.device)])
+        err = rel_l2(got, ref)
+        say(tag, "expert", e, "rows", counts[e], "rel_l2", err)
+        assert err <= TOL_REL_L2, (tag, e, err)
+    return xhat
+
+
+def test_dsv3_prefill_every_row_of_chosen_experts(cuda):
+    """DeepSeek-V3 prefill (8192 tokens) through the block kernels: every slot row of y
+    (the unweighted expert outputs) of several whole experts against the oracle's expert
+    MLP on the same fp8 operands: experts whose second 256-row tile is partial (1-64 and
+    65-128 rows), the most loaded one, one below 256 rows, and the shared expert's last
+    two tiles. The same routing through the row-tile kernels (128-row tiles) agrees
+    with the block kernels on the whole layer output."""
+    from oracle.fp8 import dequant_weight_128x128
+    from oracle.moe import expert_mlp
+    cfg = PRESETS["dsv3"]
+    T, E, K, B = 8192, cfg.n_experts, cfg.top_k, cfg.block_size
+    say("dsv3 prefill every row", T)
+    w = _big_weights(cfg, 2, cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, 2).to(cuda)
+    p = _block_op_path(cfg, w, x)
+    counts = p["m"]["expert_counts"].cpu().numpy()
     picks = []
     for lo, hi in ((256, 320), (320, 384)):
         band = np.nonzero((counts > lo) & (counts <= hi))[0]
@@ -254,19 +300,8 @@ def test_dsv3_prefill_every_row_of_chosen_experts(cuda):
     picks = list(dict.fromkeys(picks))
     assert len(picks) >= 3, counts
     say("experts", picks, "counts", counts[picks].tolist())
-    xhat = dequant_act_1x128(*quant_act_1x128(np_f32(x)))
-    for e in picks:
-        first = int(np.nonzero(b2 == e)[0][0]) * B
-        slots = np.arange(first, first + counts[e])
-        toks = tp[slots]
-        assert np.all(toks >= 0) and np.all(np.diff(toks) > 0)
-        w13 = dequant_weight_128x128(np_u8(w.w13[e]), np_f32(w.w13_scale[e]))
-        w2 = dequant_weight_128x128(np_u8(w.w2[e]), np_f32(w.w2_scale[e]))
-        ref = expert_mlp(xhat[toks], w13, w2)
-        got = np_f32(y[torch.from_numpy(slots).to(cuda)])
-        err = rel_l2(got, ref)
-        say("expert", e, "rows", counts[e], "rel_l2", err)
-        assert err <= TOL_REL_L2, (e, err)
+    xhat = _check_expert_rows(cfg, w, x, p, picks, "dsv3 8192")
+    NB, y = p["NB"], p["y"]
     # shared expert: slots NB + t; its last two 256-row tiles
     sh = np.arange(T - 512, T)
     w13 = dequant_weight_128x128(np_u8(w.shared_w13[0]), np_f32(w.shared_w13_scale[0]))
@@ -277,15 +312,16 @@ def test_dsv3_prefill_every_row_of_chosen_experts(cuda):
     say("shared expert last tiles rel_l2", err)
     assert err <= TOL_REL_L2, err
     # row-tile kernels on the same routing and operands
+    tpid, b2e, xq, xs = p["tpid"], p["b2e"], p["xq"], p["xs"]
     tiles, num, mx = ops.build_tiles(tpid, b2e, B, T, K, E, 1, 128)
     hq2, hs2 = ops.expert_gate_up(xq, xs, w, tpid, NB, tiles, num, mx, 128)
     y2 = ops.expert_down(hq2, hs2, w, T, NB, tiles, num, mx, 128)
-    out_row = ops.combine(y2, m["inv_pos"], wts, T, cfg.hidden, NB, 1)
-    err = rel_l2(np_f32(out_row), np_f32(out_blk))
+    out_row = ops.combine(y2, p["m"]["inv_pos"], p["wts"], T, cfg.hidden, NB, 1)
+    err = rel_l2(np_f32(out_row), np_f32(p["out"]))
     say("row tiles vs block kernels rel_l2", err)
     assert err < 5e-3, err
-    assert torch.equal(out_blk, ops.layer_forward(x, w, cfg))
-    del w, y, y2, hq, hq2
+    assert torch.equal(p["out"], ops.layer_forward(x, w, cfg))
+    del w, y, y2, hq2, p
     torch.cuda.empty_cache()
 
 
@@ -340,16 +376,25 @@ def test_layer_kimi_k2_full_size(cuda, kimi_weights, T):
 def test_layer_glm45_full_size_zipf(cuda):
     """GLM-4.5 layer (hidden 5120, intermediate 1536, 160 experts + 1 shared) at 4096
     tokens with Zipf(1.2) expert popularity and 10% of the experts empty: overfull
-    experts span many 256-row tiles, empty ones none."""
+    experts span many 256-row tiles, empty ones none. The oracle checks the tokens in
+    the last slot of experts whose last tiles cover every 64-row band (and the most and
+    least loaded), every token equals the op-by-op path bit for bit, and every slot
+    row of the two heaviest experts is checked against the oracle's expert MLP."""
     cfg = PRESETS["glm45"]
     say("layer glm-4.5 full zipf")
     w = synthetic.make_weights(cfg, 4, device=cuda, zipf=True, experts_device=cuda)
     x = synthetic.hidden_states(4096, cfg.hidden, 4).to(cuda)
-    out = _check_layer(cfg, w, x, tokens=[0, 1234, 4095], tag="glm45 T=4096")
     ids = ops.layer_forward(x, w, cfg, return_routing=True)[1].cpu().numpy()
     counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
     assert (counts == 0).sum() >= 16 and counts.max() > 3 * counts[counts > 0].mean()
-    del w, out
+    tokens, experts = _tile_tokens(ids, cfg.n_experts, extra=(0, 1234, 4095))
+    say("glm tokens", tokens, "experts", experts, "counts", counts[experts].tolist())
+    out = _check_layer(cfg, w, x, tokens=tokens, tag="glm45 T=4096")
+    p = _block_op_path(cfg, w, x)
+    assert torch.equal(out, p["out"])
+    heavy = [int(e) for e in np.argsort(-counts, kind="stable")[:2]]
+    _check_expert_rows(cfg, w, x, p, heavy, "glm45 heaviest")
+    del w, out, p
     torch.cuda.empty_cache()
 
 
@@ -453,6 +498,7 @@ def _check_layer_norm(cfg, w, x, gamma, residual=None, hidden_actual=None, token
     assert np.allclose(lg, ref_lg, rtol=1e-5, atol=2e-5), tag
     oi, ow = _route_oracle(cfg, lg, w)
     assert np.array_equal(ids, oi) and np.array_equal(wts, ow), tag
+    _routing_audit(cfg, w, ref_lg, lg, ids, tag)
     sel = np.arange(x.shape[0]) if tokens is None else np.asarray(tokens)
     experts = set(np.unique(ids[sel]).tolist())
     q13, s13, q2, s2 = oracle_weights(w, experts if tokens is not None else None)

@@ -163,3 +163,117 @@ def test_expert_mlp_mx_conventions():
     g2 = xd @ w13[:I].T
     ref2 = (g2 / (1 + np.exp(-g2)) * (xd @ w13[I:].T)) @ w2.T.astype(np.float64)
     assert np.allclose(silu, ref2, rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------- the MX layer composition
+
+def _mx_layer(seed, T=7, H=64, I=64, E=4, K=2):
+    """A tiny MX layer: random fp4 codes and E8M0 bytes near 2^0, biases, softmax
+    top-K routing weights."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((T, H)) * 2).astype(np.float32)
+    w13 = rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8)
+    s13 = rng.integers(119, 124, (E, 2 * I, H // 32), dtype=np.uint8)
+    w2 = rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8)
+    s2 = rng.integers(119, 124, (E, H, I // 32), dtype=np.uint8)
+    b13 = rng.standard_normal((E, 2 * I)).astype(np.float32)
+    b2 = rng.standard_normal((E, H)).astype(np.float32)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    ids = np.argsort(-lg, axis=1, kind="stable")[:, :K].astype(np.int32)
+    w = rng.uniform(0.1, 1.0, (T, K)).astype(np.float32)
+    return x, ids, w, w13, s13, b13, w2, s2, b2
+
+
+def _torch_moe_impl_dense_mx(x, ids, w, w13, s13, b13, w2, s2, b2, act, gl, ul, requant_h):
+    """_torch_moe_impl (moe_cte.py:465-612) in float64 over every expert and every
+    token, on the dequantized MX operands: gate / up einsums over all E, biases
+    (:562-564), clamps (:567-571), act(gate) * up (:574-575), down einsum + down bias
+    for every expert (:585-591), then the POST_SCALE sum over e = 0..E-1 with the
+    dense affinities (zero for unselected experts, :603-606). requant_h applies the
+    MXFP8 quantizer to each intermediate row, the operand the MX down kernel reads."""
+    T, H = x.shape
+    E, I = w13.shape[0], w13.shape[1] // 2
+    xh = OX.dequant_mxfp8(*OX.quant_mxfp8(x)).astype(np.float64)
+    W13 = np.stack([OX.dequant_mxfp4(w13[e], s13[e]) for e in range(E)]).astype(np.float64)
+    W2 = np.stack([OX.dequant_mxfp4(w2[e], s2[e]) for e in range(E)]).astype(np.float64)
+    aff = np.zeros((T, E))
+    for t in range(T):
+        for j in range(ids.shape[1]):
+            aff[t, ids[t, j]] += w[t, j]
+    gate = np.einsum("th,eih->eti", xh, W13[:, :I]) + b13[:, None, :I]
+    up = np.einsum("th,eih->eti", xh, W13[:, I:]) + b13[:, None, I:]
+    lo, hi = gl
+    gate = np.clip(gate, -np.inf if lo is None else lo, np.inf if hi is None else hi)
+    lo, hi = ul
+    up = np.clip(up, -np.inf if lo is None else lo, np.inf if hi is None else hi)
+    a = gate / (1 + np.exp(-1.702 * gate)) if act == "swish" else gate / (1 + np.exp(-gate))
+    inter = a * up
+    if requant_h:
+        inter = np.stack([OX.dequant_mxfp8(*OX.quant_mxfp8(inter[e].astype(np.float32)))
+                          for e in range(E)]).astype(np.float64)
+    nxt = np.einsum("eti,ehi->eth", inter, W2) + b2[:, None, :]
+    out = np.zeros((T, H))
+    for e in range(E):
+        out = out + nxt[e] * aff[:, e:e + 1]
+    return out
+
+
+@pytest.mark.parametrize("act, gl, ul", [("swish", (None, 7.0), (-6.0, 8.0)),
+                                         ("silu", (None, None), (None, None))])
+@pytest.mark.parametrize("requant_h", [False, True])
+def test_moe_sparse_mx_equals_the_dense_reference_form(act, gl, ul, requant_h):
+    """The oracle's per-expert gathered MX layer equals the reference fallback's dense
+    all-expert form (moe_cte.py:465-612) on the same dequantized operands: the gather,
+    the weight of each selected expert, the down bias weighted by the affinity and
+    the scatter-add are what this pins."""
+    x, ids, w, w13, s13, b13, w2, s2, b2 = _mx_layer(11)
+    got = OX.moe_sparse_mx(x, ids, w, w13, s13, b13, w2, s2, b2, act, gl, ul, requant_h=requant_h)
+    ref = _torch_moe_impl_dense_mx(x, ids, w, w13, s13, b13, w2, s2, b2, act, gl, ul, requant_h)
+    err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    # fp32 products against float64 (measured 1e-7); a dropped or unweighted bias
+    # term moves the output by more than 1e-3
+    assert err < 1e-5, err
+
+
+def test_moe_sparse_mx_float64_loops():
+    """Element-by-element loops of the POST_SCALE layer on a 3-token layer (no vector
+    routine involved): sum_k w_k * (act(clamp(x.Wg_e + bg_e)) * clamp(x.Wu_e + bu_e)) . Wd_e
+    + bd_e)."""
+    x, ids, w, w13, s13, b13, w2, s2, b2 = _mx_layer(12, T=3, H=64, I=32, E=3)
+    got = OX.moe_sparse_mx(x, ids, w, w13, s13, b13, w2, s2, b2, "swish", (None, 7.0),
+                           (-6.0, 8.0), requant_h=False)
+    xh = OX.dequant_mxfp8(*OX.quant_mxfp8(x))
+    T, H = x.shape
+    I = w13.shape[1] // 2
+    out = np.zeros((T, H))
+    for t in range(T):
+        for j in range(ids.shape[1]):
+            e = int(ids[t, j])
+            W13 = OX.dequant_mxfp4(w13[e], s13[e])
+            W2 = OX.dequant_mxfp4(w2[e], s2[e])
+            hh = []
+            for i in range(I):
+                g = sum(float(xh[t, k]) * float(W13[i, k]) for k in range(H)) + float(b13[e, i])
+                u = sum(float(xh[t, k]) * float(W13[I + i, k]) for k in range(H)) + float(b13[e, I + i])
+                g = min(g, 7.0)
+                u = min(max(u, -6.0), 8.0)
+                hh.append(g / (1.0 + np.exp(-1.702 * g)) * u)
+            for o in range(H):
+                yv = sum(hh[i] * float(W2[o, i]) for i in range(I)) + float(b2[e, o])
+                out[t, o] += float(w[t, j]) * yv
+    assert np.allclose(got, out, rtol=1e-4, atol=1e-4)
+
+
+def test_moe_sparse_mx_linear_in_routing_weights_and_bias_weighted():
+    """Doubling the routing weights doubles the output (the down bias included); with
+    all-zero weight codes each token's output is sum_k w_k * b_down[e_k] exactly."""
+    x, ids, w, w13, s13, b13, w2, s2, b2 = _mx_layer(13)
+    base = OX.moe_sparse_mx(x, ids, w, w13, s13, b13, w2, s2, b2)
+    twice = OX.moe_sparse_mx(x, ids, 2 * w, w13, s13, b13, w2, s2, b2)
+    assert np.allclose(twice, 2 * base, rtol=1e-6, atol=1e-6)
+    zero = OX.moe_sparse_mx(x, ids, w, np.zeros_like(w13), s13, b13, np.zeros_like(w2), s2, b2)
+    ref = np.zeros_like(zero)
+    for t in range(x.shape[0]):
+        for j in range(ids.shape[1]):
+            ref[t] = (ref[t] + w[t, j] * b2[ids[t, j]]).astype(np.float32)
+    assert np.array_equal(zero, ref)

@@ -671,9 +671,6 @@ static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
       else
         MOE_MX(64, 2, false, 4);
       break;
-    case 128:
-      MOE_MX(128, 2, false, 4);
-      break;
     default:
       return MOE_ERR_ARG;
   }
@@ -691,6 +688,8 @@ static int mx_common_checks(const char* _moe_fn, int T, int H, int I, int E, int
   MOE_CHECK_ARG(H > 0 && H % 256 == 0 && I > 0 && I % 128 == 0,
                 "H must be a multiple of 256 and I of 128 (H=%d I=%d); pad them", H, I);
   MOE_CHECK_ARG(mt == 16 || mt == 32 || mt == 64 || mt == 128, "mt must be 16/32/64/128");
+  // a 128-row MXFP4 tile needs more than the 512 registers of a lane (it would spill)
+  MOE_CHECK_SUPPORTED(mt != 128, "MX expert tiles stop at 64 rows (mt=128 is not built)");
   MOE_CHECK_ARG(wfmt == MOE_MX_FP4 || wfmt == MOE_MX_FP8, "weight format must be MOE_MX_FP4 or MOE_MX_FP8");
   return MOE_OK;
 }

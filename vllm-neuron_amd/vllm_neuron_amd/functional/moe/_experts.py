@@ -4,11 +4,18 @@ The operator API of the reference passes expert weights per call in its own
 layout (gate_up [E, H, 2, I], down [E, I, H]; moe_cte.py:122-131). The HIP
 kernels read the DeepSeek-V3 checkpoint stacking (w13 [E, 2I, H], w2 [E, H, I],
 128x128 fp32 block scales), which is K-contiguous. Both are accepted here; the
-reference layout is converted once per weight tensor and the result cached,
-keyed by the tensors' storage, version and shape (a second copy of the experts
-while the caller keeps the originals: pass the stacked layout to avoid it).
-An entry lives only as long as every source tensor object: a finalizer on each
-source drops it, so a later tensor allocated at a freed address never hits a
+reference layout is converted once per weight tensor and the result cached
+(a second copy of the experts while the caller keeps the originals: pass the
+stacked layout to avoid it).
+
+The key is what the bytes are, not which Python object holds them: the storage
+address, the view's offset, shape, strides and dtype, and the version counter
+(which views share with their base, so an in-place write through any of them
+invalidates the entry). A fresh view of the same parameter on every call (the
+reference's decode passes `self.gate_up_proj_weight.reshape(...)`,
+model_bf16.py:1278) therefore hits. An entry lives as long as the tensors that
+own the storage (a view's base, else the tensor itself): a finalizer on each
+owner drops it, so a later tensor allocated at a freed address never hits a
 stale entry.
 """
 import weakref
@@ -20,11 +27,18 @@ from ...weights import FP8, Fp8MoEWeights, quant_weight_blocks
 
 _CACHE = {}
 _CACHE_MAX = 8
+BUILDS = [0]  # conversions run so far (read by the tests)
 
 
 def _key(*ts):
-    return tuple((t.data_ptr(), t._version, tuple(t.shape), t.dtype) if t is not None else None
+    return tuple((t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape),
+                  tuple(t.stride()), t.dtype, t.device, t._version) if t is not None else None
                  for t in ts)
+
+
+def _owner(t):
+    """The tensor whose lifetime is the storage's: a view's base, else t."""
+    return t if t._base is None else t._base
 
 
 def _drop(key):
@@ -32,17 +46,19 @@ def _drop(key):
 
 
 def _cached(key, build, sources):
-    """build() once per key; the entry is dropped when any tensor of ``sources``
-    is garbage-collected (before its memory can be handed to another tensor)."""
+    """build() once per key; the entry is dropped when the owner of any tensor of
+    ``sources`` is garbage-collected (before its memory can be handed to another
+    tensor)."""
     hit = _CACHE.get(key)
     if hit is None:
         if len(_CACHE) >= _CACHE_MAX:
             _CACHE.pop(next(iter(_CACHE)))
         hit = build()
+        BUILDS[0] += 1
         _CACHE[key] = hit
         for t in sources:
             if t is not None:
-                weakref.finalize(t, _drop, key)
+                weakref.finalize(_owner(t), _drop, key)
     return hit
 
 

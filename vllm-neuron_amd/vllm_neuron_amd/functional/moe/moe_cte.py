@@ -261,7 +261,7 @@ def _moe_cte_mx_op(hidden_states: Tensor, expert_affinities_masked: Tensor, gate
     x = _experts.as_bf16(hidden_states[:T]).contiguous()
     xq, xs = ops.act_quant_mx(x)
     k_rows = max(1, min(E, ((N - E + 1) * B + E - 1) // max(T, 1)))
-    mt = ops.choose_mt(T, k_rows, E)
+    mt = min(ops.choose_mt(T, k_rows, E), 64)  # the MX kernels stop at 64-row tiles
     tiles, num, max_tiles = ops.build_tiles(tpid, b2e, B, T, E, E, 0, mt)
     none = lambda v: None if v != v else v
     hq, hs = ops.expert_gate_up_mx(xq, xs, w, tpid, NB, tiles, num, max_tiles, mt, NB, act,
