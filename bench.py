@@ -459,6 +459,17 @@ def cpu_dense_small(x, w, cfg, reps=3):
             "cores": cpu_threads()}
 
 
+# --only workloads (the same weights and inputs as the full run): name, preset, tokens,
+# weight seed, input seed, Zipf routing
+ONLY = {
+    "dsv3_prefill8k": ("DeepSeek-V3 MoE layer, 8192 tokens", "dsv3", 8192, 1, 2, False),
+    "kimi_k2_2048": ("Kimi-K2 MoE layer, 2048 tokens", "kimi_k2", 2048, 3, 3, False),
+    "kimi_k2_16384": ("Kimi-K2 MoE layer, 16384 tokens", "kimi_k2", 16384, 3, 3, False),
+    "glm45_zipf4096": ("GLM-4.5 MoE layer, 4096 tokens, Zipf(1.2) routing, 10% empty experts",
+                       "glm45", 4096, 4, 4, True),
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -472,6 +483,9 @@ def main():
     ap.add_argument("--prologue-calls", type=int, default=0,
                     help="only run the decode prologue (fused, then as separate launches) this "
                          "many times at 64 and 8192 tokens, for a kernel trace; no timing")
+    ap.add_argument("--only", choices=sorted(ONLY),
+                    help="time one workload alone (whole layer, --steps calls after 2 warm-up "
+                         "calls) and print its report line; for kernel traces and counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU: the layer keeps all experts "
@@ -482,6 +496,14 @@ def main():
     from vllm_neuron_amd import PRESETS, ops, synthetic
 
     dev = torch.device("cuda:0")
+    if args.only:
+        name, preset, T, wseed, xseed, zipf = ONLY[args.only]
+        cfg = PRESETS[preset]
+        print(f"[bench] only: {name}", file=sys.stderr, flush=True)
+        w = synthetic.make_weights(cfg, wseed, device=dev, zipf=zipf, experts_device=dev)
+        x = synthetic.hidden_states(T, cfg.hidden, xseed).to(dev)
+        print(json.dumps(workload_report(name, x, w, cfg, args.steps, torch, ops)))
+        return
     if args.prologue_calls:
         run_prologue(args.prologue_calls, torch, ops, dev)
         return

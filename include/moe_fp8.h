@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MOE_FP8_ABI_VERSION 2
+#define MOE_FP8_ABI_VERSION 3
 
 /* status codes */
 #define MOE_OK 0
@@ -164,21 +164,34 @@ int moe_build_tiles(const int32_t* token_position_to_id, const int32_t* block_to
  * slot of every tile, x rows gathered by token_position_to_id (shared slots map
  * to token slot - N*B - j*T). hq/hs have N*B + n_shared*T rows.
  * Replaces the gate_up half of nkilib moe_cte (moe_cte.py:356-421) and of
- * _torch_moe_impl (moe_cte.py:557-575), SiLU activation. mt in {16,32,64,128}. */
+ * _torch_moe_impl (moe_cte.py:557-575), SiLU activation. mt in {16,32,64,128}.
+ *
+ * Weight dequantization: code * w13_scale[e, row/128, k/128] (128x128 blocks),
+ * times w13_channel_scale[e, row] when that pointer is not NULL ([E, 2I] fp32,
+ * gate rows then up rows; w13_shared_channel_scale likewise [n_shared, 2I]). The
+ * channel scales carry the reference's FP8 per-channel ("row") weight scales
+ * ([E, 1, 2I] in moe_cte, moe_cte.py:178-181; [E, 2, I] in moe_tkg,
+ * moe_tkg.py:87-89) and, expanded along the rows, its static scales ([E, 2, 1]);
+ * pass all-ones block scales with them. */
 int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
-                       const uint8_t* w13, const float* w13_scale, const uint8_t* w13_shared,
-                       const float* w13_shared_scale, int n_shared,
-                       const int32_t* token_position_to_id, int NB, const int32_t* tiles,
-                       const int32_t* num_tiles, int max_tiles, int mt, uint8_t* hq, float* hs,
-                       void* stream);
+                       const uint8_t* w13, const float* w13_scale,
+                       const float* w13_channel_scale, const uint8_t* w13_shared,
+                       const float* w13_shared_scale, const float* w13_shared_channel_scale,
+                       int n_shared, const int32_t* token_position_to_id, int NB,
+                       const int32_t* tiles, const int32_t* num_tiles, int max_tiles, int mt,
+                       uint8_t* hq, float* hs, void* stream);
 
 /* y[slot, :H] = bf16(hq[slot] W_d^T) per tile slot (unweighted).
- * Replaces the down projection of moe_cte (moe_cte.py:585-588). */
+ * Replaces the down projection of moe_cte (moe_cte.py:585-588). Channel scales as
+ * moe_expert_gate_up: w2_channel_scale [E, H] (the reference's [E, 1, H] /
+ * [E, H] row scales, moe_cte.py:186-188, moe_tkg.py:90-91, or its [E, 1] static
+ * scale expanded), w2_shared_channel_scale [n_shared, H]; NULL for none. */
 int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int E,
-                    const uint8_t* w2, const float* w2_scale, const uint8_t* w2_shared,
-                    const float* w2_shared_scale, int n_shared, int NB, const int32_t* tiles,
-                    const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
-                    void* stream);
+                    const uint8_t* w2, const float* w2_scale, const float* w2_channel_scale,
+                    const uint8_t* w2_shared, const float* w2_shared_scale,
+                    const float* w2_shared_channel_scale, int n_shared, int NB,
+                    const int32_t* tiles, const int32_t* num_tiles, int max_tiles, int mt,
+                    void* y_bf16, void* stream);
 
 /* Prefill-sized variants ("block" kernels): one workgroup computes 256 slots
  * of one expert x 256 weight rows with 16x16x128 fp8 MFMA tiles, both operands
@@ -198,13 +211,16 @@ int moe_build_block_tiles(const int32_t* token_position_to_id, const int32_t* bl
                           void* stream);
 int moe_expert_gate_up_block(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
                              const uint8_t* w13, const float* w13_scale,
-                             const uint8_t* w13_shared, const float* w13_shared_scale,
-                             int n_shared, const int32_t* token_position_to_id, int NB,
-                             const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
-                             uint8_t* hq, float* hs, void* stream);
+                             const float* w13_channel_scale, const uint8_t* w13_shared,
+                             const float* w13_shared_scale,
+                             const float* w13_shared_channel_scale, int n_shared,
+                             const int32_t* token_position_to_id, int NB, const int32_t* tiles,
+                             const int32_t* num_tiles, int max_tiles, uint8_t* hq, float* hs,
+                             void* stream);
 int moe_expert_down_block(const uint8_t* hq, const float* hs, int T, int H, int I, int E,
-                          const uint8_t* w2, const float* w2_scale, const uint8_t* w2_shared,
-                          const float* w2_shared_scale, int n_shared, int NB,
+                          const uint8_t* w2, const float* w2_scale, const float* w2_channel_scale,
+                          const uint8_t* w2_shared, const float* w2_shared_scale,
+                          const float* w2_shared_channel_scale, int n_shared, int NB,
                           const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
                           void* y_bf16, void* stream);
 

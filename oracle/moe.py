@@ -7,8 +7,9 @@
 * moe_sparse_fp8       <- the same math computed per expert on the gathered tokens
                           (non-selected affinities are 0, so the sums are equal), with the
                           fp8 operands the kernels consume: x quantized 1x128, weights
-                          dequantized from 128x128 blocks, SiLU(g)*u requantized 1x128
-                          before the down projection; fp32 accumulation; the shared expert
+                          dequantized from 128x128 blocks (times optional per-channel
+                          scales), SiLU(g)*u requantized 1x128 before the down projection;
+                          fp32 accumulation; the shared expert
                           (moe_block_tkg.py:314-316, kernel-only in the reference) added
                           with weight 1.
 * topk_reduce          <- _cpu_topk_reduce, vllm_neuron/functional/moe/topk_reduce.py:144-159.
@@ -49,13 +50,15 @@ def expert_mlp(xhat, w13hat, w2hat, requant_h=True):
 
 
 def moe_sparse_fp8(x, ids, w, w13_q, w13_s, w2_q, w2_s, shared=None, requant_h=True,
-                   experts=None):
+                   experts=None, chan=None):
     """Layer output in fp32 before the final bf16 cast.
 
     x [T,H] float32 holding bf16 values; ids/w [T,K]; w13_q [E,2I,H] uint8, w13_s [E,2I/128,H/128];
     w2_q [E,H,I] uint8, w2_s [E,H/128,I/128]; shared = (w13_q, w13_s, w2_q, w2_s) of one
     expert or None. ``experts`` optionally restricts the routed experts evaluated (the others
-    contribute nothing) so full-size layers can be checked on a subset.
+    contribute nothing) so full-size layers can be checked on a subset. ``chan`` = (c13
+    [E, 2I], c2 [E, H]) multiplies each routed expert's dequantized weight rows (the
+    reference's FP8 per-channel weight scales, moe_cte.py:178-188, moe_tkg.py:87-91).
     """
     x = np.asarray(x, F)
     T, H = x.shape
@@ -72,6 +75,9 @@ def moe_sparse_fp8(x, ids, w, w13_q, w13_s, w2_q, w2_s, shared=None, requant_h=T
         wt = (np.asarray(w, F) * sel).sum(axis=1)[rows].astype(F)
         w13 = dequant_weight_128x128(w13_q[e], w13_s[e])
         w2 = dequant_weight_128x128(w2_q[e], w2_s[e])
+        if chan is not None:
+            w13 = (w13 * np.asarray(chan[0][e], F)[:, None]).astype(F)
+            w2 = (w2 * np.asarray(chan[1][e], F)[:, None]).astype(F)
         y = expert_mlp(xhat[rows], w13, w2, requant_h)
         out[rows] = (out[rows] + y * wt[:, None]).astype(F)
     if shared is not None:
@@ -112,13 +118,13 @@ def topk_reduce(inp_rows, token_ids_1based, T):
 
 def moe_block_tkg_fp8(x, gamma, eps, w_router_eh, router_bias, k, scoring, pre_norm,
                       norm_topk_prob, post_scale, w13_q, w13_s, w2_q, w2_s, shared=None,
-                      hidden_actual=None, logits=None):
+                      hidden_actual=None, logits=None, chan=None):
     """_torch_moe_block_tkg_impl (moe_block_tkg.py:57-303) with fp8 128x128 experts and a
     shared expert of weight 1: RMSNorm (padded columns 0) cast to bf16 -> fp32 router
     matmul (+ bias) -> pre_norm: activation then top-k, else top-k then activation
     (norm_topk_prob: / (sum + 1e-20)) -> experts on the normalized input, NO_SCALE weight
     1 or POST_SCALE affinity. ``logits`` (optional) replaces the router matmul so that a
-    selection made from GPU logits can be compared exactly. Returns
+    selection made from GPU logits can be compared exactly; ``chan`` as moe_sparse_fp8. Returns
     (out fp32 before the final cast, logits, ids, weights)."""
     from .router import (SOFTMAX, rms_norm_padded, route_act_topk_renorm, route_topk_act,
                          router_logits)
@@ -129,6 +135,6 @@ def moe_block_tkg_fp8(x, gamma, eps, w_router_eh, router_bias, k, scoring, pre_n
     ids, w = route(logits, k, scoring, norm_topk_prob, 1e-20, 1.0)
     if not post_scale:
         w = np.ones_like(w)
-    out = moe_sparse_fp8(xn, ids, w, w13_q, w13_s, w2_q, w2_s, shared=shared)
+    out = moe_sparse_fp8(xn, ids, w, w13_q, w13_s, w2_q, w2_s, shared=shared, chan=chan)
     return out, logits, ids, w
 

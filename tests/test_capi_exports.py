@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in header_functions():
         assert hasattr(lib, name), name
-    assert lib.moe_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.moe_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_block_formula_and_sizes_match_oracle():
@@ -100,7 +100,8 @@ def test_argument_errors_raise_reference_exception_types():
     rc = lib.moe_blockwise_mapping(p, None, None, 64, 8, 256, 256, 7, p, p, p, p, None, None, p,
                                    1 << 20, None)
     assert rc == _lib.MOE_ERR_ARG and b"257" in lib.moe_last_error()
-    rc = lib.moe_expert_gate_up(p, p, 4, 100, 256, 4, p, p, None, None, 0, p, 0, p, p, 1, 16, p, p, None)
+    rc = lib.moe_expert_gate_up(p, p, 4, 100, 256, 4, p, p, None, None, None, None, 0, p, 0, p, p, 1,
+                                 16, p, p, None)
     assert rc == _lib.MOE_ERR_ARG and b"multiples of 128" in lib.moe_last_error()
     rc = lib.moe_layer_forward(p, None, None, 1e-6, 0, 4, 7168, 2048, 256, 8, 1, p, None, None, 2,
                                1, 8, 4, 1, 1e-20, 2.5, p, p, p, p, p, p, p, p, 256, p, None, None,
@@ -112,8 +113,8 @@ def test_argument_errors_raise_reference_exception_types():
                                None, None, p, 1 << 30, None)
     assert rc == _lib.MOE_ERR_ARG and b"residual needs gamma" in lib.moe_last_error()
     # activation operands beyond 32-bit byte offsets are refused by the block kernels
-    rc = lib.moe_expert_down_block(p, p, 4, 7168, 2048, 256, p, p, None, None, 0, 1 << 21, p, p,
-                                   1, p, None)
+    rc = lib.moe_expert_down_block(p, p, 4, 7168, 2048, 256, p, p, None, None, None, None, 0, 1 << 21,
+                                   p, p, 1, p, None)
     assert rc == _lib.MOE_ERR_UNSUPPORTED and b"exceeds 4 GiB" in lib.moe_last_error()
     # MX expert tiles stop at 64 rows: mt = 128 is refused before any launch
     rc = lib.moe_expert_gate_up_mx(p, p, 4, 3072, 3072, 128, 1, p, p, None, None, None, None, 0, p,

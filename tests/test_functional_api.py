@@ -137,7 +137,8 @@ def test_converted_weight_cache_follows_its_sources():
 
     for seed in range(4):
         gu, dn = make(seed)
-        w13, _, w2, _ = _experts.routed_weights(gu, dn)
+        w13, _, w2, _, c13, c2 = _experts.routed_weights(gu, dn)
+        assert c13 is None and c2 is None
         ref13 = gu.view(torch.uint8).permute(0, 2, 3, 1).reshape(E, 2 * I, H)
         assert torch.equal(w13.view(torch.uint8), ref13)
         assert torch.equal(w2.view(torch.uint8), dn.view(torch.uint8).transpose(1, 2))
@@ -194,3 +195,34 @@ def test_operator_layout_cache_drops_freed_weights():
     b = _experts.routed_weights(gu2.reshape(E, H, 2, I2 // 2), dn2.reshape(E, I2 // 2, H))[0]
     assert _experts.BUILDS[0] == before + 1
     assert not torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+
+def test_reference_fp8_channel_scale_formats():
+    """The reference's FP8 per-channel weight scales (moe_cte [E, 1, 2I] / [E, 1, H],
+    moe_cte.py:178-188; moe_tkg row [E, 2, I] / [E, H] and static [E, 2, 1] / [E, 1],
+    moe_tkg.py:87-91) become unit 128x128 block scales plus fp32 channel scales [E, 2I]
+    (gate channels, then up) and [E, H]; mixing block and channel scales is refused."""
+    from vllm_neuron_amd.functional.moe import _experts
+    E, H, I = 3, 256, 128
+    g = torch.Generator().manual_seed(5)
+    gu = torch.randn(E, H, 2, I, generator=g).to(FP8)
+    dn = torch.randn(E, I, H, generator=g).to(FP8)
+    s_gu = torch.rand(E, 2, I, generator=g) + 0.5
+    s_dn = torch.rand(E, H, generator=g) + 0.5
+    for gs, ds in ((s_gu.reshape(E, 1, 2 * I), s_dn.reshape(E, 1, H)), (s_gu, s_dn)):
+        w13, s13, w2, s2, c13, c2 = _experts.routed_weights(gu, dn, gs, ds)
+        assert torch.all(s13 == 1) and tuple(s13.shape) == (E, 2 * I // 128, H // 128)
+        assert torch.all(s2 == 1) and tuple(s2.shape) == (E, H // 128, I // 128)
+        assert torch.equal(c13, s_gu.reshape(E, 2 * I)) and torch.equal(c2, s_dn)
+        assert torch.equal(c13[:, :I], s_gu[:, 0]) and torch.equal(c13[:, I:], s_gu[:, 1])
+    st_gu, st_dn = torch.tensor([[[2.0], [3.0]]]).repeat(E, 1, 1), torch.full((E, 1), 0.25)
+    *_, c13, c2 = _experts.routed_weights(gu, dn, st_gu, st_dn)
+    assert torch.all(c13[:, :I] == 2) and torch.all(c13[:, I:] == 3) and torch.all(c2 == 0.25)
+    # stacked layout with channel scales, and a missing down scale meaning 1
+    w13s = gu.permute(0, 2, 3, 1).reshape(E, 2 * I, H).contiguous()
+    *_, c13, c2 = _experts.routed_weights(w13s, dn.transpose(1, 2).contiguous(), s_gu, None)
+    assert torch.equal(c13, s_gu.reshape(E, 2 * I)) and torch.all(c2 == 1)
+    with pytest.raises(NotImplementedError, match="mix"):
+        _experts.routed_weights(gu, dn, torch.ones(E, H // 128, 2, I // 128), s_dn)
+    with pytest.raises(NotImplementedError):
+        _experts.routed_weights(gu, dn, torch.ones(E, 3, I), s_dn)

@@ -375,3 +375,119 @@ def test_moe_block_tkg_fresh_weight_views_convert_once(cuda):
     assert torch.equal(outs[1], outs[0]) and torch.equal(outs[2], outs[0])
     ref = M.moe_block_tkg(x, gamma, w.router_w.t(), gu, dn, **kw)[0]
     assert torch.equal(ref, outs[0])
+
+
+# ---------------------------------------------------------------- per-channel fp8 scales
+
+FP8 = torch.float8_e4m3fn
+
+
+def _chan_experts(E, H, I, seed, device):
+    """fp8 expert codes with per-output-channel scales (the reference's FP8 row
+    formats): the stacked codes q13 [E, 2I, H] / q2 [E, H, I], the channel scales
+    c13 [E, 2I] (gate, then up) / c2 [E, H] (dequantized weights ~ N(0, 0.02)), and the
+    same codes in the reference operator layout gate_up [E, H, 2, I] / down [E, I, H]."""
+    g = torch.Generator().manual_seed(seed)
+    q13 = (torch.randn(E, 2 * I, H, generator=g) * 64).clamp(-448, 448).to(FP8)
+    q2 = (torch.randn(E, H, I, generator=g) * 64).clamp(-448, 448).to(FP8)
+    c13 = (torch.rand(E, 2 * I, generator=g) + 0.5) * (0.02 / 64)
+    c2 = (torch.rand(E, H, generator=g) + 0.5) * (0.02 / 64)
+    gu = q13.view(torch.uint8).reshape(E, 2, I, H).permute(0, 3, 1, 2).contiguous().view(FP8)
+    dn = q2.view(torch.uint8).transpose(1, 2).contiguous().view(FP8)
+    return q13, q2, c13, c2, gu.to(device), dn.to(device)
+
+
+def _chan_oracle(x, ids, wts, q13, q2, c13, c2):
+    E, I2, H = q13.shape
+    ones13 = np.ones((E, I2 // 128, H // 128), np.float32)
+    ones2 = np.ones((E, H // 128, I2 // 2 // 128), np.float32)
+    return moe_sparse_fp8(np_f32(x), ids, wts, q13.view(torch.uint8).numpy(), ones13,
+                          q2.view(torch.uint8).numpy(), ones2, chan=(c13.numpy(), c2.numpy()))
+
+
+@pytest.mark.parametrize("T", [64, 2048])
+def test_moe_cte_per_channel_scales(cuda, T):
+    """moe_cte with the reference's FP8 per-channel scales gate_up_proj_scale [E, 1, 2I]
+    and down_proj_scale [E, 1, H] (moe_cte.py:178-188), against the oracle's per-channel
+    dequantization: row tiles at 64 tokens, block kernels at 2048 (512 rows per
+    expert)."""
+    say("moe_cte per-channel T", T)
+    E, K, H, I = 8, 2, 1024, 512
+    q13, q2, c13, c2, gu, dn = _chan_experts(E, H, I, 50 + T, cuda)
+    x = synthetic.hidden_states(T, H, 5).to(cuda)
+    g = torch.Generator().manual_seed(51)
+    rw = (torch.randn(H, E, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    aff = M.router(x, rw, K)
+    am, tpid, b2e, cond = M.build_blockwise_mapping(aff, E, K, 256)
+    out = M.moe_cte(x, am, gu, dn, tpid, b2e, 256, M.MoECTEImplementation.shard_on_block,
+                    gate_up_proj_scale=c13.reshape(E, 1, 2 * I).to(cuda),
+                    down_proj_scale=c2.reshape(E, 1, H).to(cuda))
+    ids, wts = _ids_weights_from_dense(aff)
+    ref = _chan_oracle(x, ids, wts, q13, q2, c13, c2)
+    err = rel_l2(np_f32(out), ref)
+    say("moe_cte per-channel rel_l2", err)
+    assert err <= TOL_REL_L2, err
+
+
+def test_moe_tkg_row_and_static_scales(cuda):
+    """moe_tkg with FP8 row quantization scales [E, 2, I] / [E, H] and static scales
+    [E, 2, 1] / [E, 1] (moe_tkg.py:87-91) against the oracle."""
+    say("moe_tkg row / static scales")
+    E, K, H, I = 8, 2, 1024, 512
+    q13, q2, c13, c2, gu, dn = _chan_experts(E, H, I, 60, cuda)
+    x = synthetic.hidden_states(32, H, 6).to(cuda)
+    g = torch.Generator().manual_seed(61)
+    rw = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    ids, _ = ops.router_topk(ops.router_logits(x, rw), K, ops.ORDER_TOPK_ACT, "softmax")
+    aff = torch.softmax(ops.router_logits(x, rw), dim=1)
+    idn = ids.cpu().numpy()
+    wts = np.take_along_axis(np_f32(aff), idn.astype(np.int64), 1)
+    post = M.ExpertAffinityScaleMode.POST_SCALE
+    row = M.moe_tkg(x, gu, dn, aff, ids, False, expert_gate_up_weights_scale=c13.reshape(E, 2, I).to(cuda),
+                    expert_down_weights_scale=c2.to(cuda), expert_affinities_scaling_mode=post)
+    err = rel_l2(np_f32(row), _chan_oracle(x, idn, wts, q13, q2, c13, c2))
+    say("moe_tkg row rel_l2", err)
+    assert err <= TOL_REL_L2, err
+    st13 = (torch.rand(E, 2, 1, generator=g) + 0.5) * (0.02 / 64)
+    st2 = (torch.rand(E, 1, generator=g) + 0.5) * (0.02 / 64)
+    static = M.moe_tkg(x, gu, dn, aff, ids, False, expert_gate_up_weights_scale=st13.to(cuda),
+                       expert_down_weights_scale=st2.to(cuda), expert_affinities_scaling_mode=post)
+    ref = _chan_oracle(x, idn, wts, q13, q2, st13.expand(E, 2, I).reshape(E, 2 * I),
+                       st2.expand(E, H))
+    err = rel_l2(np_f32(static), ref)
+    say("moe_tkg static rel_l2", err)
+    assert err <= TOL_REL_L2, err
+
+
+def test_moe_block_tkg_row_scales_with_shared_expert(cuda):
+    """moe_block_tkg with per-channel routed scales and a bf16 shared expert (quantized
+    to 128x128 blocks): the routed experts take the channel scales, the shared expert
+    none, in the same launch."""
+    say("moe_block_tkg row scales + shared")
+    E, K, H, I = 8, 2, 1024, 512
+    q13, q2, c13, c2, gu, dn = _chan_experts(E, H, I, 70, cuda)
+    g = torch.Generator().manual_seed(71)
+    x = synthetic.hidden_states(16, H, 7).to(cuda).reshape(1, 16, H)
+    gamma = (1 + 0.1 * torch.randn(1, H, generator=g)).to(cuda)
+    rw = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    sh = [(0.02 * torch.randn(*s, generator=g)).to(torch.bfloat16).to(cuda)
+          for s in ((H, I), (H, I), (I, H))]
+    out, lg = M.moe_block_tkg(x, gamma, rw.t(), gu, dn, top_k=K, shared_expert_gate_w=sh[0],
+                              shared_expert_up_w=sh[1], shared_expert_down_w=sh[2],
+                              expert_gate_up_weights_scale=c13.reshape(E, 2, I).to(cuda),
+                              expert_down_weights_scale=c2.to(cuda),
+                              router_act_fn=M.RouterActFnType.SOFTMAX,
+                              expert_affinities_scaling_mode=M.ExpertAffinityScaleMode.POST_SCALE)
+    sq = _experts.shared_weights(sh[0], sh[1], sh[2], I)
+    shared = (np_u8(sq[0][0]), np_f32(sq[1][0]), np_u8(sq[2][0]), np_f32(sq[3][0]))
+    E_, I2 = E, 2 * I
+    ones13 = np.ones((E_, I2 // 128, H // 128), np.float32)
+    ones2 = np.ones((E_, H // 128, I // 128), np.float32)
+    xs = np_f32(x.reshape(16, H))
+    ref, _, _, _ = moe_block_tkg_fp8(xs, np_f32(gamma), 1e-6, np_f32(rw), None, K, R.SOFTMAX, True,
+                                     False, True, q13.view(torch.uint8).numpy(), ones13,
+                                     q2.view(torch.uint8).numpy(), ones2, shared=shared,
+                                     logits=np_f32(lg), chan=(c13.numpy(), c2.numpy()))
+    err = rel_l2(np_f32(out), ref)
+    say("moe_block_tkg row scales rel_l2", err)
+    assert err <= TOL_REL_L2, err

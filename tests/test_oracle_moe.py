@@ -147,3 +147,33 @@ def test_block_tkg_scaling_modes_and_selection_order():
     c, *_ = moe_block_tkg_fp8(x[p], gamma, 1e-6, wr, None, 2, SOFTMAX, True, True, True, *ws)
     d, *_ = moe_block_tkg_fp8(x, gamma, 1e-6, wr, None, 2, SOFTMAX, True, True, True, *ws)
     assert np.array_equal(c, d[p])
+
+
+def test_channel_scales_equal_the_dense_form_and_scale_exactly():
+    """Per-channel weight scales (the reference's FP8 row / static formats): the sparse
+    form with chan = (c13, c2) equals _torch_moe_impl's dense form on weights whose rows
+    were multiplied by the scales beforehand; doubling the up-half scales or the down
+    scales doubles the output exactly (powers of two commute with every rounding)."""
+    from oracle.fp8 import dequant_act_1x128, quant_act_1x128
+    x, ids, w, q13, s13, q2, s2 = _small_layer(5)
+    E, I2, H = q13.shape
+    I = I2 // 2
+    T = x.shape[0]
+    rng = np.random.default_rng(6)
+    c13 = rng.uniform(0.5, 2.0, (E, I2)).astype(np.float32)
+    c2 = rng.uniform(0.5, 2.0, (E, H)).astype(np.float32)
+    got = moe_sparse_fp8(x, ids, w, q13, s13, q2, s2, requant_h=False, chan=(c13, c2))
+    xh = dequant_act_1x128(*quant_act_1x128(x))
+    w13 = np.stack([dequant_weight_128x128(q13[e], s13[e]) * c13[e][:, None] for e in range(E)])
+    w2 = np.stack([dequant_weight_128x128(q2[e], s2[e]) * c2[e][:, None] for e in range(E)])
+    gate_up = np.stack([w13[:, :I, :], w13[:, I:, :]], axis=2).transpose(0, 3, 2, 1)
+    aff = scatter_dense(ids, w, E).reshape(T * E, 1)
+    dense = moe_dense_reference(xh, aff, gate_up, w2.transpose(0, 2, 1))
+    assert np.allclose(got, dense, rtol=1e-4, atol=1e-5)
+    assert not np.allclose(got, moe_sparse_fp8(x, ids, w, q13, s13, q2, s2, requant_h=False),
+                           rtol=1e-2, atol=1e-3)
+    base = moe_sparse_fp8(x, ids, w, q13, s13, q2, s2, chan=(c13, c2))
+    up2 = c13.copy()
+    up2[:, I:] *= 2
+    assert np.array_equal(moe_sparse_fp8(x, ids, w, q13, s13, q2, s2, chan=(up2, c2)), 2 * base)
+    assert np.array_equal(moe_sparse_fp8(x, ids, w, q13, s13, q2, s2, chan=(c13, 2 * c2)), 2 * base)

@@ -247,18 +247,19 @@ static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const voi
                                w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
   if (!norm && !fz.quant_done) MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
   if (block) {
-    MOE_STEP(moe_expert_gate_up_block(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
-                                      w13_shared_scale, n_shared, w.tpid, (int)NB, w.btiles,
+    MOE_STEP(moe_expert_gate_up_block(w.xq, w.xs, T, H, I, E, w13, w13_scale, nullptr, w13_shared,
+                                      w13_shared_scale, nullptr, n_shared, w.tpid, (int)NB, w.btiles,
                                       w.bnum, mbt, w.hq, w.hs, stream));
-    MOE_STEP(moe_expert_down_block(w.hq, w.hs, T, H, I, E, w2, w2_scale, w2_shared,
-                                   w2_shared_scale, n_shared, (int)NB, w.btiles, w.bnum, mbt,
+    MOE_STEP(moe_expert_down_block(w.hq, w.hs, T, H, I, E, w2, w2_scale, nullptr, w2_shared,
+                                   w2_shared_scale, nullptr, n_shared, (int)NB, w.btiles, w.bnum, mbt,
                                    w.y, stream));
   } else {
-    MOE_STEP(moe_expert_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared,
-                                w13_shared_scale, n_shared, w.tpid, (int)NB, w.tiles,
+    MOE_STEP(moe_expert_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, nullptr, w13_shared,
+                                w13_shared_scale, nullptr, n_shared, w.tpid, (int)NB, w.tiles,
                                 w.num_tiles, max_tiles, mt, w.hq, w.hs, stream));
-    MOE_STEP(moe_expert_down(w.hq, w.hs, T, H, I, E, w2, w2_scale, w2_shared, w2_shared_scale,
-                             n_shared, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y,
+    MOE_STEP(moe_expert_down(w.hq, w.hs, T, H, I, E, w2, w2_scale, nullptr, w2_shared,
+                             w2_shared_scale, nullptr, n_shared, (int)NB, w.tiles, w.num_tiles,
+                             max_tiles, mt, w.y,
                              stream));
   }
   MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)R, n_shared, out_bf16, stream));

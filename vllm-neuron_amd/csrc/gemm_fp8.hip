@@ -47,6 +47,10 @@ struct GemmArgs {
   uint8_t* hq;
   float* hs;
   uint16_t* y;
+  // optional per-output-channel weight scales ([E, 2I] gate_up / [E, H] down, and
+  // the shared experts'): multiplied into each output column after the K loop
+  const float* cs;
+  const float* cssh;
   int T, H, I, E, nsh;
   long NB;
 };
@@ -319,6 +323,18 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
     }
     wait_vm<0>();  // the tail's repeated loads land before the stages are reused
 
+    // Per-output-channel weight scales, 1 when absent (a multiply by 1 is exact):
+    // accumulator column j of this wave is weight row nt * 128 + 32 wave + 16 j + r16
+    // (gate, j < 2; the up rows follow I later) or nt * 64 NW + 64 wave + 16 j + r16 (down).
+    float cw[4] = {1.f, 1.f, 1.f, 1.f};
+    if (const float* csb = is_sh ? p.cssh : p.cs) {
+      csb += (size_t)ej * ((KIND == 0) ? 2 * p.I : p.H);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        cw[j] = csb[(KIND == 0) ? ((j < 2 ? 0 : p.I) + nt * 128 + wave * 32 + (j & 1) * 16 + r16)
+                                : (nt * 64 * NW + wave * 64 + j * 16 + r16)];
+    }
+
     if (KIND == 0) {
       // h = SiLU(gate) * up, written over the gate accumulators.
 #pragma unroll
@@ -328,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
           float m = 0.f;
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) {
-            const float gt = acc[ms][jj][i], up = acc[ms][jj + 2][i];
+            const float gt = acc[ms][jj][i] * cw[jj], up = acc[ms][jj + 2][i] * cw[jj + 2];
             // hardware reciprocal (about 1 ulp): h only feeds the 1x128 fp8 quantization
             const float h = gt * __builtin_amdgcn_rcpf(1.0f + __expf(-gt)) * up;
             acc[ms][jj][i] = h;
@@ -370,7 +386,7 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int col = nt * 64 * NW + wave * 64 + j * 16 + r16;
-              p.y[(size_t)yrow * p.H + col] = (uint16_t)bf16x2(acc[ms][j][i], 0.f);
+              p.y[(size_t)yrow * p.H + col] = (uint16_t)bf16x2(acc[ms][j][i] * cw[j], 0.f);
             }
           }
         }
@@ -448,8 +464,10 @@ using namespace moe;
 
 extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
                                   const uint8_t* w13, const float* w13_scale,
-                                  const uint8_t* w13_shared, const float* w13_shared_scale,
-                                  int n_shared, const int32_t* token_position_to_id, int NB,
+                                  const float* w13_channel_scale, const uint8_t* w13_shared,
+                                  const float* w13_shared_scale,
+                                  const float* w13_shared_channel_scale, int n_shared,
+                                  const int32_t* token_position_to_id, int NB,
                                   const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
                                   int mt, uint8_t* hq, float* hs, void* stream) {
   MOE_API_BEGIN("moe_expert_gate_up");
@@ -473,6 +491,8 @@ extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int
   a.ws = w13_scale;
   a.wsh = w13_shared;
   a.wssh = w13_shared_scale;
+  a.cs = w13_channel_scale;
+  a.cssh = w13_shared_channel_scale;
   a.tpid = token_position_to_id;
   a.tiles = (const int4*)tiles;
   a.num_tiles = num_tiles;
@@ -490,8 +510,10 @@ extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int
 }
 
 extern "C" int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int E,
-                               const uint8_t* w2, const float* w2_scale, const uint8_t* w2_shared,
-                               const float* w2_shared_scale, int n_shared, int NB,
+                               const uint8_t* w2, const float* w2_scale,
+                               const float* w2_channel_scale, const uint8_t* w2_shared,
+                               const float* w2_shared_scale, const float* w2_shared_channel_scale,
+                               int n_shared, int NB,
                                const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
                                int mt, void* y_bf16, void* stream) {
   MOE_API_BEGIN("moe_expert_down");
@@ -514,6 +536,8 @@ extern "C" int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H,
   a.ws = w2_scale;
   a.wsh = w2_shared;
   a.wssh = w2_shared_scale;
+  a.cs = w2_channel_scale;
+  a.cssh = w2_shared_channel_scale;
   a.tiles = (const int4*)tiles;
   a.num_tiles = num_tiles;
   a.y = (uint16_t*)y_bf16;

@@ -70,6 +70,8 @@ struct BlkArgs {
   uint8_t* hq;
   float* hs;
   uint16_t* y;
+  const float* cs;    // optional per-output-channel weight scales (routed, shared)
+  const float* cssh;
   int T, H, I, E, nsh;
   long NB;
 };
@@ -529,6 +531,20 @@ __device__ __forceinline__ void block_item(const BlkArgs& p, const BlkLds& s, co
   // Accumulator layout (16x16): lane l, register i holds D[4*(l/16) + i][l%16];
   // with the tile's weight-row order, acc[m][n][i] of lane l is output column
   // 4 (l % 16) + n (gate_up, n < 4) or 8 (l % 16) + n (down) of the wave's half.
+  // Per-output-channel weight scales, when given, multiply each column first
+  // (workgroup-uniform branch).
+  if (const float* csb = is_sh ? p.cssh : p.cs) {
+    csb += (size_t)ej * ((KIND == 0) ? 2 * p.I : p.H);
+    float c[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+      c[n] = csb[(KIND == 0) ? ((n < 4 ? 0 : p.I) + nt * 128 + 64 * wn + 4 * l16 + (n & 3))
+                             : (nt * kBN + 128 * wn + 8 * l16 + n)];
+#pragma unroll
+    for (int m = 0; m < MF; ++m)
+#pragma unroll
+      for (int n = 0; n < 8; ++n) acc[m][n] *= c[n];
+  }
   if (KIND == 0) {
     // h = SiLU(gate) * up for this wave's 64 h columns; the row amax of the 1x128
     // group combines the two column-half waves through LDS.
@@ -778,8 +794,10 @@ static int block_gemm_common_checks(const char* _moe_fn, int T, int H, int I, in
 
 extern "C" int moe_expert_gate_up_block(const uint8_t* xq, const float* xs, int T, int H, int I,
                                         int E, const uint8_t* w13, const float* w13_scale,
-                                        const uint8_t* w13_shared, const float* w13_shared_scale,
-                                        int n_shared, const int32_t* token_position_to_id, int NB,
+                                        const float* w13_channel_scale, const uint8_t* w13_shared,
+                                        const float* w13_shared_scale,
+                                        const float* w13_shared_channel_scale, int n_shared,
+                                        const int32_t* token_position_to_id, int NB,
                                         const int32_t* tiles, const int32_t* num_tiles,
                                         int max_tiles, uint8_t* hq, float* hs, void* stream) {
   MOE_API_BEGIN("moe_expert_gate_up_block");
@@ -797,6 +815,8 @@ extern "C" int moe_expert_gate_up_block(const uint8_t* xq, const float* xs, int 
   a.ws = w13_scale;
   a.wsh = w13_shared;
   a.wssh = w13_shared_scale;
+  a.cs = w13_channel_scale;
+  a.cssh = w13_shared_channel_scale;
   a.tpid = token_position_to_id;
   a.tiles = (const int4*)tiles;
   a.seg = (const int2*)(tiles + 4 * (size_t)max_tiles);
@@ -815,8 +835,10 @@ extern "C" int moe_expert_gate_up_block(const uint8_t* xq, const float* xs, int 
 
 extern "C" int moe_expert_down_block(const uint8_t* hq, const float* hs, int T, int H, int I, int E,
                                      const uint8_t* w2, const float* w2_scale,
-                                     const uint8_t* w2_shared, const float* w2_shared_scale,
-                                     int n_shared, int NB, const int32_t* tiles,
+                                     const float* w2_channel_scale, const uint8_t* w2_shared,
+                                     const float* w2_shared_scale,
+                                     const float* w2_shared_channel_scale, int n_shared, int NB,
+                                     const int32_t* tiles,
                                      const int32_t* num_tiles, int max_tiles, void* y_bf16,
                                      void* stream) {
   MOE_API_BEGIN("moe_expert_down_block");
@@ -834,6 +856,8 @@ extern "C" int moe_expert_down_block(const uint8_t* hq, const float* hs, int T, 
   a.ws = w2_scale;
   a.wsh = w2_shared;
   a.wssh = w2_shared_scale;
+  a.cs = w2_channel_scale;
+  a.cssh = w2_shared_channel_scale;
   a.tiles = (const int4*)tiles;
   a.seg = (const int2*)(tiles + 4 * (size_t)max_tiles);
   a.num_tiles = num_tiles;

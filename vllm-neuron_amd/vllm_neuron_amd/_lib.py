@@ -11,7 +11,7 @@ import os
 import threading
 
 _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libmoe_fp8.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 NOALLOC_SCRATCH_BYTES = 64 << 20  # MOE_NOALLOC_SCRATCH_BYTES
 
 MOE_OK, MOE_ERR_ARG, MOE_ERR_UNSUPPORTED, MOE_ERR_HIP = 0, -1, -2, -3
@@ -40,10 +40,10 @@ PROTOTYPES = {
     "moe_act_quant_1x128": (_i, [_p, _i, _i, _p, _p, _p]),
     "moe_max_tiles": (_i, [_i, _i, _i, _i, _i, _i, _i]),
     "moe_build_tiles": (_i, [_p, _p, _i, _i, _i, _i, _i, _i, _p, _i, _p, _p]),
-    "moe_expert_gate_up": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _p, _p, _i,
-                                _i, _p, _p, _p]),
-    "moe_expert_down": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _i, _p,
-                             _p]),
+    "moe_expert_gate_up": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p, _i, _p, _p,
+                                _i, _i, _p, _p, _p]),
+    "moe_expert_down": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p, _p, _i, _i,
+                             _p, _p]),
     "moe_combine": (_i, [_p, _p, _p, _i, _i, _i, _i, _i, _p, _p]),
     "moe_layer_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i, _i]),
     "moe_layer_forward": (_i, [_p, _p, _p, _f, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p, _i, _i, _i,
@@ -55,10 +55,10 @@ PROTOTYPES = {
     "moe_max_block_tiles": (_i, [_i, _i, _i, _i, _i, _i]),
     "moe_block_tiles_workspace_bytes": (_sz, [_i, _i]),
     "moe_build_block_tiles": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _i, _p, _p, _sz, _p]),
-    "moe_expert_gate_up_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _p, _i, _p, _p,
-                                      _i, _p, _p, _p]),
-    "moe_expert_down_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _i, _i, _p, _p, _i, _p,
-                                   _p]),
+    "moe_expert_gate_up_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p, _i,
+                                      _p, _p, _i, _p, _p, _p]),
+    "moe_expert_down_block": (_i, [_p, _p, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p, _p,
+                                   _i, _p, _p]),
     "moe_act_quant_mx": (_i, [_p, _i, _i, _p, _p, _p]),
     "moe_expert_gate_up_mx": (_i, [_p, _p, _i, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _p, _i,
                                    _p, _p, _i, _i, _i, _f, _f, _f, _f, _p, _p, _p]),

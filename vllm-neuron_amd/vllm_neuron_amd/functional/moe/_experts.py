@@ -3,7 +3,8 @@
 The operator API of the reference passes expert weights per call in its own
 layout (gate_up [E, H, 2, I], down [E, I, H]; moe_cte.py:122-131). The HIP
 kernels read the DeepSeek-V3 checkpoint stacking (w13 [E, 2I, H], w2 [E, H, I],
-128x128 fp32 block scales), which is K-contiguous. Both are accepted here; the
+128x128 fp32 block scales, or per-output-channel scales), which is K-contiguous.
+Both are accepted here; the
 reference layout is converted once per weight tensor and the result cached
 (a second copy of the experts while the caller keeps the originals: pass the
 stacked layout to avoid it).
@@ -87,13 +88,61 @@ def weight_dims(gate_up, down):
     return E, H, I
 
 
-def routed_weights(gate_up, down, gate_up_scale=None, down_scale=None):
-    """(w13, w13_scale, w2, w2_scale) in the kernels' layout from either layout.
+def _channel_scales(gate_up_scale, down_scale, E, H, I, block13, block2):
+    """The reference's FP8 per-channel weight-scale formats as fp32 (c13 [E, 2I],
+    c2 [E, H]), or (None, None) when both scales are 128x128 blocks (shapes block13 /
+    block2) or absent. Accepted: gate_up [E, 1, 2I] (moe_cte shard_on_block,
+    moe_cte.py:178-181: gate channels, then up), [E, 2, I] (moe_tkg row
+    quantization, moe_tkg.py:87-88), [E, 2, 1] (moe_tkg static, :88-89), [E, 2I];
+    down [E, 1, H] (moe_cte.py:186-188), [E, H] (moe_tkg row, :90), [E, 1] (moe_tkg
+    static, :90-91). Both scales must use the same family (block or channel)."""
+    def is_block(t, shape):
+        return t is None or tuple(t.shape) == shape
 
-    Stacked: gate_up [E, 2I, H], gate_up_scale [E, 2I/128, H/128]; down [E, H, I],
-    down_scale [E, H/128, I/128]. Reference: gate_up [E, H, 2, I], gate_up_scale
-    [E, H/128, 2, I/128]; down [E, I, H], down_scale [E, I/128, H/128]. Missing
-    scales mean 1.0 (codes used as values)."""
+    if is_block(gate_up_scale, block13) and is_block(down_scale, block2):
+        return None, None
+
+    def chan13(t):
+        if t is None:
+            return torch.ones(E, 2 * I, device=dev)
+        sh = tuple(t.shape)
+        if sh in ((E, 1, 2 * I), (E, 2 * I)):
+            return t.reshape(E, 2 * I).float()
+        if sh in ((E, 2, I), (E, 2, 1)):
+            return t.float().expand(E, 2, I).reshape(E, 2 * I)
+        raise NotImplementedError(
+            f"gate_up_proj_scale {sh}: supported are 128x128 blocks {block13} and the per-channel "
+            f"[E, 1, 2I] / [E, 2, I] / [E, 2, 1] (E={E}, I={I})")
+
+    def chan2(t):
+        if t is None:
+            return torch.ones(E, H, device=dev)
+        sh = tuple(t.shape)
+        if sh in ((E, 1, H), (E, H)):
+            return t.reshape(E, H).float()
+        if sh == (E, 1):
+            return t.float().expand(E, H)
+        raise NotImplementedError(
+            f"down_proj_scale {sh}: supported are 128x128 blocks {block2} and the per-channel "
+            f"[E, 1, H] / [E, H] / [E, 1] (E={E}, H={H})")
+
+    dev = (gate_up_scale if gate_up_scale is not None else down_scale).device
+    if (gate_up_scale is not None and tuple(gate_up_scale.shape) == block13) or \
+            (down_scale is not None and tuple(down_scale.shape) == block2):
+        raise NotImplementedError("gate_up and down scales mix 128x128 blocks and per-channel scales")
+    return chan13(gate_up_scale).contiguous(), chan2(down_scale).contiguous()
+
+
+def routed_weights(gate_up, down, gate_up_scale=None, down_scale=None):
+    """(w13, w13_scale, w2, w2_scale, w13_chan, w2_chan) in the kernels' layout from either
+    layout.
+
+    Stacked: gate_up [E, 2I, H], down [E, H, I]; reference: gate_up [E, H, 2, I], down
+    [E, I, H] (moe_cte.py:122-131). Scales are 128x128 blocks (stacked [E, 2I/128, H/128]
+    / [E, H/128, I/128]; reference [E, H/128, 2, I/128] / [E, I/128, H/128]), in which
+    case the channel scales are None, or the reference's FP8 per-channel formats (see
+    _channel_scales), in which case the block scales are ones and the channel scales
+    carry them. Missing scales mean 1.0 (codes used as values)."""
     _need_fp8(gate_up, "gate_up_proj_weight")
     _need_fp8(down, "down_proj_weight")
     dev = gate_up.device
@@ -103,18 +152,15 @@ def routed_weights(gate_up, down, gate_up_scale=None, down_scale=None):
         if tuple(down.shape) != (E, H, I):
             raise ValueError(f"down_proj_weight must be [E, H, I] = {(E, H, I)} for a stacked "
                              f"gate_up [E, 2I, H], got {tuple(down.shape)}")
+        c13, c2 = _channel_scales(gate_up_scale, down_scale, E, H, I, (E, I2 // 128, H // 128),
+                                  (E, H // 128, I // 128))
+        if c13 is not None:
+            return (gate_up.contiguous(), _ones_scale(E, I2, H, dev), down.contiguous(),
+                    _ones_scale(E, H, I, dev), c13, c2)
         s13 = gate_up_scale if gate_up_scale is not None else _ones_scale(E, I2, H, dev)
         s2 = down_scale if down_scale is not None else _ones_scale(E, H, I, dev)
-        if tuple(s13.shape) != (E, I2 // 128, H // 128):
-            raise NotImplementedError(
-                f"gate_up_proj_scale {tuple(s13.shape)}: only 128x128 block scales "
-                f"[E, 2I/128, H/128] = {(E, I2 // 128, H // 128)} are supported")
-        if tuple(s2.shape) != (E, H // 128, I // 128):
-            raise NotImplementedError(
-                f"down_proj_scale {tuple(s2.shape)}: only 128x128 block scales "
-                f"[E, H/128, I/128] = {(E, H // 128, I // 128)} are supported")
         return (gate_up.contiguous(), s13.float().contiguous(), down.contiguous(),
-                s2.float().contiguous())
+                s2.float().contiguous(), None, None)
     if gate_up.dim() != 4 or gate_up.shape[2] != 2:
         raise ValueError(f"gate_up_proj_weight must be [E, H, 2, I] or [E, 2I, H], got "
                          f"{tuple(gate_up.shape)}")
@@ -122,24 +168,22 @@ def routed_weights(gate_up, down, gate_up_scale=None, down_scale=None):
     if tuple(down.shape) != (E, I, H):
         raise ValueError(f"down_proj_weight must be [E, I, H] = {(E, I, H)}, got "
                          f"{tuple(down.shape)}")
-    if gate_up_scale is not None and tuple(gate_up_scale.shape) != (E, H // 128, 2, I // 128):
-        raise NotImplementedError(
-            f"gate_up_proj_scale {tuple(gate_up_scale.shape)}: only 128x128 block scales "
-            f"[E, H/128, 2, I/128] are supported")
-    if down_scale is not None and tuple(down_scale.shape) != (E, I // 128, H // 128):
-        raise NotImplementedError(
-            f"down_proj_scale {tuple(down_scale.shape)}: only 128x128 block scales "
-            f"[E, I/128, H/128] are supported")
+    c13, c2 = _channel_scales(gate_up_scale, down_scale, E, H, I, (E, H // 128, 2, I // 128),
+                              (E, I // 128, H // 128))
+    if c13 is None:
+        gate_up_block, down_block = gate_up_scale, down_scale
+    else:
+        gate_up_block = down_block = None
 
     def build():
         w13 = gate_up.permute(0, 2, 3, 1).reshape(E, 2 * I, H).contiguous()
-        if gate_up_scale is None:
+        if gate_up_block is None:
             s13 = _ones_scale(E, 2 * I, H, dev)
         else:
-            s13 = gate_up_scale.permute(0, 2, 3, 1).reshape(E, 2 * I // 128, H // 128)
+            s13 = gate_up_block.permute(0, 2, 3, 1).reshape(E, 2 * I // 128, H // 128)
         w2 = down.transpose(1, 2).contiguous()
-        s2 = _ones_scale(E, H, I, dev) if down_scale is None else down_scale.transpose(1, 2)
-        return w13, s13.float().contiguous(), w2, s2.float().contiguous()
+        s2 = _ones_scale(E, H, I, dev) if down_block is None else down_block.transpose(1, 2)
+        return w13, s13.float().contiguous(), w2, s2.float().contiguous(), c13, c2
 
     srcs = (gate_up, down, gate_up_scale, down_scale)
     return _cached(("nf",) + _key(*srcs), build, srcs)
@@ -185,12 +229,16 @@ def shared_weights(gate_w, up_w, down_w, I):
     return _cached(("shared", I) + _key(*srcs), build, srcs)
 
 
-def make_weights(w13, s13, w2, s2, shared=None):
+def make_weights(w13, s13, w2, s2, c13=None, c2=None, shared=None):
+    """Fp8MoEWeights of routed experts (with optional channel scales c13 / c2) and
+    optional shared experts (w13, s13, w2, s2); shared experts without channel scales
+    get unit ones when the routed experts have them."""
     kw = {}
     if shared is not None:
         kw = dict(shared_w13=shared[0], shared_w13_scale=shared[1], shared_w2=shared[2],
                   shared_w2_scale=shared[3])
-    return Fp8MoEWeights(router_w=None, w13=w13, w13_scale=s13, w2=w2, w2_scale=s2, **kw)
+    return Fp8MoEWeights(router_w=None, w13=w13, w13_scale=s13, w2=w2, w2_scale=s2,
+                         w13_chan=c13, w2_chan=c2, **kw)
 
 
 def as_bf16(x):

@@ -21,7 +21,9 @@ the experts' 1x128 quantization in one pass; fp32 input: moe_rms_norm) -> moe_ro
 the reference's fp32 matmul of bf16 values) -> moe_router_topk -> blockwise
 mapping -> fp8 experts -> combine. Routed experts are float8_e4m3fn with
 128x128 block scales (expert_gate_up_weights_scale / expert_down_weights_scale
-in the block-scale shapes); floating-point shared-expert weights are quantized
+in the block-scale shapes) or the reference's FP8 per-channel scales (row
+[E, 2, I] / [E, H], static [E, 2, 1] / [E, 1], moe_tkg.py:87-91, applied per
+output column by the GEMM epilogues); floating-point shared-expert weights are quantized
 once to the same format. router_mm_dtype is accepted for signature
 compatibility; the logits are always accumulated in fp32. The GPU work is one
 torch.library operator (moe_fp8::moe_block_tkg), an opaque node under torch.compile.
@@ -185,7 +187,7 @@ def _block_tkg_op(x: Tensor, gamma: Tensor, router_weights: Tensor, gate_up: Ten
     Returns (out [T, H], logits [T, E] fp32, residual_out [T, H] or [0, H])."""
     T, H = x.shape
     ha = None if hidden_actual <= 0 else hidden_actual
-    w13, s13, w2, s2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
+    w13, s13, w2, s2, c13, c2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
     I = w13.shape[1] // 2
     # 1. (residual add, :341, :421-428) RMSNorm, cast back to the input dtype (:135-151).
     # bf16 input: one fused pass that also quantizes the normalized rows for the experts.
@@ -215,7 +217,7 @@ def _block_tkg_op(x: Tensor, gamma: Tensor, router_weights: Tensor, gate_up: Ten
     shared = None
     if shared_gate is not None:
         shared = _experts.shared_weights(shared_gate, shared_up, shared_down, I)
-    w = _experts.make_weights(w13, s13, w2, s2, shared)
+    w = _experts.make_weights(w13, s13, w2, s2, c13, c2, shared)
     out = _experts.routed_forward(_experts.as_bf16(xn), ids, wts, w, xq=xq, xs=xs)
     if x.dtype != torch.bfloat16:
         out = out.to(x.dtype)

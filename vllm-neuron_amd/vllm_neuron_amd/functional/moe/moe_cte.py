@@ -13,7 +13,10 @@ token_position_to_id / block_to_expert -> fp8 gate_up with SiLU * up and the
 dense affinities in expert order. Experts are float8_e4m3fn with 128x128 fp32
 block scales, in the reference layout (gate_up [E, H, 2, I], scales
 [E, H/128, 2, I/128]; down [E, I, H], scales [E, I/128, H/128]) or the
-checkpoint stacking (gate_up [E, 2I, H], down [E, H, I]).
+checkpoint stacking (gate_up [E, 2I, H], down [E, H, I]), or with the
+reference's FP8 per-channel scales gate_up_proj_scale [E, 1, 2I] and
+down_proj_scale [E, 1, H] (moe_cte.py:178-188), which the GEMM epilogues apply
+per output column.
 
 Supported: SiLU, POST_SCALE and NO_SCALE, implementation shard_on_block /
 shard_on_i / shard_on_i_hybrid / shard_on_i_dropping (one kernel family serves
@@ -151,7 +154,7 @@ def _moe_cte_op(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up
                 no_scale: bool) -> Tensor:
     """Opaque graph node of moe_cte (arguments checked by moe_cte): the experts of a
     mapping, combined per token with the dense affinities in expert order."""
-    w13, s13, w2, s2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
+    w13, s13, w2, s2, c13, c2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
     E, H = w13.shape[0], w13.shape[2]
     T = expert_affinities_masked.numel() // E
     B = block_size
@@ -159,7 +162,7 @@ def _moe_cte_op(hidden_states: Tensor, expert_affinities_masked: Tensor, gate_up
     b2e = block_to_expert.contiguous()
     N = b2e.numel()
     x = _experts.as_bf16(hidden_states[:T]).contiguous()
-    w = _experts.make_weights(w13, s13, w2, s2)
+    w = _experts.make_weights(w13, s13, w2, s2, c13, c2)
     # Expected routed rows per token from the mapping size (N ~ T*K/B + E - 1);
     # it only picks the tile height. Tile lists are sized for any mapping (K = E).
     k_rows = max(1, min(E, ((N - E + 1) * B + E - 1) // max(T, 1)))

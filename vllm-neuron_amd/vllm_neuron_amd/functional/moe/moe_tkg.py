@@ -8,11 +8,13 @@ mask_unselected_experts). Compute path (all HIP): align-by-expert mapping of
 the ids, fp8 1x128 activation quant, fp8 gate_up + SiLU * up, fp8 down,
 combine in k order with fp32 accumulation.
 
-Experts are float8_e4m3fn with 128x128 fp32 block scales in the reference
-layout ([E, H, 2, I] / [E, I, H]) or the checkpoint stacking; the reference's
-row-wise and static fp8 scale shapes, MX weights, biases, clamps, non-SiLU
+Experts are float8_e4m3fn in the reference layout ([E, H, 2, I] / [E, I, H]) or
+the checkpoint stacking, with 128x128 fp32 block scales or the reference's FP8
+per-channel scales: row quantization [E, 2, I] / [E, H] and static [E, 2, 1] /
+[E, 1] (moe_tkg.py:87-91), applied per output column by the GEMM epilogues.
+Static activation input scales, MX weights, biases, clamps, non-SiLU
 activations, A2A-v layouts and expert-parallel slicing raise
-NotImplementedError.
+NotImplementedError (activations are quantized dynamically per 1x128 group).
 """
 from typing import Optional
 
@@ -113,9 +115,9 @@ def _moe_tkg_op(hidden_input: Tensor, gate_up: Tensor, down: Tensor,
                 wts: Tensor, output_dtype: torch.dtype) -> Tensor:
     """Opaque graph node of moe_tkg (arguments checked by moe_tkg): experts ids [T, K]
     weighted by wts [T, K], combined per token in k order."""
-    w13, s13, w2, s2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
+    w13, s13, w2, s2, c13, c2 = _experts.routed_weights(gate_up, down, gate_up_scale, down_scale)
     x = _experts.as_bf16(hidden_input).contiguous()
-    w = _experts.make_weights(w13, s13, w2, s2)
+    w = _experts.make_weights(w13, s13, w2, s2, c13, c2)
     out = _experts.routed_forward(x, ids, wts, w)
     return out if output_dtype == torch.bfloat16 else out.to(output_dtype)
 

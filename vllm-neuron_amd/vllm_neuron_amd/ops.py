@@ -259,8 +259,9 @@ def expert_gate_up(xq, xs, w, tpid, NB, tiles, num_tiles, max_tiles, mt):
     hq = torch.empty(P, I, device=xq.device, dtype=FP8)
     hs = torch.empty(P, I // 128, device=xq.device, dtype=torch.float32)
     _lib.call("moe_expert_gate_up", ptr(_u8(xq)), ptr(xs), T, H, I, E, ptr(_u8(w.w13)),
-              ptr(w.w13_scale), ptr(_u8(w.shared_w13)) if S else None,
-              ptr(w.shared_w13_scale) if S else None, S, ptr(tpid), NB, ptr(tiles),
+              ptr(w.w13_scale), ptr(w.w13_chan), ptr(_u8(w.shared_w13)) if S else None,
+              ptr(w.shared_w13_scale) if S else None, ptr(w.shared_w13_chan) if S else None, S,
+              ptr(tpid), NB, ptr(tiles),
               ptr(num_tiles), max_tiles, mt, ptr(_u8(hq)), ptr(hs), _stream())
     return hq, hs
 
@@ -270,8 +271,9 @@ def expert_down(hq, hs, w, T, NB, tiles, num_tiles, max_tiles, mt):
     S = w.n_shared
     y = torch.empty(hq.shape[0], H, device=hq.device, dtype=torch.bfloat16)
     _lib.call("moe_expert_down", ptr(_u8(hq)), ptr(hs), T, H, I, E, ptr(_u8(w.w2)),
-              ptr(w.w2_scale), ptr(_u8(w.shared_w2)) if S else None,
-              ptr(w.shared_w2_scale) if S else None, S, NB, ptr(tiles), ptr(num_tiles),
+              ptr(w.w2_scale), ptr(w.w2_chan), ptr(_u8(w.shared_w2)) if S else None,
+              ptr(w.shared_w2_scale) if S else None, ptr(w.shared_w2_chan) if S else None, S, NB,
+              ptr(tiles), ptr(num_tiles),
               max_tiles, mt, ptr(y), _stream())
     return y
 
@@ -307,8 +309,9 @@ def expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num_tiles, max_tiles):
     hq = torch.empty(NB + S * T, I, device=xq.device, dtype=FP8)
     hs = torch.empty(NB + S * T, I // 128, device=xq.device, dtype=torch.float32)
     _lib.call("moe_expert_gate_up_block", ptr(_u8(xq)), ptr(xs), T, H, I, E, ptr(_u8(w.w13)),
-              ptr(w.w13_scale), ptr(_u8(w.shared_w13)) if S else None,
-              ptr(w.shared_w13_scale) if S else None, S, ptr(tpid), NB, ptr(tiles),
+              ptr(w.w13_scale), ptr(w.w13_chan), ptr(_u8(w.shared_w13)) if S else None,
+              ptr(w.shared_w13_scale) if S else None, ptr(w.shared_w13_chan) if S else None, S,
+              ptr(tpid), NB, ptr(tiles),
               ptr(num_tiles), max_tiles, ptr(_u8(hq)), ptr(hs), _stream())
     return hq, hs
 
@@ -318,8 +321,9 @@ def expert_down_block(hq, hs, w, T, NB, tiles, num_tiles, max_tiles):
     S = w.n_shared
     y = torch.empty(hq.shape[0], H, device=hq.device, dtype=torch.bfloat16)
     _lib.call("moe_expert_down_block", ptr(_u8(hq)), ptr(hs), T, H, I, E, ptr(_u8(w.w2)),
-              ptr(w.w2_scale), ptr(_u8(w.shared_w2)) if S else None,
-              ptr(w.shared_w2_scale) if S else None, S, NB, ptr(tiles), ptr(num_tiles),
+              ptr(w.w2_scale), ptr(w.w2_chan), ptr(_u8(w.shared_w2)) if S else None,
+              ptr(w.shared_w2_scale) if S else None, ptr(w.shared_w2_chan) if S else None, S, NB,
+              ptr(tiles), ptr(num_tiles),
               max_tiles, ptr(y), _stream())
     return y
 
@@ -372,6 +376,13 @@ def selftest_mfma(a, b, shape=0):
 
 # ---------------------------------------------------------------- whole layer
 
+def _no_channel_scales(w):
+    if getattr(w, "has_channel_scales", False):
+        raise NotImplementedError(
+            "the whole-layer entry takes 128x128 block-scaled experts; experts with per-channel "
+            "scales run through the operator path (functional.moe.moe_cte / moe_tkg)")
+
+
 def layer_forward(x, w, cfg, return_routing=False, gamma=None, eps=1e-6, hidden_actual=None,
                   residual=None):
     """Whole layer on the HIP path.
@@ -382,6 +393,7 @@ def layer_forward(x, w, cfg, return_routing=False, gamma=None, eps=1e-6, hidden_
     Returns out [T,H] bf16; (out, residual_sum) when a residual is given; the
     routing (ids, weights, logits) is appended when return_routing."""
     _need_cuda(x, w.w13, gamma, residual)
+    _no_channel_scales(w)
     T, H = x.shape
     _need(x, torch.bfloat16, (T, H), "hidden_states")
     if residual is not None:
@@ -426,6 +438,7 @@ def layer_forward_noalloc(x, w, cfg, return_routing=False, gamma=None, eps=1e-6,
     scratch replaces the workspace, so only the outputs are allocated here (by the
     caller, in code that must not allocate). Same arguments and results."""
     _need_cuda(x, w.w13, gamma, residual)
+    _no_channel_scales(w)
     T, H = x.shape
     _need(x, torch.bfloat16, (T, H), "hidden_states")
     if residual is not None:

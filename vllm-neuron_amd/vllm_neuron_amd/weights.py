@@ -60,6 +60,13 @@ class Fp8MoEWeights:
     shared_w13_scale: Optional[torch.Tensor] = None
     shared_w2: Optional[torch.Tensor] = None    # [S, H, I] e4m3fn
     shared_w2_scale: Optional[torch.Tensor] = None
+    # Optional per-output-channel weight scales (the reference's FP8 row / static
+    # formats, moe_cte.py:178-188, moe_tkg.py:87-91): W = q * block_scale * chan[row],
+    # with all-ones block scales. fp32 [E, 2I] / [E, H] (and [S, 2I] / [S, H]).
+    w13_chan: Optional[torch.Tensor] = None
+    w2_chan: Optional[torch.Tensor] = None
+    shared_w13_chan: Optional[torch.Tensor] = None
+    shared_w2_chan: Optional[torch.Tensor] = None
 
     @property
     def n_experts(self):
@@ -98,7 +105,17 @@ class Fp8MoEWeights:
             S = self.shared_w13.shape[0]
             if tuple(self.shared_w13.shape) != (S, I2, H) or tuple(self.shared_w2.shape) != (S, H, I):
                 raise ValueError("shared expert weights must be [S, 2I, H] / [S, H, I]")
+        for name, t, shape in (("w13_chan", self.w13_chan, (E, I2)), ("w2_chan", self.w2_chan, (E, H)),
+                               ("shared_w13_chan", self.shared_w13_chan, (self.n_shared, I2)),
+                               ("shared_w2_chan", self.shared_w2_chan, (self.n_shared, H))):
+            if t is not None and (tuple(t.shape) != shape or t.dtype != torch.float32):
+                raise ValueError(f"{name} must be fp32 {shape}, got {t.dtype} {tuple(t.shape)}")
         return self
+
+    @property
+    def has_channel_scales(self):
+        return any(t is not None for t in (self.w13_chan, self.w2_chan, self.shared_w13_chan,
+                                           self.shared_w2_chan))
 
 
 def from_checkpoint_tensors(items, n_experts):
