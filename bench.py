@@ -463,6 +463,8 @@ def cpu_dense_small(x, w, cfg, reps=3):
 # weight seed, input seed, Zipf routing
 ONLY = {
     "dsv3_prefill8k": ("DeepSeek-V3 MoE layer, 8192 tokens", "dsv3", 8192, 1, 2, False),
+    "kimi_k2_1": ("Kimi-K2 MoE layer, 1 token", "kimi_k2", 1, 3, 3, False),
+    "dsv3_decode64": ("DeepSeek-V3 MoE layer, decode 64 tokens", "dsv3", 64, 1, 1, False),
     "kimi_k2_2048": ("Kimi-K2 MoE layer, 2048 tokens", "kimi_k2", 2048, 3, 3, False),
     "kimi_k2_16384": ("Kimi-K2 MoE layer, 16384 tokens", "kimi_k2", 16384, 3, 3, False),
     "glm45_zipf4096": ("GLM-4.5 MoE layer, 4096 tokens, Zipf(1.2) routing, 10% empty experts",

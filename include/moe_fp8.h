@@ -199,10 +199,14 @@ int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int
  * expert per tile: `tiles` is max_tiles * 24 bytes (int32x4 tiles followed by
  * int32x2 {first tile, tile count} of each tile's expert), built by
  * moe_build_block_tiles with a scratch workspace of
- * moe_block_tiles_workspace_bytes(N, max_tiles). Same outputs as
+ * moe_block_tiles_workspace_bytes(N, max_tiles). Its `num_tiles` is a header of
+ * MOE_BLOCK_TILES_HEADER int32: the tile count, then the first tile of each XCD's
+ * range (9 values: ranges of whole experts with about equal work), which the block
+ * GEMMs read. Same outputs as
  * moe_expert_gate_up / moe_expert_down (same replaced reference interface,
  * moe_cte.py:356-421 and :557-588); the layer uses them when the average
  * expert receives more than 32 rows. */
+#define MOE_BLOCK_TILES_HEADER 16
 int moe_max_block_tiles(int T, int K, int E, int N, int B, int n_shared);
 size_t moe_block_tiles_workspace_bytes(int N, int max_tiles);
 int moe_build_block_tiles(const int32_t* token_position_to_id, const int32_t* block_to_expert,

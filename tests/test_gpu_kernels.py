@@ -266,7 +266,8 @@ def test_block_tiles_cover_every_slot_once(cuda, T, K, E, B, S):
     ids = np.stack([rng.choice(E, K, replace=False, p=p) for _ in range(T)]).astype(np.int32)
     m = ops.blockwise_mapping(ids=torch.from_numpy(ids).to(cuda), n_experts=E, block_size=B)
     tiles, num, mx = ops.build_block_tiles(m["token_position_to_id"], m["block_to_expert"], B, T, K, E, S)
-    n = int(num.item())
+    hdr = num.cpu().numpy()
+    n = int(hdr[0])
     raw = tiles.cpu().numpy()
     tl = raw[: 4 * mx].reshape(mx, 4)[:n]
     sg = raw[4 * mx:].reshape(mx, 2)[:n]
@@ -283,6 +284,25 @@ def test_block_tiles_cover_every_slot_once(cuda, T, K, E, B, S):
             assert np.all(b2e[np.arange(s0, s0 + rows) // B] == e)
     assert np.all(seen[:NB][tpid >= 0] == 1) and np.all(seen[NB:] == 1)
     assert np.all(seen[:NB][tpid < 0] <= 1)
+    # XCD ranges: a partition of the tiles into 8 runs of at most cap tiles (the grid's
+    # share per XCD); a cut leaves an expert boundary only where the cap forces it, and
+    # with every cut on a boundary each range is within one expert's cost of an equal
+    # share (tile cost 3 + ceil(rows / 64))
+    cut = hdr[1:10]
+    cap = max(3 * mx // 16, (mx + 7) // 8)
+    assert cut[0] == 0 and cut[8] == n and np.all(np.diff(cut) >= 0), cut
+    assert np.all(np.diff(cut) <= cap), (cut, cap)
+    on_boundary = [c in (0, n) or tl[c, 0] != tl[c - 1, 0] for c in cut[1:8]]
+    for x, ok in zip(range(1, 8), on_boundary):
+        assert ok or cut[x] in (cut[x - 1] + cap, n - (8 - x) * cap), (x, cut, cap)
+    if all(on_boundary):
+        cost = 3 + (tl[:, 2] + 63) // 64
+        pref = np.concatenate([[0], np.cumsum(cost)])
+        share = pref[-1] / 8
+        seg_cost = max(pref[f + c] - pref[f] for f, c in sg)
+        for x in range(8):
+            assert pref[cut[x + 1]] - pref[cut[x]] <= share + seg_cost, (x, cut, share, seg_cost)
+    say("block tiles", n, "tiles, XCD cuts", cut.tolist(), "cap", cap)
 
 
 @pytest.mark.parametrize("T,K,S,with_w", [(64, 8, 1, True), (300, 6, 0, True), (5, 2, 2, False),

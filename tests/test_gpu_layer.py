@@ -454,7 +454,7 @@ def test_block_kernels_every_tile_height(cuda):
     NB = tpid.numel()
     xq, xs = ops.act_quant(x)
     tiles, num, mx = ops.build_block_tiles(tpid, b2e, 256, T, 1, 8, 1)
-    rows = sorted(tiles[:4 * int(num.item())].cpu().numpy().reshape(-1, 4)[:, 2].tolist())
+    rows = sorted(tiles[:4 * int(num[0].item())].cpu().numpy().reshape(-1, 4)[:, 2].tolist())
     assert {(r - 1) // 64 for r in rows} == {0, 1, 2, 3}, rows
     hq, hs = ops.expert_gate_up_block(xq, xs, w, tpid, NB, tiles, num, mx)
     y = ops.expert_down_block(hq, hs, w, T, NB, tiles, num, mx)

@@ -119,7 +119,7 @@ static LayerWs carve(char* base, int T, int H, int I, int E, int K, int n_sh, in
   if (use_block(T, K, E)) {
     const int mbt = moe_max_block_tiles(T, K, E, N, B, n_sh);
     w.btiles = (int32_t*)take((size_t)mbt * 24);
-    w.bnum = (int32_t*)take(16);
+    w.bnum = (int32_t*)take(MOE_BLOCK_TILES_HEADER * 4);  // count + XCD ranges
   }
   w.bytes = off;
   return w;

@@ -39,6 +39,7 @@
 // Fragment lane layout (16x16x128): lane l supplies row l%16 and the bytes
 // [(l/16)*16, +16) and [64 + (l/16)*16, +16) of the 128-wide K block, the same
 // mapping for A and B. Accumulator: lane l, register i holds D[4*(l/16) + i][l%16].
+#include "mapping.h"
 #include "moe_common.h"
 #include "moe_internal.h"
 
@@ -620,15 +621,15 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
   __shared__ float sW[2][kMaxKB];
   const BlkLds s{sTA, sTB0, sTB1, sTB2, sSA, sDummy, sR0, sR1, sLast, sSrc, sRed, sW};
 
-  // XCD-aware item index: workgroup b runs on XCD b % 8; XCD x takes the
-  // contiguous item range [x * per, (x + 1) * per).
+  // XCD-aware item index: workgroup b runs on XCD b % 8, and XCD x takes the items
+  // of tiles [cut[x], cut[x + 1]) of the list's header (whole experts, about equal
+  // cost; see block_tile_cuts), in order. A range holds at most
+  // block_tiles_cap(max_tiles) tiles, and the grid gives each XCD that many items'
+  // workgroups.
   const int NT = (KIND == 0) ? p.I / 128 : p.H / kBN;
-  const int count = p.num_tiles[0] * NT;
-  const int per = (count + 7) / 8;
-  const int jx = blockIdx.x >> 3;
-  if (jx >= per) return;
-  const int L = (blockIdx.x & 7) * per + jx;
-  if (L >= count) return;
+  const int x = blockIdx.x & 7;
+  const int L = p.num_tiles[1 + x] * NT + (int)(blockIdx.x >> 3);
+  if (L >= p.num_tiles[2 + x] * NT) return;
   const int2 sg = p.seg[L / NT];
   const int r0 = L - NT * sg.x;
   const int nt = r0 / sg.y;
@@ -653,6 +654,7 @@ __global__ __launch_bounds__(kBlkThreads) void expert_gemm_block_kernel(BlkArgs 
 // slot range from its first block to its last valid slot, cut into chunks of
 // 256 rows; seg[t] = {first tile of the segment, tiles in the segment}.
 // Shared experts j: ceil(T/256) tiles over slots [NB + j*T, NB + (j+1)*T).
+// num_tiles[0] = the tile count, num_tiles[1..9] = the XCD ranges.
 // One workgroup; per-block last-valid lengths go through global scratch.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void build_block_tiles_kernel(
@@ -660,6 +662,7 @@ __global__ __launch_bounds__(1024) void build_block_tiles_kernel(
     int n_shared, int* __restrict__ vlen, int* __restrict__ cnt, int4* __restrict__ tiles,
     int2* __restrict__ seg, int max_tiles, int32_t* __restrict__ num_tiles) {
   __shared__ int s_part[1024];
+  __shared__ int s_wave[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int b = wave; b < N; b += 16) {
     const int32_t* blk = tpid + (long)b * B;
@@ -733,13 +736,16 @@ __global__ __launch_bounds__(1024) void build_block_tiles_kernel(
     }
   }
   if (tid == 0) num_tiles[0] = min(base + n_shared * per, max_tiles);
+  __syncthreads();
+  __threadfence_block();  // the tile stores above are this workgroup's
+  block_tile_cuts(tiles, min(base + n_shared * per, max_tiles), max_tiles, num_tiles, s_wave);
 }
 
 template <int KIND>
 static void launch_block(const BlkArgs& a, int max_tiles, hipStream_t st) {
+  // each XCD's range holds at most block_tiles_cap(max_tiles) tiles
   const int NT = (KIND == 0) ? a.I / 128 : a.H / kBN;
-  long items = (long)max_tiles * NT;
-  items = (items + 7) / 8 * 8;
+  const long items = 8L * block_tiles_cap(max_tiles) * NT;
   hipLaunchKernelGGL(expert_gemm_block_kernel<KIND>, dim3((unsigned)items), dim3(kBlkThreads), 0, st, a);
 }
 

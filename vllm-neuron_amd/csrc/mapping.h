@@ -100,6 +100,64 @@ static __device__ __forceinline__ int block_inclusive_sum(int v, int* s_wave) {
   return v + add;
 }
 
+// Cut points of a block-tile list over the 8 XCDs: hdr[1 + x], x = 0..8, is the first
+// tile of XCD x's range and hdr[9] = n. The ranges hold whole experts (the sibling
+// tiles of an expert share its weight tiles in one XCD's L2) and about equal cost,
+// a tile costing 3 + ceil(rows / 64): the fixed work of its K steps plus one unit
+// per 64-row MFMA group, the split of the block kernels' time by tile height. A
+// split into equal item counts left the XCD with the tallest tiles up to 10 %
+// behind the others. Every range holds at most block_tiles_cap(max_tiles) tiles, the
+// share of the launch grid each XCD gets (cuts are clamped to that, off expert
+// boundaries if need be), so every item has a workgroup. Whole workgroup of 1024
+// threads, after the tile list's stores (this workgroup's) are complete.
+static __host__ __device__ inline int block_tiles_cap(int max_tiles) {
+  return max(3 * max_tiles / 16, (max_tiles + 7) / 8);
+}
+static __device__ void block_tile_cuts(const int4* __restrict__ tiles, int n, int max_tiles,
+                                       int32_t* __restrict__ hdr, int* s_wave) {
+  __shared__ unsigned long long s_best[8];
+  __shared__ long s_tot;
+  const int tid = threadIdx.x;
+  auto cost = [&](int t) { return 3 + (tiles[t].z + 63) / 64; };
+  if (tid < 8) s_best[tid] = ~0ull;
+  int part = 0;
+  for (int t = tid; t < n; t += blockDim.x) part += cost(t);
+  const int inc = block_inclusive_sum(part, s_wave);
+  if (tid == (int)blockDim.x - 1) s_tot = inc;
+  __syncthreads();
+  const long C = s_tot;
+  long base = 0;
+  for (int t0 = 0; t0 < n; t0 += blockDim.x) {
+    const int t = t0 + tid;
+    const int c = t < n ? cost(t) : 0;
+    const int ci = block_inclusive_sum(c, s_wave);
+    const long excl = base + ci - c;
+    if (t < n && (t == 0 || tiles[t].x != tiles[t - 1].x)) {
+      for (int x = 1; x < 8; ++x) {
+        const long d = 8 * excl - (long)x * C;
+        atomicMin(&s_best[x], ((unsigned long long)(d < 0 ? -d : d) << 20) | (unsigned)t);
+      }
+    }
+    if (tid == (int)blockDim.x - 1) s_tot = ci;  // the chunk's total
+    __syncthreads();
+    base += s_tot;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const int cap = block_tiles_cap(max_tiles);  // 8 cap >= max_tiles >= n
+    int prev = 0;
+    hdr[1] = 0;
+    for (int x = 1; x < 8; ++x) {
+      int v = s_best[x] == ~0ull ? n : (int)(s_best[x] & 0xFFFFF);
+      // monotone, at most cap tiles in this range and at most cap in each later one
+      v = min(max(v, max(prev, n - (8 - x) * cap)), min(prev + cap, n));
+      hdr[1 + x] = v;
+      prev = v;
+    }
+    hdr[9] = n;
+  }
+}
+
 // Everything after the per-expert counts: block offsets (exclusive scan of
 // ceil(count/B)), expert_counts, block_to_expert, conditions and the optional tile
 // list. Thread tid < E holds run = count of expert tid. Leaves the inclusive
@@ -194,6 +252,12 @@ static __device__ void finish_mapping(int T, int E, int B, int N, int run, int32
     }
   }
   if (tid == 0) to.num_tiles[0] = min(ntiles + to.n_shared * per, to.max_tiles);
+  if (to.span) {  // block tiles: the XCD ranges (the tile stores above are this workgroup's)
+    __syncthreads();
+    __threadfence_block();
+    block_tile_cuts(to.tiles, min(ntiles + to.n_shared * per, to.max_tiles), to.max_tiles,
+                    to.num_tiles, s_wave);
+  }
 }
 
 // The whole mapping in one workgroup of 1024 threads, for ids and at most one

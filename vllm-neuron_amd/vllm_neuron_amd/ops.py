@@ -15,6 +15,7 @@ from ._lib import ptr
 ORDER_TOPK_ACT, ORDER_ACT_TOPK, ORDER_GROUPED = 0, 1, 2
 SCORING = {"softmax": 0, "sigmoid": 1}
 FP8 = torch.float8_e4m3fn
+BLOCK_TILES_HEADER = 16  # int32 header of a block-tile list (MOE_BLOCK_TILES_HEADER)
 
 
 def _stream():
@@ -293,7 +294,8 @@ def build_block_tiles(tpid, b2e, B, T, K, E, n_shared):
     lib = _lib.load()
     max_tiles = lib.moe_max_block_tiles(T, K, E, N, B, n_shared)
     tiles = torch.empty(max_tiles * 6, device=tpid.device, dtype=torch.int32)
-    num = torch.empty(1, device=tpid.device, dtype=torch.int32)
+    # the list's header: the tile count, then the XCD ranges the block kernels read
+    num = torch.empty(BLOCK_TILES_HEADER, device=tpid.device, dtype=torch.int32)
     wsb = lib.moe_block_tiles_workspace_bytes(N, max_tiles)
     ws = torch.empty(wsb, device=tpid.device, dtype=torch.uint8)
     _lib.call("moe_build_block_tiles", ptr(tpid), ptr(b2e), N, B, T, E, n_shared, ptr(tiles),
