@@ -245,7 +245,7 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
 
     auto issue = [&](Stage& S, int kb) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) load_lds16(wb + boff[i] + (size_t)kb * MOE_GROUP, &S.b[wave][i * 1024]);
+      for (int i = 0; i < 8; ++i) load_lds16_nt(wb + boff[i] + (size_t)kb * MOE_GROUP, &S.b[wave][i * 1024]);
 #pragma unroll
       for (int a = 0; a < NA; ++a) load_lds16(aptr[a] + (size_t)kb * MOE_GROUP, &S.a[aslot[a]][0]);
       load_lds4(asp + kb, (uint8_t*)&S.as[sslot][0]);

@@ -331,7 +331,14 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_mx_kernel(MxArgs p) {
   auto issue = [&](const MxSrc<NA>& s, Stage& S, int t) {
     const size_t kb0 = (size_t)t * KPS;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) load_lds16(s.wb + s.boff[i] + (size_t)t * 128, &S.b[wave][i * 1024]);
+    for (int i = 0; i < 8; ++i) {
+      // decode tiles (<= 32 rows: one tile per expert) stream each weight once: the
+      // non-temporal hint (GPT-OSS-120B 64 tokens -7 %); taller tiles re-read them
+      if constexpr (MT <= 32)
+        load_lds16_nt(s.wb + s.boff[i] + (size_t)t * 128, &S.b[wave][i * 1024]);
+      else
+        load_lds16(s.wb + s.boff[i] + (size_t)t * 128, &S.b[wave][i * 1024]);
+    }
     if constexpr (!TBL) {
 #pragma unroll
       for (int kk = 0; kk < KPS; ++kk)
@@ -352,7 +359,10 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_mx_kernel(MxArgs p) {
     for (int i = 0; i < 8; ++i) {
       const int c = 64 * i + lane, row = c >> 3, pc = (c & 7) ^ (row & 7);
       const int off = (16 * pc < KS) ? 16 * pc : 0;
-      load_lds16(s.wsb + (size_t)wrow_of(d, row >> 4, row & 15) * KS + off, sTbl + wave * 8192 + i * 1024);
+      if constexpr (MT <= 32)
+        load_lds16_nt(s.wsb + (size_t)wrow_of(d, row >> 4, row & 15) * KS + off, sTbl + wave * 8192 + i * 1024);
+      else
+        load_lds16(s.wsb + (size_t)wrow_of(d, row >> 4, row & 15) * KS + off, sTbl + wave * 8192 + i * 1024);
     }
   };
   // bias of the lane's four weight rows (column tile j, row r16), loaded with

@@ -128,6 +128,15 @@ __device__ __forceinline__ void load_lds16(const void* g, uint8_t* lds_wave_base
   __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
 }
 
+// The same with the non-temporal hint (nt): for data read once per call, such as
+// expert weights streamed at decode. It keeps the stream from displacing reused
+// lines (activation rows, scales) in L2 and the MALL, and raised the decode GEMMs'
+// weight stream from 6.2 to 6.7 TB/s (a plain read probe: 6.1-6.4 TB/s without the
+// hint, 6.6 with it).
+__device__ __forceinline__ void load_lds16_nt(const void* g, uint8_t* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 16, 0, 2);
+}
+
 __device__ __forceinline__ void load_lds4(const void* g, uint8_t* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 4, 0, 0);
 }
