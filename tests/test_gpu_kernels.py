@@ -179,6 +179,45 @@ def test_router_grouped_nonfinite_group_scores(cuda, gs):
         assert np.array_equal(w.cpu().numpy(), ow), tg
 
 
+NAN_ZERO_CASES = [c for c in ROUTER_CASES if c[4] == 1 and (c[3] != 2 or c[5] == 1)]
+
+
+@pytest.mark.parametrize("case", NAN_ZERO_CASES, ids=[c[0] for c in NAN_ZERO_CASES])
+@pytest.mark.parametrize("T", [1, 64])
+def test_router_topk_nan_and_signed_zero_keys(cuda, case, T):
+    """NaN keys are never selected and -0 ties +0 (then the lower index wins), as in
+    the oracle's stable descending sort; rows of mostly tied keys exercise the
+    index order. Sigmoid scoring, so a NaN logit leaves the other keys finite."""
+    name, E, K, order, scoring, ng, tg, renorm, eps, scale, use_bias = case
+    say("router_topk_nan_zero", name, T)
+    rng = np.random.default_rng(E + 7 * T)
+    lg = rng.normal(0, 1.5, (T, E)).astype(np.float32)
+    for t in range(T):
+        kind = t % 4 if T > 1 else 0
+        if kind == 0:   # NaN keys among finite ones, fewer than E - K of them
+            lg[t, rng.choice(E, max(1, (E - K) // 3), replace=False)] = np.nan
+            lg[t, rng.choice(E, E // 4, replace=False)] = rng.choice(np.float32([0.0, -0.0]), E // 4)
+        elif kind == 1:  # only signed zeros and a few +-1: ties everywhere
+            lg[t] = rng.choice(np.float32([0.0, -0.0, 0.0, -0.0, 1.0, -1.0]), E)
+        elif kind == 2:  # all keys -0 or +0
+            lg[t] = rng.choice(np.float32([0.0, -0.0]), E)
+    bias = rng.normal(0, 0.01, E).astype(np.float32) if use_bias else None
+    ids, w, aff = ops.router_topk(torch.from_numpy(lg).to(cuda), K, order, scoring, ng, tg,
+                                  None if bias is None else torch.from_numpy(bias).to(cuda),
+                                  renorm, eps, scale, dense=True)
+    with np.errstate(invalid="ignore"):
+        if order == 0:
+            oi, ow = R.route_topk_act(lg, K, R.SIGMOID, renorm, eps, scale)
+        elif order == 1:
+            oi, ow = R.route_act_topk_renorm(lg, K, R.SIGMOID, renorm, eps, scale)
+        else:
+            oi, ow = R.route_grouped(lg, bias, K, ng, tg, R.SIGMOID, renorm, eps, scale)
+    assert not np.isnan(lg[np.arange(T)[:, None], oi]).any()
+    assert np.array_equal(ids.cpu().numpy(), oi)
+    assert np.array_equal(w.cpu().numpy(), ow)
+    assert np.array_equal(aff.cpu().numpy(), R.scatter_dense(oi, ow, E))
+
+
 MAP_CASES = [(1, 8, 256, 256), (7, 2, 8, 4), (64, 2, 8, 256), (64, 8, 256, 256), (300, 8, 160, 16),
              (4096, 8, 160, 256), (8192, 8, 256, 256), (1000, 6, 384, 64), (513, 1, 5, 1),
              (256, 16, 64, 32), (200, 12, 96, 8)]  # one chunk, more than 2 ids per thread

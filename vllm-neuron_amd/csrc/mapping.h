@@ -94,8 +94,14 @@ static __device__ __forceinline__ int block_inclusive_sum(int v, int* s_wave) {
   v = dpp_add_in<0x143, 0xC>(v);
   if (lane == 63) s_wave[wave] = v;
   __syncthreads();
+  // the totals of the waves before this one: all 16 entries read together, one
+  // wait (s_wave holds 16; entries of absent waves are read and masked off)
   int add = 0;
-  for (int q = 0; q < wave; ++q) add += s_wave[q];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int w = s_wave[q];
+    add += (q < wave) ? w : 0;
+  }
   __syncthreads();
   return v + add;
 }
@@ -163,18 +169,39 @@ static __device__ void block_tile_cuts(const int4* __restrict__ tiles, int n, in
 // list. Thread tid < E holds run = count of expert tid. Leaves the inclusive
 // block scan in s_blk, the counts in s_cnt and, for compact rows, the exclusive
 // count scan in s_cex (and count_off); 1024 threads.
+// SMALL (at most 256 tokens, so at most 256 blocks and tiles per expert): each
+// expert's thread writes its own blocks and tiles, with no binary search over the
+// scans; with fewer than 2^16 ids (ids_bound = T * K, which bounds both totals)
+// the block and tile counts are scanned together, 16 bits each.
+template <bool SMALL = false>
 static __device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __restrict__ expert_counts,
                                int32_t* __restrict__ block_to_expert, int32_t* __restrict__ conditions,
                                int32_t* __restrict__ block_off, int32_t* __restrict__ count_off,
                                const TileOut& to, int* s_blk, int* s_cnt, int* s_cex, int* s_tile,
-                               int* s_wave) {
+                               int* s_wave, long ids_bound = 1L << 30) {
   const int tid = threadIdx.x;
-  int blk = 0;
+  const bool pack = SMALL && ids_bound < 65536;  // workgroup-uniform
+  const int mt = to.mt, tpb = (to.tiles != nullptr) ? (B + mt - 1) / mt : 0;
+  // tiles of expert tid: per block ceil(rows/mt) tiles (row tiles), or ceil(c_e/mt)
+  // tiles running across the expert's blocks (block tiles, span = 1)
+  auto tiles_of = [&](int c) {
+    return to.span ? (c + mt - 1) / mt : (c / B) * tpb + (c % B + mt - 1) / mt;
+  };
+  int blk = 0, ntl = 0;
   if (tid < E) {
     if (expert_counts != nullptr) expert_counts[tid] = run;
     blk = (run + B - 1) / B;
+    if (SMALL && to.tiles != nullptr) ntl = tiles_of(run);
   }
-  const int cum = block_inclusive_sum(blk, s_wave);
+  int cum, tcum_small = 0;
+  if (pack) {
+    const int both = block_inclusive_sum(blk | (ntl << 16), s_wave);
+    cum = both & 0xffff;
+    tcum_small = both >> 16;
+  } else {
+    cum = block_inclusive_sum(blk, s_wave);
+  }
+  int cex = 0;
   if (tid < E) {
     if (block_off != nullptr) block_off[tid] = cum - blk;  // exclusive
     s_blk[tid] = cum;                                      // inclusive cumulative blocks
@@ -182,62 +209,85 @@ static __device__ void finish_mapping(int T, int E, int B, int N, int run, int32
   }
   if (to.compact) {  // workgroup-uniform
     const int ccum = block_inclusive_sum(run, s_wave);
+    cex = ccum - run;
     if (tid < E) {
-      s_cex[tid] = ccum - run;
-      if (count_off != nullptr) count_off[tid] = ccum - run;
+      s_cex[tid] = cex;
+      if (count_off != nullptr) count_off[tid] = cex;
     }
   }
   __syncthreads();
   const int total = s_blk[E - 1];
-  // block_to_expert[b] = #{ e < E-1 : cum[e] <= b }   (cum non-decreasing)
-  for (int b = tid; b < N; b += blockDim.x) {
-    int lo = 0, hi = E - 1;  // search in cum[0 .. E-2]
-    while (lo < hi) {
-      int mid = (lo + hi) >> 1;
-      if (s_blk[mid] <= b) lo = mid + 1;
-      else hi = mid;
+  // block_to_expert[b] = #{ e < E-1 : cum[e] <= b }   (cum non-decreasing): the
+  // expert whose blocks [cum[e] - blk_e, cum[e]) hold b, and E - 1 from total on
+  if (SMALL) {
+    if (tid < E) {
+      for (int b = cum - blk; b < cum && b < N; ++b) {
+        block_to_expert[b] = tid;
+        if (conditions != nullptr) conditions[b] = 1;
+      }
     }
-    block_to_expert[b] = lo;
-    if (conditions != nullptr) conditions[b] = (b < total) ? 1 : 0;
+    for (int b = total + tid; b < N; b += blockDim.x) {
+      block_to_expert[b] = E - 1;
+      if (conditions != nullptr) conditions[b] = 0;
+    }
+  } else {
+    for (int b = tid; b < N; b += blockDim.x) {
+      int lo = 0, hi = E - 1;  // search in cum[0 .. E-2]
+      while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (s_blk[mid] <= b) lo = mid + 1;
+        else hi = mid;
+      }
+      block_to_expert[b] = lo;
+      if (conditions != nullptr) conditions[b] = (b < total) ? 1 : 0;
+    }
   }
   if (to.tiles == nullptr) return;  // workgroup-uniform
   // Tile list from the counts. Expert e owns slots [off_e*B, off_e*B + c_e),
   // so its tiles follow without reading token_position_to_id: per block
   // ceil(rows/mt) tiles (row tiles), or ceil(c_e/mt) tiles running across the
   // expert's blocks (block tiles, span = 1).
-  const int mt = to.mt, tpb = (B + mt - 1) / mt;
-  int nt = 0;
-  if (tid < E)
-    nt = to.span ? (run + mt - 1) / mt : (run / B) * tpb + (run % B + mt - 1) / mt;
-  const int tcum = block_inclusive_sum(nt, s_wave);
+  int nt = ntl;
+  if (!SMALL && tid < E) nt = tiles_of(run);
+  const int tcum = pack ? tcum_small : block_inclusive_sum(nt, s_wave);
   if (tid < E) s_tile[tid] = tcum;
   __syncthreads();
   const int ntiles = s_tile[E - 1];
-  for (int i = tid; i < ntiles && i < to.max_tiles; i += blockDim.x) {
+  // Tile i of expert e (local index loc): row tiles per block, or block tiles
+  // sharing the expert's rows equally.
+  auto put_tile = [&](int i, int e, int first, int loc, int c, int cum_e, int tcum_e, int cex_e) {
+    const long base = (long)(cum_e - (c + B - 1) / B) * B;
+    if (to.span) {
+      // the expert's ceil(c / mt) tiles share its rows equally, so sibling tiles
+      // advance through K at the same rate and share each weight block in L2
+      const int ntl_e = tcum_e - first, h = (c + ntl_e - 1) / ntl_e;
+      const long in_e = (long)loc * h;  // first slot of the tile, relative to the expert
+      const long row = to.compact ? cex_e + in_e : base + in_e;
+      to.tiles[i] = make_int4(e, (int)(base + in_e), min(h, c - loc * h), (int)row);
+      to.seg[i] = make_int2(first, ntl_e);
+    } else {
+      const int j = loc / tpb, m = loc - j * tpb;
+      const int rows = min(B, c - j * B);
+      const long in_e = (long)j * B + m * mt;
+      const long row = to.compact ? cex_e + in_e : base + in_e;
+      to.tiles[i] = make_int4(e, (int)(base + in_e), min(mt, rows - m * mt), (int)row);
+    }
+  };
+  if (SMALL) {
+    if (tid < E) {
+      const int first = tcum - nt;
+      for (int i = first; i < tcum && i < to.max_tiles; ++i) put_tile(i, tid, first, i - first, run, cum, tcum, cex);
+    }
+  }
+  for (int i = tid; !SMALL && i < ntiles && i < to.max_tiles; i += blockDim.x) {
     int lo = 0, hi = E - 1;  // first e with s_tile[e] > i
     while (lo < hi) {
       int mid = (lo + hi) >> 1;
       if (s_tile[mid] <= i) lo = mid + 1;
       else hi = mid;
     }
-    const int e = lo, first = (e > 0) ? s_tile[e - 1] : 0, loc = i - first;
-    const int c = s_cnt[e];
-    const long base = (long)(s_blk[e] - (c + B - 1) / B) * B;
-    if (to.span) {
-      // the expert's ceil(c / mt) tiles share its rows equally, so sibling tiles
-      // advance through K at the same rate and share each weight block in L2
-      const int ntl = s_tile[e] - first, h = (c + ntl - 1) / ntl;
-      const long in_e = (long)loc * h;  // first slot of the tile, relative to the expert
-      const long row = to.compact ? s_cex[e] + in_e : base + in_e;
-      to.tiles[i] = make_int4(e, (int)(base + in_e), min(h, c - loc * h), (int)row);
-      to.seg[i] = make_int2(first, ntl);
-    } else {
-      const int j = loc / tpb, m = loc - j * tpb;
-      const int rows = min(B, c - j * B);
-      const long in_e = (long)j * B + m * mt;
-      const long row = to.compact ? s_cex[e] + in_e : base + in_e;
-      to.tiles[i] = make_int4(e, (int)(base + in_e), min(mt, rows - m * mt), (int)row);
-    }
+    const int e = lo, first = (e > 0) ? s_tile[e - 1] : 0;
+    put_tile(i, e, first, i - first, s_cnt[e], s_blk[e], s_tile[e], to.compact ? s_cex[e] : 0);
   }
   const int per = (T + mt - 1) / mt;
   const int hsh = to.span ? (T + per - 1) / per : mt;  // equal block-tile heights
@@ -327,8 +377,8 @@ static __device__ void map_small_body(const int32_t* __restrict__ ids, const int
 #pragma unroll
     for (int w = 0; w < 8; ++w) run += __popc(bm[tid][w]);
   }
-  finish_mapping(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off,
-                 nullptr, to, s_blk, s_cnt, s_cex, s_tile, s_wave);
+  finish_mapping<true>(T, E, B, N, run, expert_counts, block_to_expert, conditions, ws.block_off,
+                       nullptr, to, s_blk, s_cnt, s_cex, s_tile, s_wave, (long)T * K);
   auto scatter = [&](int i, int e) {
     const int t = i / K;
     int out = -1;

@@ -89,10 +89,13 @@ __device__ __forceinline__ float div_by(float x, float d, float rd) {
 // Deterministic fp32 exp / sigmoid built from individually rounded IEEE ops
 // (no contraction), so the host oracle reproduces them bit for bit:
 // Cody-Waite reduction with C1 = 355/512 (exact), degree-7 Taylor (Horner),
-// scale by 2^n. Argument clamped to [-80, 80] (no subnormal intermediates).
+// scale by 2^n. Argument clamped to [-80, 80] (no subnormal intermediates); a NaN
+// argument returns NaN, as the oracle's clip does (fmaxf would turn it into -80,
+// and a NaN logit into a sigmoid key of 1).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float det_exp_f32(float x) {
 #pragma clang fp contract(off)
+  if (x != x) return x;
   x = fminf(fmaxf(x, -80.0f), 80.0f);
   float n = __builtin_rintf(x * 0x1.715476p+0f);          // log2(e)
   float r = (x - n * 0x1.63p-1f) - n * -0x1.bd0106p-13f;  // ln2 = C1 + C2, C1 = 355/512

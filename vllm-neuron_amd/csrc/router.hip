@@ -402,6 +402,63 @@ __device__ __forceinline__ KeyIdx wave_argmax(float v, int i) {
           __builtin_amdgcn_readlane(i, 63)};
 }
 
+// Selection candidates as one unsigned 64-bit value each: the key's bits mapped
+// to an order-preserving u32 (negative keys inverted, the sign bit set on the
+// rest; -0 is taken as +0, which better() treats as equal) above the inverted
+// expert index, so a larger value is exactly better() (larger key, then lower
+// index) and one u64 compare replaces it. 0 is "no candidate": NaN keys, masked
+// experts and lanes past E.
+__device__ __forceinline__ uint64_t pack_key(float v, int e) {
+  uint32_t u = (uint32_t)__float_as_int(v == 0.f ? 0.f : v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)e;
+}
+__device__ __forceinline__ float unpack_key(uint64_t p) {
+  const uint32_t o = (uint32_t)(p >> 32);
+  return __int_as_float((int)((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o));
+}
+
+// Per-lane bitonic sort of N (a power of two) packed candidates, descending.
+template <int N>
+__device__ __forceinline__ void sort_desc_u64(uint64_t (&a)[N]) {
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int l = i ^ j;
+        if (l > i) {
+          const uint64_t x = a[i], y = a[l];
+          const bool sw = ((i & k) == 0) ? (x < y) : (x > y);
+          a[i] = sw ? y : x;
+          a[l] = sw ? x : y;
+        }
+      }
+}
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ void max_step_u64(uint64_t& v) {
+  const uint32_t lo = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)(uint32_t)(v >> 32));
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  v = o > v ? o : v;
+}
+
+// Wave maximum of packed candidates (the same reduction tree as wave_argmax),
+// read from lane 63 as a scalar.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  max_step_u64<0xB1, 0xF>(v);
+  max_step_u64<0x4E, 0xF>(v);
+  max_step_u64<0x141, 0xF>(v);
+  max_step_u64<0x140, 0xF>(v);
+  max_step_u64<0x142, 0xA>(v);
+  max_step_u64<0x143, 0xC>(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 // Value of lane k (k wave-uniform): a scalar read, no LDS round trip.
 __device__ __forceinline__ float lane_f32(float v, int k) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), k));
@@ -657,30 +714,28 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
       }
     }
 
-    // K rounds of wave argmax; lane k keeps the k-th winner.
+    // K rounds; lane k keeps the k-th winner. Each lane sorts its own packed
+    // candidates once, so a round is the wave maximum of the lane heads (one u64
+    // compare per step), after which the winning lane (the one whose head it is:
+    // indices are distinct) drops its head. A NaN key is never a candidate; with
+    // no candidate left the round's maximum is 0 and its id is -1.
+    uint64_t pk[PM];
+#pragma unroll
+    for (int j = 0; j < PM; ++j)
+      pk[j] = (valid[j] && key[j] == key[j]) ? pack_key(key[j], lane + 64 * j) : 0ull;
+    sort_desc_u64<PM>(pk);
     int my_id = -1;
     float my_key = 0.f;
-    int taken[PM];
-#pragma unroll
-    for (int j = 0; j < PM; ++j) taken[j] = -1;
     for (int k = 0; k < K; ++k) {
-      float bv = NEG_INF;
-      int bi = 0x7fffffff;
+      const uint64_t best = wave_max_u64(pk[0]);
+      if (pk[0] == best) {  // the winner; lanes with nothing left shift zeros
 #pragma unroll
-      for (int j = 0; j < PM; ++j) {
-        int e = lane + 64 * j;
-        if (valid[j] && taken[j] < 0 && better(key[j], e, bv, bi)) {
-          bv = key[j];
-          bi = e;
-        }
+        for (int j = 0; j + 1 < PM; ++j) pk[j] = pk[j + 1];
+        pk[PM - 1] = 0ull;
       }
-      KeyIdx b = wave_argmax(bv, bi);
-#pragma unroll
-      for (int j = 0; j < PM; ++j)
-        if (lane + 64 * j == b.i) taken[j] = k;
       if (lane == k) {
-        my_id = (b.i < E) ? b.i : -1;  // no valid candidate left (NaN keys): id -1
-        my_key = b.v;
+        my_id = best != 0ull ? (int)~(uint32_t)best : -1;
+        my_key = best != 0ull ? unpack_key(best) : NEG_INF;
       }
     }
 
@@ -713,6 +768,16 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
       if (lds_ids) s_ids[t * K + lane] = my_id;
     }
     if (aff != nullptr) {
+      // round of each expert's selection (-1: not selected), from the winners
+      int taken[PM];
+#pragma unroll
+      for (int j = 0; j < PM; ++j) taken[j] = -1;
+      for (int k = 0; k < K; ++k) {
+        const int id = __builtin_amdgcn_readlane(my_id, k);
+#pragma unroll
+        for (int j = 0; j < PM; ++j)
+          if (id >= 0 && lane + 64 * j == id) taken[j] = k;
+      }
 #pragma unroll
       for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
