@@ -171,8 +171,9 @@ static __device__ void block_tile_cuts(const int4* __restrict__ tiles, int n, in
 // count scan in s_cex (and count_off); 1024 threads.
 // SMALL (at most 256 tokens, so at most 256 blocks and tiles per expert): each
 // expert's thread writes its own blocks and tiles, with no binary search over the
-// scans; with fewer than 2^16 ids (ids_bound = T * K, which bounds both totals)
-// the block and tile counts are scanned together, 16 bits each.
+// scans; with fewer than 2^16 ids (ids_bound = T * K, which bounds every total)
+// the block and tile counts are scanned together, 16 bits each, and with fewer
+// than 2^10 the expert counts join them (compact rows), 10 bits each.
 template <bool SMALL = false>
 static __device__ void finish_mapping(int T, int E, int B, int N, int run, int32_t* __restrict__ expert_counts,
                                int32_t* __restrict__ block_to_expert, int32_t* __restrict__ conditions,
@@ -193,8 +194,14 @@ static __device__ void finish_mapping(int T, int E, int B, int N, int run, int32
     blk = (run + B - 1) / B;
     if (SMALL && to.tiles != nullptr) ntl = tiles_of(run);
   }
-  int cum, tcum_small = 0;
-  if (pack) {
+  int cum, tcum_small = 0, ccum_small = 0;
+  const bool pack3 = pack && to.compact && ids_bound < 1024;  // workgroup-uniform
+  if (pack3) {
+    const int all = block_inclusive_sum(blk | (ntl << 10) | (run << 20), s_wave);
+    cum = all & 0x3ff;
+    tcum_small = (all >> 10) & 0x3ff;
+    ccum_small = all >> 20;
+  } else if (pack) {
     const int both = block_inclusive_sum(blk | (ntl << 16), s_wave);
     cum = both & 0xffff;
     tcum_small = both >> 16;
@@ -208,7 +215,7 @@ static __device__ void finish_mapping(int T, int E, int B, int N, int run, int32
     s_cnt[tid] = run;
   }
   if (to.compact) {  // workgroup-uniform
-    const int ccum = block_inclusive_sum(run, s_wave);
+    const int ccum = pack3 ? ccum_small : block_inclusive_sum(run, s_wave);
     cex = ccum - run;
     if (tid < E) {
       s_cex[tid] = cex;

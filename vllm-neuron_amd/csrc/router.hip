@@ -499,6 +499,11 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
   const int P = (E + 63) / 64;
   const float NEG_INF = -__builtin_inff();
   const bool need_act = order != MOE_ORDER_TOPK_ACT;
+  // With split-K partials the whole workgroup visits every (token, expert) pair
+  // to sum them, and a sigmoid activation (selection keys and weights read only
+  // the activation, never the raw logit again) is applied right there rather
+  // than by the token's single wave.
+  const bool pre_act = part != nullptr && need_act && scoring == MOE_SCORING_SIGMOID;
 
   // The correction bias is loaded first so its latency overlaps the logits' loads.
   float cb[PM];
@@ -523,7 +528,7 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
       const int tl = q / E, e = q - tl * E;
       const float lgv = (lbias != nullptr) ? sum + lbias[e] : sum;
       if (logits_out != nullptr) logits_out[(size_t)(t0 + tl) * E + e] = lgv;
-      s_act[tl][e] = lgv;
+      s_act[tl][e] = pre_act ? det_sigmoid_f32(lgv) : lgv;
     };
     // Up to 16 splits: Q >= ksplit loads per pair and 32 / Q pairs per thread at a
     // time (32 loads in flight). Pairs past the end reload the last pair.
@@ -586,15 +591,18 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
         int e = lane + 64 * j;
         lg[j] = (j < P && e < E) ? row[e] : NEG_INF;
       }
-    } else {
+    } else if (!pre_act) {
 #pragma unroll
       for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
         lg[j] = (j < P && e < E) ? s_act[wave][e] : NEG_INF;
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < PM; ++j) lg[j] = NEG_INF;  // not read: s_act holds the activations
     }
 
-    if (need_act) {
+    if (need_act && !pre_act) {
       if (scoring == MOE_SCORING_SIGMOID) {
 #pragma unroll
         for (int j = 0; j < PM; ++j) {
