@@ -220,7 +220,8 @@ def test_router_topk_nan_and_signed_zero_keys(cuda, case, T):
 
 MAP_CASES = [(1, 8, 256, 256), (7, 2, 8, 4), (64, 2, 8, 256), (64, 8, 256, 256), (300, 8, 160, 16),
              (4096, 8, 160, 256), (8192, 8, 256, 256), (1000, 6, 384, 64), (513, 1, 5, 1),
-             (256, 16, 64, 32), (200, 12, 96, 8)]  # one chunk, more than 2 ids per thread
+             (256, 16, 64, 32), (200, 12, 96, 8),  # one chunk, more than 2 ids per thread
+             (256, 256, 512, 1), (256, 300, 300, 2)]  # one chunk with >= 2^16 ids: unpacked scans
 
 
 @pytest.mark.parametrize("T,K,E,B", MAP_CASES)
