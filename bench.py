@@ -15,7 +15,8 @@ Phases:
   C  the same layer at prefill (8192 tokens), reported under "prefill8k".
   D  the CPU oracle on a bounded token sample (rank 0, N = 1 only): median of 3
      timed runs after one warm-up.
-  E  (unless --no-extra) the other workloads, under "extra": the small layer
+  E  (unless --no-extra) the other workloads, under "extra", each the median of three
+     timed loops (its "timing" field): the small layer
      (64 tokens, hidden 1024, 8 experts, top-2), Kimi-K2 over 1..16384 tokens
      (1 token also with 32 inputs cycled so the weights do not stay in the 256 MB
      MALL), GLM-4.5 with Zipf-skewed routing, and the GPT-OSS-120B layer with
@@ -117,15 +118,20 @@ def run_phase_b(x, w, cfg, steps, torch, ops):
     return gu, dn, ids
 
 
-def time_layer(x, w, cfg, steps, warmup, torch, ops):
+def time_layer(x, w, cfg, steps, warmup, torch, ops, loops=1):
+    """Seconds per layer call: the mean over `steps` calls, or with loops > 1 the
+    median of that many timed loops (one stall then moves one loop, not the figure)."""
     for _ in range(warmup):
         ops.layer_forward(x, w, cfg)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        ops.layer_forward(x, w, cfg)
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps
+    runs = []
+    for _ in range(loops):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ops.layer_forward(x, w, cfg)
+        torch.cuda.synchronize()
+        runs.append((time.perf_counter() - t0) / steps)
+    return sorted(runs)[len(runs) // 2]
 
 
 def graph_ms(fn, reps, torch):
@@ -188,7 +194,8 @@ def workload_report(name, x, w, cfg, steps, torch, ops):
     64 tokens, the device time of the same call replayed from a HIP graph)."""
     T = x.shape[0]
     H, I, E = cfg.hidden, cfg.intermediate, cfg.n_experts
-    sec = time_layer(x, w, cfg, steps, 2, torch, ops)
+    loop = max(steps // 2, 5)
+    sec = time_layer(x, w, cfg, loop, 2, torch, ops, loops=3)
     gms = graph_ms(lambda: ops.layer_forward(x, w, cfg), max(steps, 20), torch) if T <= 64 else None
     fms = flushed_ms(lambda: ops.layer_forward(x, w, cfg), max(steps, 20), torch) if T <= 64 else None
     ids = ops.layer_forward(x, w, cfg, return_routing=True)[1]
@@ -197,6 +204,7 @@ def workload_report(name, x, w, cfg, steps, torch, ops):
     nbytes = ((active + cfg.n_shared) * (expert_bytes(H, I, "gate_up") + expert_bytes(H, I, "down"))
               + E * H * 2 + T * H * 2 * 2)
     rep = {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
+           "timing": f"median of 3 loops of {loop} calls after 2 warm-up calls",
            "tokens_per_s": round(T / sec, 1), "active_experts": active,
            "alg_bytes": nbytes, "alg_flops": flops,
            "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
@@ -263,12 +271,15 @@ def mx_report(name, layer, x, steps, torch):
     E, I, hr = w.n_experts, w.intermediate, layer.hidden_actual or H
     for _ in range(2):
         layer(x, None, True, None)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        layer(x, None, True, None)
-    torch.cuda.synchronize()
-    sec = (time.perf_counter() - t0) / steps
+    loop, runs = max(steps // 2, 5), []
+    for _ in range(3):  # median of three timed loops
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(loop):
+            layer(x, None, True, None)
+        torch.cuda.synchronize()
+        runs.append((time.perf_counter() - t0) / loop)
+    sec = sorted(runs)[1]
     gms = graph_ms(lambda: layer(x, None, True, None), max(steps, 20), torch) if T <= 64 else None
     fms = flushed_ms(lambda: layer(x, None, True, None), max(steps, 20), torch) if T <= 64 else None
     from vllm_neuron_amd import ops
@@ -281,6 +292,7 @@ def mx_report(name, layer, x, steps, torch):
     nbytes = active * per_expert + E * H * 2 + T * H * 2 * 2
     flops = 2 * rows * 3 * hr * hr + 2 * T * H * E
     rep = {"workload": name, "tokens": T, "ms_per_step": round(sec * 1e3, 4),
+           "timing": f"median of 3 loops of {loop} calls after 2 warm-up calls",
            "tokens_per_s": round(T / sec, 1), "active_experts": active,
            "alg_bytes": nbytes, "alg_flops": flops,
            "hbm_frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
