@@ -2,8 +2,9 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product package imports this
 directory: only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker (or the
-timed CPU baseline), never as the computation that is shipped or measured.
+``cpu_baseline`` leg of ``bench.py`` use it, and only as the reference the GPU
+results are compared with (or the timed CPU baseline), never as the computation
+that is shipped or measured.
 
 It restates, in numpy, the CPU fallbacks of the reference plugin
 (jinhuang12/vllm-neuron) for this path:
