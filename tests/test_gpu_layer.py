@@ -373,6 +373,25 @@ def test_layer_kimi_k2_full_size(cuda, kimi_weights, T):
         assert torch.equal(out, _op_path(cfg, kimi_weights, x))
 
 
+@pytest.mark.parametrize("T,B", [(100, 256), (128, 16), (160, 256), (256, 64), (256, 16)])
+def test_layer_fused_mapping_tile_heights(cuda, T, B):
+    """Up to 256 tokens the layer's top-k launch ends in the mapping and writes the tile
+    list from each expert's own thread. A small grouped layer (32 experts, top-8, four
+    groups with two kept, one shared expert) reaches the tile heights the full-size
+    configs do not at these token counts: 25-32 rows per expert (64-row tiles) and
+    40-64 (block tiles with their XCD cuts), with 256- and 16-slot blocks. Every token
+    against the oracle, and the op-by-op path (separate mapping and tile-list kernels)
+    bit for bit."""
+    cfg = MoEConfig(1024, 512, 32, 8, n_shared=1, scoring="sigmoid", grouped=True, n_group=4,
+                    topk_group=2, renorm=True, routed_scaling=2.5, block_size=B)
+    block = ops.use_block_kernels(T, cfg.top_k, cfg.n_experts)
+    say("layer fused mapping", T, B, "block" if block else f"mt {ops.choose_mt(T, cfg.top_k, cfg.n_experts)}")
+    w = synthetic.make_weights(cfg, 7, device=cuda, experts_device=cuda)
+    x = synthetic.hidden_states(T, cfg.hidden, 7).to(cuda)
+    out = _check_layer(cfg, w, x, tag=f"fused mapping T={T} B={B}")
+    assert torch.equal(out, _op_path(cfg, w, x))
+
+
 def test_layer_glm45_full_size_zipf(cuda):
     """GLM-4.5 layer (hidden 5120, intermediate 1536, 160 experts + 1 shared) at 4096
     tokens with Zipf(1.2) expert popularity and 10% of the experts empty: overfull
