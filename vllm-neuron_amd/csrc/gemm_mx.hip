@@ -222,7 +222,7 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_mx_kernel(MxArgs p) {
   constexpr int KPS = Stage::KPS, AQ = Stage::AQ, NSQ = Stage::NSQ;
   constexpr int NA = (KPS * AQ + NW - 1) / NW;  // activation loads per wave per stage
   constexpr int NV = 8 + (TBL ? 0 : KPS) + NA + KPS;  // direct-to-LDS loads per wave per stage
-  static_assert(PD >= 2 && PD <= 3 && (PD - 2) * NV < 64, "pipeline depth");
+  static_assert(PD >= 2 && PD <= 6 && (PD - 2) * NV < 64, "pipeline depth");
   __shared__ __attribute__((aligned(1024))) Stage st[PD];
   __shared__ __attribute__((aligned(16))) uint8_t sTbl[TBL ? NW * 64 * 128 : 16];
   __shared__ long sSrc[2][MT];
@@ -238,7 +238,9 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_mx_kernel(MxArgs p) {
   const std::integral_constant<int, WFMT> wfmt{};
   int wi = blockIdx.x;
   if (wi >= total) return;
-  const bool stream = NSTG >= PD;  // crossing step NSTG - PD + 1 >= 1 follows the token loads
+  // crossing step NSTG - PD + 1 >= 1 follows the token loads; a ring deeper than
+  // three stages (one item per workgroup) drains between items instead
+  const bool stream = PD <= 3 && NSTG >= PD;
   const size_t wrow_bytes = (size_t)Kdim * ((WFMT == kFmtFp4) ? 64 : 128) / 128;
   const int rows_w = (KIND == 0) ? 2 * p.I : p.H;
 
@@ -659,10 +661,12 @@ static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
   switch (mt) {
     case 16:
       if (half) {
+        // one item per workgroup: six stages in flight, since a half-width item at
+        // one token is a short chain of K steps rather than a byte stream
         if (tbl)
-          MOE_MX(16, 3, true, 2);
+          MOE_MX(16, 6, true, 2);
         else
-          MOE_MX(16, 3, false, 2);
+          MOE_MX(16, 6, false, 2);
       } else if (tbl) {
         MOE_MX(16, 3, true, 4);
       } else {
