@@ -345,22 +345,34 @@ def extra_workloads(steps, torch, ops, synthetic, PRESETS, dev, cpu_tokens):
         cpu.append(oracle_sample("GLM-4.5 MoE layer (Zipf)", x, w, cfg, max(1, cpu_tokens // 4)))
     del w
     torch.cuda.empty_cache()
-    from vllm_neuron_amd import MXFP4MoE
     print("[bench] extra: gpt-oss-120b mxfp4", file=sys.stderr, flush=True)
+    layer, inputs = gpt_oss_setup(torch, dev)
+    for T in (1, 64, 2048):
+        out.append(mx_report(gpt_oss_name(T), layer, inputs(T), steps, torch))
+    del layer
+    torch.cuda.empty_cache()
+    return out, cpu
+
+
+def gpt_oss_setup(torch, dev):
+    """The GPT-OSS-120B MXFP4 layer (128 experts, top-4, hidden 2880 padded to 3072, the
+    pre-MoE RMSNorm) with seeded synthetic weights, and its input rows for T tokens."""
+    from vllm_neuron_amd import MXFP4MoE, synthetic
     E, Hp, Ip, Hr = 128, 3072, 3072, 2880
     wm = synthetic.make_mx_weights(E, Hp, Ip, 5, device=dev, h_real=Hr, i_real=Hr)
     gamma = (1 + 0.1 * torch.randn(Hp, generator=torch.Generator().manual_seed(5))).to(dev)
     gamma[Hr:] = 0
     layer = MXFP4MoE(wm, 4, norm_weight=gamma, eps=1e-5, hidden_actual=Hr)
-    for T in (1, 64, 2048):
+
+    def inputs(T):
         x = torch.zeros(T, Hp)
         x[:, :Hr] = torch.randn(T, Hr, generator=torch.Generator().manual_seed(6))
-        x = x.to(torch.bfloat16).to(dev)
-        out.append(mx_report(f"GPT-OSS-120B MoE layer, MXFP4 experts (128, top-4, Swish, clamps, "
-                             f"biases), {T} tokens", layer, x, steps, torch))
-    del wm, layer
-    torch.cuda.empty_cache()
-    return out, cpu
+        return x.to(torch.bfloat16).to(dev)
+    return layer, inputs
+
+
+def gpt_oss_name(T):
+    return f"GPT-OSS-120B MoE layer, MXFP4 experts (128, top-4, Swish, clamps, biases), {T} tokens"
 
 
 def cpu_threads():
@@ -482,6 +494,8 @@ ONLY = {
     "glm45_zipf4096": ("GLM-4.5 MoE layer, 4096 tokens, Zipf(1.2) routing, 10% empty experts",
                        "glm45", 4096, 4, 4, True),
 }
+# --only GPT-OSS-120B MXFP4 workloads: tokens
+ONLY_MX = {"gpt_oss_1": 1, "gpt_oss_64": 64, "gpt_oss_2048": 2048}
 
 
 def main():
@@ -497,7 +511,7 @@ def main():
     ap.add_argument("--prologue-calls", type=int, default=0,
                     help="only run the decode prologue (fused, then as separate launches) this "
                          "many times at 64 and 8192 tokens, for a kernel trace; no timing")
-    ap.add_argument("--only", choices=sorted(ONLY),
+    ap.add_argument("--only", choices=sorted(ONLY) + sorted(ONLY_MX),
                     help="time one workload alone (whole layer, --steps calls after 2 warm-up "
                          "calls) and print its report line; for kernel traces and counter passes")
     args = ap.parse_args()
@@ -510,6 +524,12 @@ def main():
     from vllm_neuron_amd import PRESETS, ops, synthetic
 
     dev = torch.device("cuda:0")
+    if args.only in ONLY_MX:
+        T = ONLY_MX[args.only]
+        print(f"[bench] only: {gpt_oss_name(T)}", file=sys.stderr, flush=True)
+        layer, inputs = gpt_oss_setup(torch, dev)
+        print(json.dumps(mx_report(gpt_oss_name(T), layer, inputs(T), args.steps, torch)))
+        return
     if args.only:
         name, preset, T, wseed, xseed, zipf = ONLY[args.only]
         cfg = PRESETS[preset]
