@@ -588,3 +588,47 @@ def test_layer_module_norm_and_residual(cuda):
     assert torch.equal(pad[:40], out[:40]) and torch.all(pad[40:] == 0)
     with pytest.raises(ValueError):
         FP8BlockMoE(cfg, w)(x, None, False, None, residual=r)
+
+
+NORM_RIDE_SHAPES = {
+    # Kimi-K2's router (7168 columns: 3-4 chunks per thread; 384 experts: 6 x 28 logits
+    # workgroups), small experts, with the residual add
+    "kimi_router": (MoEConfig(7168, 128, 384, 8, n_shared=1, scoring="sigmoid", grouped=True,
+                              n_group=1, topk_group=1, renorm=True, routed_scaling=2.827), None, True),
+    # padded hidden size (1000 real columns of 1024), no residual
+    "padded": (MoEConfig(1024, 512, 16, 4, n_shared=1, scoring="sigmoid", grouped=True, n_group=4,
+                         topk_group=2, renorm=True, routed_scaling=2.5), 1000, False),
+    "padded_residual": (MoEConfig(1024, 512, 16, 4, n_shared=1, scoring="sigmoid", grouped=True,
+                                  n_group=4, topk_group=2, renorm=True, routed_scaling=2.5), 1000, True),
+}
+
+
+@pytest.mark.parametrize("T", [1, 3, 4, 5])
+@pytest.mark.parametrize("shape", sorted(NORM_RIDE_SHAPES))
+def test_layer_norm_rides_in_router_launch(cuda, shape, T):
+    """Up to four tokens the layer's RMSNorm (with the residual add) runs inside the
+    router logits launch: every logits and quantization workgroup reads the token rows
+    and computes their norm factors itself, and the quantization workgroups write the
+    residual stream. From five tokens the norm is a launch of its own. Either way every
+    output is the same bits as the layer without its norm, run on the rows
+    ops.rms_norm_quant normalizes (pinned against the oracle's norm in
+    test_rms_norm_quant_fused)."""
+    cfg, ha, with_res = NORM_RIDE_SHAPES[shape]
+    say("norm in the router launch", shape, T)
+    w = synthetic.make_weights(cfg, 3, device=cuda)
+    x = (2 * synthetic.hidden_states(T, cfg.hidden, 10 + T)).to(torch.bfloat16).to(cuda)
+    r = synthetic.hidden_states(T, cfg.hidden, 20 + T).to(cuda) if with_res else None
+    gamma = _gamma(cfg.hidden, 4, cuda)
+    got = ops.layer_forward(x, w, cfg, return_routing=True, gamma=gamma, eps=1e-6,
+                            hidden_actual=ha, residual=r)
+    if with_res:
+        out, rsum, *routing = got
+        assert np.array_equal(np_f32(rsum), bf16_round(np_f32(x) + np_f32(r)))
+    else:
+        out, *routing = got
+    xn = ops.rms_norm_quant(x, gamma, 1e-6, ha, r)[0]
+    ref_out, *ref_routing = ops.layer_forward(xn, w, cfg, return_routing=True)
+    assert torch.equal(out, ref_out)
+    for a, b in zip(routing, ref_routing):  # ids, weights, logits
+        assert torch.equal(a, b)
+    assert not torch.equal(out, ops.layer_forward(x, w, cfg))  # the norm is applied

@@ -256,6 +256,37 @@ def test_gpt_oss_120b_layer(cuda, gpt_oss_weights, T, tokens):
     assert np.all(got[:, c["h_real"]:] == 0)  # padded hidden columns stay zero
 
 
+@pytest.mark.parametrize("T,with_res", [(1, True), (1, False), (4, True), (5, True)])
+def test_gpt_oss_norm_rides_in_router_launch(cuda, gpt_oss_weights, T, with_res):
+    """Up to four tokens the GPT-OSS layer's RMSNorm (and residual add) runs inside the
+    router logits launch, whose MXFP8 quantization workgroups normalize the rows
+    again and write the residual stream; from five tokens the norm is a launch of its
+    own. Either way every output is the same bits as the layer without its norm, run
+    on the rows ops.rms_norm_quant normalizes."""
+    from oracle.moe import bf16_round
+    c = GPT_OSS
+    w = gpt_oss_weights
+    say("gpt-oss norm in the router launch", T, with_res)
+    x = _padded_hidden(T, 300 + T, cuda)
+    r = _padded_hidden(T, 400 + T, cuda) if with_res else None
+    gamma = torch.zeros(c["H"])
+    gamma[:c["h_real"]] = 1 + 0.1 * torch.randn(c["h_real"], generator=torch.Generator().manual_seed(9))
+    gamma = gamma.to(torch.bfloat16).float().to(cuda)
+    args = (w, c["K"], "swish", (None, LIMIT), (1 - LIMIT, 1 + LIMIT))
+    got = ops.layer_forward_mx(x, *args, return_routing=True, gamma=gamma, eps=1e-5,
+                               hidden_actual=c["h_real"], residual=r)
+    if with_res:
+        out, rsum, *routing = got
+        assert np.array_equal(np_f32(rsum), bf16_round(np_f32(x) + np_f32(r)))
+    else:
+        out, *routing = got
+    xn = ops.rms_norm_quant(x, gamma, 1e-5, c["h_real"], r)[0]
+    ref_out, *ref_routing = ops.layer_forward_mx(xn, *args, return_routing=True)
+    assert torch.equal(out, ref_out)
+    for a, b in zip(routing, ref_routing):  # ids, weights, logits
+        assert torch.equal(a, b)
+
+
 def _ids_from_dense(a):
     K = int((a != 0).sum(1).max())
     ids = np.zeros((a.shape[0], K), np.int32)

@@ -203,15 +203,6 @@ static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const voi
     moe::set_error(_moe_fn, "%s", saved);                      \
     return rc;                                                 \
   }
-  // Pre-MoE RMSNorm (with the residual add) and the 1x128 quantization of the
-  // normalized rows in one pass; the router reads the normalized bf16 rows.
-  const void* xr = x_bf16;
-  if (norm) {
-    MOE_STEP(moe_rms_norm_quant(x_bf16, residual_bf16, gamma, T, H,
-                                hidden_actual > 0 ? hidden_actual : H, eps, w.xn,
-                                residual_out_bf16, w.xq, w.xs, stream));
-    xr = w.xn;
-  }
   // The mapping also writes the expert tile list, from the counts.
   const bool block = use_block(T, K, E);
   const int mbt = block ? moe_max_block_tiles(T, K, E, N, B, n_shared) : 0;
@@ -232,20 +223,27 @@ static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const voi
   to.n_shared = n_shared;
   to.compact = 1;  // hq / y hold only the routed and shared rows
   to.row_shared = R;
-  // Decode sizes: the quantization rides in the logits launch and the mapping ends
-  // the top-k launch (router_logits_topk says which it did).
+  // Pre-MoE RMSNorm (with the residual add) and the 1x128 quantization of the
+  // normalized rows: up to a few tokens inside the logits launch, else in one pass
+  // before it (router_logits_topk). Decode sizes: the quantization rides in the
+  // logits launch and the mapping ends the top-k launch (router_logits_topk says
+  // which it did).
   RouterFuse fz = map_fuse(w, B, N, to);
-  if (!norm) {
-    fz.xq = w.xq;
-    fz.xs = w.xs;
+  fz.xq = w.xq;
+  fz.xs = w.xs;
+  if (norm) {
+    fz.norm = NormRide{(const uint16_t*)residual_bf16, gamma, (uint16_t*)residual_out_bf16,
+                       hidden_actual > 0 ? hidden_actual : H, eps};
+    fz.xn = w.xn;
   }
-  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+  MOE_STEP(router_logits_topk(x_bf16, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
                               w.router_ws_bytes, corr_bias, K, order, scoring, n_group, topk_group,
                               renorm, renorm_eps, routed_scale, ids, wts, stream, &fz));
   if (!fz.map_done)
     MOE_STEP(blockwise_mapping(ids, nullptr, nullptr, T, K, E, B, N, w.tpid, w.b2e, w.cond, w.counts,
                                w.inv, nullptr, w.map_ws, w.map_ws_bytes, to, stream));
-  if (!norm && !fz.quant_done) MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
+  // (with the norm the quantization is always done: in the logits launch or by the norm)
+  if (!fz.quant_done) MOE_STEP(moe_act_quant_1x128(x_bf16, T, H, w.xq, w.xs, stream));
   if (block) {
     MOE_STEP(moe_expert_gate_up_block(w.xq, w.xs, T, H, I, E, w13, w13_scale, nullptr, w13_shared,
                                       w13_shared_scale, nullptr, n_shared, w.tpid, (int)NB, w.btiles,
@@ -408,14 +406,6 @@ extern "C" int moe_layer_forward_mx(
     moe::set_error(_moe_fn, "%s", saved);                      \
     return rc;                                                 \
   }
-  const void* xr = x_bf16;
-  if (norm) {
-    // residual add + RMSNorm (its 1x128 codes land in xq and are replaced below)
-    MOE_STEP(moe_rms_norm_quant(x_bf16, residual_bf16, gamma, T, H,
-                                hidden_actual > 0 ? hidden_actual : H, eps, w.xn,
-                                residual_out_bf16, w.xq, w.xs, stream));
-    xr = w.xn;
-  }
   TileOut to{};
   to.tiles = (int4*)w.tiles;
   to.num_tiles = w.num_tiles;
@@ -423,13 +413,21 @@ extern "C" int moe_layer_forward_mx(
   to.mt = mt;
   to.compact = 1;
   to.row_shared = R;
+  // Residual add + RMSNorm: up to a few tokens inside the logits launch, else in a
+  // pass of its own before it (whose 1x128 codes land in xq and are replaced below).
   // Decode sizes: the MXFP8 quantization rides in the logits launch and the
   // mapping ends the top-k launch (router_logits_topk says which it did).
   RouterFuse fz = map_fuse(w, B, N, to);
   fz.xq = w.xq;
   fz.xs = xs;
   fz.quant_mx = 1;
-  MOE_STEP(router_logits_topk(xr, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
+  if (norm) {
+    fz.norm = NormRide{(const uint16_t*)residual_bf16, gamma, (uint16_t*)residual_out_bf16,
+                       hidden_actual > 0 ? hidden_actual : H, eps};
+    fz.xn = w.xn;
+  }
+  const void* xr = norm ? w.xn : x_bf16;  // what the router read, unless the norm rode
+  MOE_STEP(router_logits_topk(x_bf16, router_w_bf16, router_bias, T, H, E, logits, w.router_ws,
                               w.router_ws_bytes, nullptr, K, order, scoring, 1, 1, renorm,
                               renorm_eps, routed_scale, ids, wts, stream, &fz));
   if (!fz.map_done)

@@ -227,6 +227,52 @@ __device__ __forceinline__ void bf16x8_to_f32(const int4 c, float (&v)[8]) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// RMSNorm steps shared by every kernel that normalizes rows, so all of them give
+// the same bits. A row v (x, or bf16(x + residual)) of H values, ha of them real:
+//   rn = 1 / sqrt(sum_{c < ha} v_c^2 / ha + eps),  y_c = (v_c * rn) * gamma_c for
+//   c < ha, else 0,
+// with the sum of squares taken by a 256-thread workgroup: each thread over its
+// 8-value chunks (chunk c = thread + 256 j) in order, a butterfly over the wave,
+// then the four wave sums in order.
+// ---------------------------------------------------------------------------
+// v = bf16(v + r) for one chunk: the next residual stream, rounded to nearest even.
+__device__ __forceinline__ void norm_residual8(float (&v)[8], const int4 rc) {
+  float r[8];
+  bf16x8_to_f32(rc, r);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] + r[e]));
+}
+
+// The squares of one chunk (columns [col, col + 8)) added to ss, columns from ha on left out.
+__device__ __forceinline__ float norm_sumsq8(float ss, const float (&v)[8], int col, int ha) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (col + e < ha) ss += v[e] * v[e];
+  return ss;
+}
+
+__device__ __forceinline__ float norm_wave_sum(float ss) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  return ss;
+}
+
+// rn from the four wave sums of the row.
+__device__ __forceinline__ float norm_factor(const float* wave_sums, int ha, float eps) {
+  const float tot = ((wave_sums[0] + wave_sums[1]) + wave_sums[2]) + wave_sums[3];
+  return 1.0f / sqrtf(tot / (float)ha + eps);
+}
+
+// The normalized values of one chunk in fp32 (before the bf16 rounding); gamma of
+// the chunk in g0, g1.
+__device__ __forceinline__ void norm_apply8(const float (&v)[8], float rn, const float4 g0,
+                                            const float4 g1, int col, int ha, float (&y)[8]) {
+  const float gm[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = (col + e < ha) ? (v[e] * rn) * gm[e] : 0.f;
+}
+
 // E8M0 exponent e of an MX block with magnitude maximum amax (OCP MX v1.0 6.3):
 // floor(log2(amax)) - 8 (8 = emax of e4m3), at least -127; the scale byte is
 // e + 127 and the elements are v * 2^-e (a power of two: exact), clamped to +-448
@@ -243,10 +289,32 @@ __device__ __forceinline__ uint32_t mx_e4m3x2(float a, float b, float f) {
   return e4m3x2(fminf(fmaxf(a * f, -448.0f), 448.0f), fminf(fmaxf(b * f, -448.0f), 448.0f));
 }
 
+// MXFP8 codes of chunk c (8 consecutive values v of a 32-value block; lanes 4k ..
+// 4k + 3 hold the block's four chunks): the block amax is combined over the 4-lane
+// group, which writes 32 codes and one scale byte. Every lane calls it (live: the
+// chunk exists; whole 4-lane groups share it).
+__device__ __forceinline__ void mx_quant_chunk(const float (&v)[8], bool live, long c,
+                                               uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
+  float a = 0.f;
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
+  }
+  a = fmaxf(a, __shfl_xor(a, 1, MOE_WAVE));
+  a = fmaxf(a, __shfl_xor(a, 2, MOE_WAVE));
+  if (live) {
+    const int ex = mx_exponent(a);
+    const float f = mx_inv_scale(ex);
+    const uint32_t lo = mx_e4m3x2(v[0], v[1], f) | (mx_e4m3x2(v[2], v[3], f) << 16);
+    const uint32_t hi = mx_e4m3x2(v[4], v[5], f) | (mx_e4m3x2(v[6], v[7], f) << 16);
+    *(uint2*)(q + c * 8) = make_uint2(lo, hi);
+    if ((c & 3) == 0) s[c >> 2] = (uint8_t)(ex + 127);
+  }
+}
+
 // MXFP8 quantization of `chunks` 8-value chunks of bf16 rows (chunks % 4 == 0) by
 // workgroup `blk` of `nblk` equal workgroups: lane q of a 4-lane group holds 8
-// consecutive values of one 32-value block (one 16-byte load), the block amax is
-// combined over the group, and the group writes 32 codes and one scale byte.
+// consecutive values of one 32-value block (one 16-byte load).
 __device__ __forceinline__ void mx_act_quant_body(const uint16_t* __restrict__ x, long chunks,
                                                   uint8_t* __restrict__ q, uint8_t* __restrict__ s,
                                                   int blk, int nblk) {
@@ -254,22 +322,8 @@ __device__ __forceinline__ void mx_act_quant_body(const uint16_t* __restrict__ x
   for (long c0 = (long)blk * blockDim.x; c0 < chunks; c0 += stride) {
     const long c = c0 + threadIdx.x;  // whole 4-lane groups share the bound (chunks % 4 == 0)
     float v[8];
-    float a = 0.f;
-    if (c < chunks) {
-      bf16x8_to_f32(*(const int4*)(x + c * 8), v);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) a = fmaxf(a, fabsf(v[i]));
-    }
-    a = fmaxf(a, __shfl_xor(a, 1, MOE_WAVE));
-    a = fmaxf(a, __shfl_xor(a, 2, MOE_WAVE));
-    if (c < chunks) {
-      const int ex = mx_exponent(a);
-      const float f = mx_inv_scale(ex);
-      const uint32_t lo = mx_e4m3x2(v[0], v[1], f) | (mx_e4m3x2(v[2], v[3], f) << 16);
-      const uint32_t hi = mx_e4m3x2(v[4], v[5], f) | (mx_e4m3x2(v[6], v[7], f) << 16);
-      *(uint2*)(q + c * 8) = make_uint2(lo, hi);
-      if ((c & 3) == 0) s[c >> 2] = (uint8_t)(ex + 127);
-    }
+    if (c < chunks) bf16x8_to_f32(*(const int4*)(x + c * 8), v);
+    mx_quant_chunk(v, c < chunks, c, q, s);
   }
 }
 

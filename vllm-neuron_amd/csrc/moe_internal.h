@@ -63,16 +63,38 @@ struct TileOut {
   long row_shared;
 };
 
+// The pre-MoE RMSNorm of the layer's rows (with gamma set): v = x, or bf16(x +
+// residual) written to res_out as the next residual stream; the rows normalized
+// over their first ha columns.
+struct NormRide {
+  const uint16_t* res;
+  const float* gamma;
+  uint16_t* res_out;
+  int ha;
+  float eps;
+};
+
+// Up to this many tokens the norm rides in the router logits launch: every
+// workgroup of that launch reads the token rows and computes their norm factors
+// itself (at most 16384 columns).
+constexpr int kNormRideT = 4;
+constexpr int kNormRideMaxH = 16384;
+
 // Work that router_logits_topk may fold into its launches for the layer: the
 // quantization of x into xq / xs (when xq is set: 1x128 fp8 codes and fp32 scales,
 // or with quant_mx MXFP8 codes and E8M0 scale bytes) and blockwise_mapping of the
 // ids it selects (when tpid is set; ids only, no padding mask, inv_pos = inv,
-// workspace map_ws, tile list `to`). On return quant_done / map_done say which it
-// did; the caller runs the rest itself.
+// workspace map_ws, tile list `to`). With norm.gamma set, x is normalized first:
+// inside the logits launch where it can ride (then the quantization rides too),
+// otherwise by moe_rms_norm_quant into xn (its 1x128 codes land in xq / xs), which
+// the router then reads. On return quant_done / map_done say which it did; the
+// caller runs the rest itself (from xn when the norm was requested).
 struct RouterFuse {
   uint8_t* xq;
   void* xs;
   int quant_mx;
+  NormRide norm;
+  void* xn;
   int B, N;
   int32_t *tpid, *b2e, *cond, *counts, *inv;
   void* map_ws;

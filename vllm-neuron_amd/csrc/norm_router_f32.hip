@@ -86,33 +86,21 @@ __global__ __launch_bounds__(256) void rms_norm_vec_kernel(
       } else {
         bf16x8_to_f32(*(const int4*)((const uint16_t*)x + base + 8 * c), v[j]);
       }
-      if (RES) {
-        float r[8];
-        bf16x8_to_f32(*(const int4*)(res + base + 8 * c), r);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[j][e] = bf16_bits_to_f32(f32_to_bf16_bits(v[j][e] + r[e]));
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (8 * c + e < ha) ss += v[j][e] * v[j][e];
+      if (RES) norm_residual8(v[j], *(const int4*)(res + base + 8 * c));
+      ss = norm_sumsq8(ss, v[j], 8 * c, ha);
     }
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  ss = norm_wave_sum(ss);
   if ((tid & 63) == 0) s_part[tid >> 6] = ss;
   __syncthreads();
-  const float tot = ((s_part[0] + s_part[1]) + s_part[2]) + s_part[3];
-  const float rn = 1.0f / sqrtf(tot / (float)ha + eps);
+  const float rn = norm_factor(s_part, ha, eps);
   const int G = H / MOE_GROUP;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int c = tid + 256 * j;
     if (c >= nch) continue;  // whole 16-lane segments leave together when H % 128 == 0
-    const float gm[8] = {gv[j][0].x, gv[j][0].y, gv[j][0].z, gv[j][0].w,
-                         gv[j][1].x, gv[j][1].y, gv[j][1].z, gv[j][1].w};
     float y[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = (8 * c + e < ha) ? (v[j][e] * rn) * gm[e] : 0.f;
+    norm_apply8(v[j], rn, gv[j][0], gv[j][1], 8 * c, ha, y);
     if (RES) {
       uint32_t w[4];
 #pragma unroll

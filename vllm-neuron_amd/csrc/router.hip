@@ -17,6 +17,9 @@ namespace moe {
 // launch of its own: by the extra workgroups [qblk0, qblk0 + qnblk)
 // (act_quant_vec_body / mx_act_quant_body) in the 64 x 64 form, by the wide form
 // as it loads x (1x128 only: qq set, qnblk 0).
+// With norm.gamma set (64 x 64 form, T <= kNormRideT) x holds the raw rows: every
+// workgroup computes the rows' norm factors and normalizes what it reads, and the
+// quantization workgroups also write the residual stream.
 struct LogitsSide {
   int* zero;
   const uint16_t* qx;
@@ -24,7 +27,119 @@ struct LogitsSide {
   uint8_t* qq;
   void* qs;
   int qblk0, qnblk, qmx;
+  NormRide norm;
 };
+
+// ---------------------------------------------------------------------------
+// The RMSNorm riding in the logits launch, for up to kNormRideT token rows. Each
+// workgroup (256 threads) sums the squares of every row itself with
+// rms_norm_vec_kernel's steps (the same chunks per thread, butterfly and wave-sum
+// order), so the normalized rows are bit-identical to moe_rms_norm_quant's.
+// ---------------------------------------------------------------------------
+constexpr int kNormRideChunks = kNormRideMaxH / (8 * 256);  // 16-byte chunks per thread and row
+
+// Norm factors of rows [0, T) of x into s_rn (T <= kNormRideT), for the whole
+// workgroup (two barriers).
+__device__ __forceinline__ void norm_ride_factors(const uint16_t* __restrict__ x, const NormRide& nr,
+                                                  int T, int H, float (*s_ws)[4], float* s_rn) {
+  const int tid = threadIdx.x, nch = H >> 3;
+#pragma unroll
+  for (int t = 0; t < kNormRideT; ++t) {
+    if (t < T) {  // workgroup-uniform
+      int4 xc[kNormRideChunks], rc[kNormRideChunks];
+#pragma unroll
+      for (int j = 0; j < kNormRideChunks; ++j) {
+        const int c = tid + 256 * j;
+        if (c < nch) {
+          xc[j] = *(const int4*)(x + (size_t)t * H + 8 * c);
+          if (nr.res != nullptr) rc[j] = *(const int4*)(nr.res + (size_t)t * H + 8 * c);
+        }
+      }
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < kNormRideChunks; ++j) {
+        const int c = tid + 256 * j;
+        if (c < nch) {
+          float v[8];
+          bf16x8_to_f32(xc[j], v);
+          if (nr.res != nullptr) norm_residual8(v, rc[j]);
+          ss = norm_sumsq8(ss, v, 8 * c, nr.ha);
+        }
+      }
+      ss = norm_wave_sum(ss);
+      if ((tid & 63) == 0) s_ws[t][tid >> 6] = ss;
+    }
+  }
+  __syncthreads();
+  if (tid < T) s_rn[tid] = norm_factor(s_ws[tid], nr.ha, nr.eps);
+  __syncthreads();
+}
+
+// The normalized chunk at element offset off (column col of its row, factor rn) as
+// four bf16x2 words; v receives the chunk's row values (bf16(x + residual), or x).
+__device__ __forceinline__ int4 norm_ride_chunk(const uint16_t* __restrict__ x, const NormRide& nr,
+                                                size_t off, int col, float rn, float (&v)[8]) {
+  bf16x8_to_f32(*(const int4*)(x + off), v);
+  if (nr.res != nullptr) norm_residual8(v, *(const int4*)(nr.res + off));
+  const float4 g0 = *(const float4*)(nr.gamma + col), g1 = *(const float4*)(nr.gamma + col + 4);
+  float y[8];
+  norm_apply8(v, rn, g0, g1, col, nr.ha, y);
+  return make_int4((int)bf16x2(y[0], y[1]), (int)bf16x2(y[2], y[3]), (int)bf16x2(y[4], y[5]),
+                   (int)bf16x2(y[6], y[7]));
+}
+
+__device__ __forceinline__ void norm_ride_res_out(const NormRide& nr, size_t off, const float (&v)[8]) {
+  if (nr.res_out != nullptr)
+    *(int4*)(nr.res_out + off) = make_int4((int)bf16x2(v[0], v[1]), (int)bf16x2(v[2], v[3]),
+                                           (int)bf16x2(v[4], v[5]), (int)bf16x2(v[6], v[7]));
+}
+
+// act_quant_vec_body on the normalized rows (groups = T * H / 128, the same lane
+// mapping, one quad per wave at a time), writing the residual stream as it goes.
+__device__ __forceinline__ void act_quant_norm_body(const uint16_t* __restrict__ x, const NormRide& nr,
+                                                    const float* s_rn, int H, long groups,
+                                                    uint8_t* __restrict__ q, float* __restrict__ s,
+                                                    int blk, int nblk) {
+  const int lane = threadIdx.x & 63, wpb = blockDim.x >> 6, G = H / MOE_GROUP;
+  const long quads = (groups + 3) / 4;
+  const long nwaves = (long)nblk * wpb;
+  for (long q0 = (long)blk * wpb + (threadIdx.x >> 6); q0 < quads; q0 += nwaves) {
+    const long gi = 4 * q0 + (lane >> 4);
+    if (gi < groups) {  // whole 16-lane segments share gi
+      const long row = gi / G;
+      const int col = (int)(gi - row * G) * MOE_GROUP + 8 * (lane & 15);
+      const size_t off = (size_t)row * H + col;
+      float v[8], yb[8];
+      const int4 yw = norm_ride_chunk(x, nr, off, col, s_rn[row], v);
+      norm_ride_res_out(nr, off, v);
+      bf16x8_to_f32(yw, yb);
+      quant8_1x128(yb, q + off, s + gi, (lane & 15) == 0);
+    }
+  }
+}
+
+// mx_act_quant_body on the normalized rows (chunks = T * H / 8), writing the
+// residual stream as it goes.
+__device__ __forceinline__ void mx_act_quant_norm_body(const uint16_t* __restrict__ x, const NormRide& nr,
+                                                       const float* s_rn, int H, long chunks,
+                                                       uint8_t* __restrict__ q, uint8_t* __restrict__ s,
+                                                       int blk, int nblk) {
+  const long stride = (long)nblk * blockDim.x;
+  const int nch = H >> 3;
+  for (long c0 = (long)blk * blockDim.x; c0 < chunks; c0 += stride) {
+    const long c = c0 + threadIdx.x;  // whole 4-lane groups share the bound (chunks % 4 == 0)
+    float yb[8];
+    if (c < chunks) {
+      const long row = c / nch;
+      const int col = (int)(c - row * nch) * 8;
+      float v[8];
+      const int4 yw = norm_ride_chunk(x, nr, (size_t)c * 8, col, s_rn[row], v);
+      norm_ride_res_out(nr, (size_t)c * 8, v);
+      bf16x8_to_f32(yw, yb);
+    }
+    mx_quant_chunk(yb, c < chunks, c, q, s);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // logits[t, e] = sum_h x[t, h] * w[e, h]   (bf16 operands, fp32 accumulation)
@@ -40,6 +155,8 @@ struct LogitsSide {
 // K is split into ks chunks; with more than one chunk the kernel writes fp32
 // partials [ks, T, E] that router_logits_reduce sums in chunk order.
 // ---------------------------------------------------------------------------
+// NORM: x holds the raw rows and the norm rides along (side.norm; T <= kNormRideT).
+template <bool NORM>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const float* __restrict__ bias, int T, int H, int E, int kchunk, int ks,
@@ -47,6 +164,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   // x tile: 64 rows x 256 columns (four 64-column K steps), rows padded by 8.
   constexpr int KW = 256, LDX = KW + 8;
   __shared__ __attribute__((aligned(16))) uint16_t sx[64][LDX];
+  __shared__ float s_ws[kNormRideT][4], s_rn[kNormRideT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // Tiles (64 tokens x 64 experts x one K chunk) are numbered expert tile fastest,
   // then K chunk, then token tile, and workgroup b takes tile (b % 8) * per + b / 8:
@@ -56,12 +174,21 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   const long total = (long)nct * ((T + 63) / 64) * ks;
   const long per = (total + 7) / 8;
   if (side.qnblk > 0 && (int)blockIdx.x >= side.qblk0) {  // whole workgroup
-    if (side.qmx)
+    if constexpr (NORM) {
+      norm_ride_factors(side.qx, side.norm, T, H, s_ws, s_rn);
+      if (side.qmx)
+        mx_act_quant_norm_body(side.qx, side.norm, s_rn, H, side.qgroups, side.qq, (uint8_t*)side.qs,
+                               blockIdx.x - side.qblk0, side.qnblk);
+      else
+        act_quant_norm_body(side.qx, side.norm, s_rn, H, side.qgroups, side.qq, (float*)side.qs,
+                            blockIdx.x - side.qblk0, side.qnblk);
+    } else if (side.qmx) {
       mx_act_quant_body(side.qx, side.qgroups, side.qq, (uint8_t*)side.qs, blockIdx.x - side.qblk0,
                         side.qnblk);
-    else
+    } else {
       act_quant_vec_body(side.qx, side.qgroups, side.qq, (float*)side.qs, blockIdx.x - side.qblk0,
                          side.qnblk);
+    }
     return;
   }
   if (side.zero != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *side.zero = 0;
@@ -79,6 +206,19 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   const bool erow_ok = erow < E;
   if (!erow_ok) erow = E - 1;
   const uint16_t* wrow = w + (size_t)erow * H;
+  // NORM (T <= kNormRideT, so t0 = 0): the rows' norm factors first; then every x-tile
+  // chunk below row T is normalized as it is loaded (only chunk 0 of threads tid < 32 T,
+  // or 8 T in the 64-column steps; the rest of the tile stays zero).
+  if constexpr (NORM) norm_ride_factors(x, side.norm, T, H, s_ws, s_rn);
+  // chunk (row, col) of the x tile, row < T: the raw or the normalized bf16 values
+  auto x_chunk = [&](int row, int col) -> int4 {
+    if constexpr (NORM) {
+      float v[8];
+      return norm_ride_chunk(x, side.norm, (size_t)row * H + col, col, s_rn[row], v);
+    } else {
+      return *(const int4*)(x + (size_t)row * H + col);
+    }
+  };
 
   v4f acc[4];
 #pragma unroll
@@ -93,9 +233,13 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int idx = tid + c * 256, row = idx >> 5, col = (idx & 31) * 8;
-      const int tr = min(t0 + row, T - 1);  // rows past T load row T-1 and are zeroed
-      xv[c] = *(const int4*)(x + (size_t)tr * H + k0 + col);
-      if (t0 + row >= T) xv[c] = make_int4(0, 0, 0, 0);
+      if (NORM) {
+        xv[c] = (t0 + row < T) ? x_chunk(t0 + row, k0 + col) : make_int4(0, 0, 0, 0);
+      } else {
+        const int tr = min(t0 + row, T - 1);  // rows past T load row T-1 and are zeroed
+        xv[c] = x_chunk(tr, k0 + col);
+        if (t0 + row >= T) xv[c] = make_int4(0, 0, 0, 0);
+      }
     }
     v8bf b[4][2];
 #pragma unroll
@@ -126,7 +270,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
       int idx = tid + c * 256;
       int row = idx >> 3, col = (idx & 7) * 8;
       int4 v = {0, 0, 0, 0};
-      if (t0 + row < T) v = *(const int4*)(x + (size_t)(t0 + row) * H + k0 + col);
+      if (t0 + row < T) v = x_chunk(t0 + row, k0 + col);
       *(int4*)&sx[row][col] = v;
     }
     v8bf b[2];
@@ -312,9 +456,14 @@ static void launch_router_logits(const RouterPlan& pl, const void* x_bf16, const
 #undef MOE_WIDE
   } else {
     const long blocks = logits_blocks(pl, T, E) + std::max(side.qnblk, 0);
-    hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk,
-                       pl.ks, out, side);
+    if (side.norm.gamma != nullptr)
+      hipLaunchKernelGGL(router_logits_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk,
+                         pl.ks, out, side);
+    else
+      hipLaunchKernelGGL(router_logits_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, bias, T, H, E, pl.kchunk,
+                         pl.ks, out, side);
   }
 }
 
@@ -921,13 +1070,37 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
   if (fuse != nullptr) fuse->quant_done = fuse->map_done = false;
   const RouterPlan pl = router_plan(T, H, E);
   const int ks = pl.ks;
-  if (T == 0 || E > kTopkMaxE ||
-      (ks > 1 && (workspace == nullptr || workspace_bytes < (size_t)ks * T * E * sizeof(float)))) {
+  const bool separate =
+      T == 0 || E > kTopkMaxE ||
+      (ks > 1 && (workspace == nullptr || workspace_bytes < (size_t)ks * T * E * sizeof(float)));
+  // The norm rides in the logits launch (with the quantization) where that launch can
+  // carry it: the 64 x 64 form, at most kNormRideT tokens and kNormRideMaxH columns, the
+  // arguments moe_rms_norm_quant accepts. Otherwise moe_rms_norm_quant runs first (and
+  // reports bad arguments) and the router reads its rows.
+  bool ride = false, quant_by_norm = false;
+  if (fuse != nullptr && fuse->norm.gamma != nullptr) {
+    const NormRide& nr = fuse->norm;
+    auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    ride = !separate && T <= kNormRideT && !pl.wide && H % MOE_GROUP == 0 && H <= kNormRideMaxH &&
+           nr.ha >= 1 && nr.ha <= H && nr.eps >= 0.f && (nr.res == nullptr) == (nr.res_out == nullptr) &&
+           a16(x_bf16) && a16(nr.res) && a16(nr.res_out) && a16(nr.gamma) && fuse->xq != nullptr &&
+           fuse->xs != nullptr && ((uintptr_t)fuse->xq & 7) == 0;
+    if (!ride) {
+      const int rc = moe_rms_norm_quant(x_bf16, nr.res, nr.gamma, T, H, nr.ha, nr.eps, fuse->xn,
+                                        nr.res_out, fuse->xq, (float*)fuse->xs, stream);
+      if (rc != MOE_OK) return rc;
+      x_bf16 = fuse->xn;
+      quant_by_norm = !fuse->quant_mx;  // its 1x128 codes are the layer's
+    }
+  }
+  if (separate) {
     int rc = moe_router_logits(x_bf16, w_bf16, bias, T, H, E, logits, workspace, workspace_bytes,
                                stream);
     if (rc != MOE_OK) return rc;
-    return moe_router_topk(logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
-                           renorm_eps, routed_scale, ids, weights, nullptr, stream);
+    rc = moe_router_topk(logits, corr_bias, T, E, K, order, scoring, n_group, topk_group, renorm,
+                         renorm_eps, routed_scale, ids, weights, nullptr, stream);
+    if (rc == MOE_OK && fuse != nullptr) fuse->quant_done = quant_by_norm;
+    return rc;
   }
   MOE_API_BEGIN("moe_layer_forward (router)");
   // The checks of moe_router_logits and moe_router_topk.
@@ -976,12 +1149,13 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
   // The quantization in the logits launch (codes as moe_act_quant_1x128's, or as
   // moe_act_quant_mx's; the MX form only as extra workgroups of the 64 x 64 form).
   const bool do_quant = fuse != nullptr && fuse->xq != nullptr && fuse->xs != nullptr &&
-                        ((uintptr_t)fuse->xq & 7) == 0 &&
+                        ((uintptr_t)fuse->xq & 7) == 0 && !quant_by_norm &&
                         (fuse->quant_mx ? H % 32 == 0 && !pl.wide : H % MOE_GROUP == 0);
   if (do_quant) {
     side.qq = fuse->xq;
     side.qs = fuse->xs;
     side.qmx = fuse->quant_mx;
+    if (ride) side.norm = fuse->norm;  // ride implies do_quant and the 64 x 64 form
     if (!pl.wide) {  // extra workgroups; the wide form quantizes as it loads x
       side.qx = (const uint16_t*)x_bf16;
       if (fuse->quant_mx) {
@@ -1039,7 +1213,7 @@ int moe::router_logits_topk(const void* x_bf16, const void* w_bf16, const float*
 #undef MOE_TOPK_FUSED
   }
   if (fuse != nullptr) {
-    fuse->quant_done = do_quant;
+    fuse->quant_done = do_quant || quant_by_norm;
     fuse->map_done = do_map;
   }
   MOE_API_END();
