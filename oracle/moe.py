@@ -55,7 +55,7 @@ def moe_sparse_fp8(x, ids, w, w13_q, w13_s, w2_q, w2_s, shared=None, requant_h=T
 
     x [T,H] float32 holding bf16 values; ids/w [T,K]; w13_q [E,2I,H] uint8, w13_s [E,2I/128,H/128];
     w2_q [E,H,I] uint8, w2_s [E,H/128,I/128]; shared = (w13_q, w13_s, w2_q, w2_s) of one
-    expert or None. ``experts`` optionally restricts the routed experts evaluated (the others
+    expert, a list of such tuples (their outputs added in list order), or None. ``experts`` optionally restricts the routed experts evaluated (the others
     contribute nothing) so full-size layers can be checked on a subset. ``chan`` = (c13
     [E, 2I], c2 [E, H]) multiplies each routed expert's dequantized weight rows (the
     reference's FP8 per-channel weight scales, moe_cte.py:178-188, moe_tkg.py:87-91).
@@ -80,8 +80,8 @@ def moe_sparse_fp8(x, ids, w, w13_q, w13_s, w2_q, w2_s, shared=None, requant_h=T
             w2 = (w2 * np.asarray(chan[1][e], F)[:, None]).astype(F)
         y = expert_mlp(xhat[rows], w13, w2, requant_h)
         out[rows] = (out[rows] + y * wt[:, None]).astype(F)
-    if shared is not None:
-        sq13, ss13, sq2, ss2 = shared
+    for sh in ([] if shared is None else shared if isinstance(shared, list) else [shared]):
+        sq13, ss13, sq2, ss2 = sh
         y = expert_mlp(xhat, dequant_weight_128x128(sq13, ss13),
                        dequant_weight_128x128(sq2, ss2), requant_h)
         out = (out + y).astype(F)

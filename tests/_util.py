@@ -47,9 +47,10 @@ def oracle_weights(w, experts=None):
 
 
 def oracle_shared(w):
+    """The shared experts' operands for oracle.moe.moe_sparse_fp8: None, one tuple, or a
+    list of tuples from two shared experts on."""
     if w.n_shared == 0:
         return None
-    if w.n_shared != 1:
-        raise NotImplementedError
-    return (np_u8(w.shared_w13[0]), np_f32(w.shared_w13_scale[0]), np_u8(w.shared_w2[0]),
-            np_f32(w.shared_w2_scale[0]))
+    sh = [(np_u8(w.shared_w13[j]), np_f32(w.shared_w13_scale[j]), np_u8(w.shared_w2[j]),
+           np_f32(w.shared_w2_scale[j])) for j in range(w.n_shared)]
+    return sh[0] if w.n_shared == 1 else sh

@@ -392,6 +392,24 @@ def test_layer_fused_mapping_tile_heights(cuda, T, B):
     assert torch.equal(out, _op_path(cfg, w, x))
 
 
+@pytest.mark.parametrize("B,S,K", [(256, 1, 8), (16, 2, 4), (1, 0, 1), (64, 1, 2), (3, 2, 8)])
+def test_layer_one_token_mapping(cuda, B, S, K):
+    """At one token the top-k launch's mapping is written by one wave: each selected
+    expert e gets block, slot, compact row and tile rank(e) (its place among the
+    selected experts), and the shared experts' tiles follow. Over block sizes (1, 3,
+    16, 64, 256 slots), 0-2 shared experts and top-1/2/4/8 the layer equals the
+    oracle and the op-by-op path (the general mapping kernel and tile builder) bit for
+    bit."""
+    cfg = MoEConfig(1024, 512, 32, K, n_shared=S, scoring="sigmoid", grouped=True, n_group=4,
+                    topk_group=2, renorm=True, routed_scaling=2.5, block_size=B)
+    say("layer one-token mapping", B, S, K)
+    w = synthetic.make_weights(cfg, 11, device=cuda, experts_device=cuda)
+    for seed in (11, 12):
+        x = synthetic.hidden_states(1, cfg.hidden, seed).to(cuda)
+        out = _check_layer(cfg, w, x, tag=f"one-token mapping B={B} S={S} K={K} seed={seed}")
+        assert torch.equal(out, _op_path(cfg, w, x))
+
+
 def test_layer_glm45_full_size_zipf(cuda):
     """GLM-4.5 layer (hidden 5120, intermediate 1536, 160 experts + 1 shared) at 4096
     tokens with Zipf(1.2) expert popularity and 10% of the experts empty: overfull

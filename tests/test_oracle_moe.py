@@ -78,6 +78,12 @@ def test_shared_expert_adds_with_unit_weight():
     routed = moe_sparse_fp8(x, ids, w, q13, s13, q2, s2)
     only = moe_sparse_fp8(x, np.zeros_like(ids), np.ones_like(w) * 0.5, q13[:1], s13[:1], q2[:1], s2[:1])
     assert np.allclose(with_sh - routed, only, rtol=1e-5, atol=1e-6)
+    # two shared experts (a list): each adds its own unit-weight output
+    two = moe_sparse_fp8(x, ids, w, q13, s13, q2, s2,
+                         shared=[tuple(a[0] for a in shared), (q13[1], s13[1], q2[1], s2[1])])
+    only1 = moe_sparse_fp8(x, np.zeros_like(ids), np.ones_like(w) * 0.5, q13[1:2], s13[1:2], q2[1:2],
+                           s2[1:2])
+    assert np.allclose(two - routed, only + only1, rtol=1e-5, atol=1e-6)
 
 
 def test_topk_reduce_docstring_examples():

@@ -413,4 +413,83 @@ static __device__ void map_small_body(const int32_t* __restrict__ ids, const int
   }
 }
 
+// map_small_body's outputs for one token (T = 1) with row tiles (to.span == 0), written
+// by one wave with no barrier. The token's K ids (s_ids, K <= 64) are distinct experts
+// or negative (the top-k selection names each expert at most once), so each selected
+// expert e has one row, and with rank(e) = #{selected experts < e}: block rank(e),
+// slot rank(e) * B holding token 0, compact row rank(e) and tile rank(e); blocks past
+// the selected ones belong to E - 1 with condition 0, and the shared experts' tiles
+// follow. Every output address is written once. PM: E <= 64 PM (experts per lane).
+template <int PM>
+static __device__ void map_one_token(const int* s_ids, int K, int E, int B, int N,
+                                     int32_t* __restrict__ tpid, int32_t* __restrict__ block_to_expert,
+                                     int32_t* __restrict__ conditions,
+                                     int32_t* __restrict__ expert_counts, int32_t* __restrict__ inv_pos,
+                                     const MapWs& ws, const TileOut& to) {
+  const int lane = threadIdx.x & 63;
+  const int id = lane < K ? s_ids[lane] : -1;
+  const bool sel = id >= 0 && id < E;
+  const int m = (int)__popcll(__ballot(sel));
+  const int dropped = (int)__popcll(__ballot(lane < K && id >= E));
+  // one pass over the ids (uniform values): this lane's rank, the selected experts
+  // below each of its experts e = lane + 64 j, whether e is selected, and the expert of
+  // block `lane` (N <= T K <= 64 blocks)
+  int rank = 0, blk_e = E - 1, below[PM];
+  bool mine[PM];
+#pragma unroll
+  for (int j = 0; j < PM; ++j) {
+    below[j] = 0;
+    mine[j] = false;
+  }
+  for (int k = 0; k < K; ++k) {
+    const int o = __builtin_amdgcn_readlane(id, k);
+    if (o >= 0 && o < E) {  // uniform
+      rank += o < id ? 1 : 0;
+#pragma unroll
+      for (int j = 0; j < PM; ++j) {
+        below[j] += o < lane + 64 * j ? 1 : 0;
+        mine[j] = mine[j] || o == lane + 64 * j;
+      }
+    }
+  }
+  // the expert of block `lane`: the selected expert whose rank is `lane`
+  for (int k = 0; k < K; ++k) {
+    const int o = __builtin_amdgcn_readlane(id, k), r = __builtin_amdgcn_readlane(rank, k);
+    if (o >= 0 && o < E && r == lane) blk_e = o;
+  }
+#pragma unroll
+  for (int j = 0; j < PM; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      if (expert_counts != nullptr) expert_counts[e] = mine[j] ? 1 : 0;
+      ws.block_off[e] = below[j];
+    }
+  }
+  if (lane < N) {
+    block_to_expert[lane] = lane < m ? blk_e : E - 1;
+    if (conditions != nullptr) conditions[lane] = lane < m ? 1 : 0;
+  }
+  // slots, block by block: the first slot of block b < m holds token 0, the rest are empty
+  const bool vec = ((uintptr_t)tpid & 15) == 0 && B % 4 == 0;  // uniform
+  for (int b = 0; b < N; ++b) {
+    int32_t* blk = tpid + (long)b * B;
+    const int first = b < m ? 0 : -1;
+    if (vec) {
+      for (int i = 4 * lane; i < B; i += 256) *(int4*)(blk + i) = make_int4(i == 0 ? first : -1, -1, -1, -1);
+    } else {
+      for (int i = lane; i < B; i += 64) blk[i] = i == 0 ? first : -1;
+    }
+  }
+  if (lane < K && inv_pos != nullptr) inv_pos[lane] = sel ? (to.compact ? rank : rank * B) : -1;
+  if (lane == 0) ws.status[0] = dropped;
+  if (to.tiles == nullptr) return;
+  if (sel && rank < to.max_tiles)
+    to.tiles[rank] = make_int4(id, rank * B, 1, to.compact ? rank : rank * B);
+  const long NB = (long)N * B;
+  const long row_sh = to.compact ? to.row_shared : NB;
+  for (int j = lane; j < to.n_shared; j += 64)
+    if (m + j < to.max_tiles) to.tiles[m + j] = make_int4(E + j, (int)(NB + j), 1, (int)(row_sh + j));
+  if (lane == 0) to.num_tiles[0] = min(m + to.n_shared, to.max_tiles);
+}
+
 }  // namespace moe

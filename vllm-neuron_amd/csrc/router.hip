@@ -951,7 +951,8 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     // scope and takes a ticket; the last one acquires every workgroup's ids. One
     // fence per workgroup: a device-scope fence writes back (release) or
     // invalidates (acquire) the whole L2 of its XCD. mj.ws.status[1] was cleared
-    // by the logits launch.
+    // by the logits launch. One token with row tiles: one wave writes the same
+    // outputs from the ids in LDS (map_one_token), with no barrier or scan.
     __shared__ uint32_t s_bm[PM * 64][8];
     __shared__ int s_blk[PM * 64], s_cnt[PM * 64], s_cex[PM * 64], s_tile[PM * 64];
     __shared__ int s_wave[16];
@@ -966,6 +967,12 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
       }
       __syncthreads();
       if (!s_last) return;  // whole workgroup
+    }
+    if (T == 1 && lds_ids && !mj.to.span) {  // workgroup-uniform: one token, row tiles
+      if (threadIdx.x < 64)
+        map_one_token<PM>(s_ids, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond, mj.counts, mj.inv,
+                          mj.ws, mj.to);
+      return;
     }
     map_small_body(ids, lds_ids ? s_ids : nullptr, T, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond,
                    mj.counts, mj.inv, mj.ws, mj.to, s_bm, s_blk, s_cnt, s_cex, s_tile, s_wave);
