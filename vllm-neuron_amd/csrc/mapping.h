@@ -413,65 +413,66 @@ static __device__ void map_small_body(const int32_t* __restrict__ ids, const int
   }
 }
 
-// map_small_body's outputs for one token (T = 1) with row tiles (to.span == 0), written
-// by one wave with no barrier. The token's K ids (s_ids, K <= 64) are distinct experts
+// map_small_body's outputs for one token (T = 1) with row tiles (to.span == 0), with no
+// barrier. The token's K ids (s_ids: 16-byte aligned LDS, K <= 64) are distinct experts
 // or negative (the top-k selection names each expert at most once), so each selected
-// expert e has one row, and with rank(e) = #{selected experts < e}: block rank(e),
-// slot rank(e) * B holding token 0, compact row rank(e) and tile rank(e); blocks past
-// the selected ones belong to E - 1 with condition 0, and the shared experts' tiles
-// follow. Every output address is written once. PM: E <= 64 PM (experts per lane).
-template <int PM>
+// expert e has one row, and with rank(e) = #{selected experts < e}: block rank(e), slot
+// rank(e) * B holding token 0, compact row rank(e) and tile rank(e); blocks past the
+// selected ones belong to E - 1 with condition 0, and the shared experts' tiles follow.
+// Every thread scans the K ids and plays three parts: expert e = tid (E <= blockDim.x),
+// pair k = tid and block b = tid (N <= T K <= 64); the waves then fill the slots block by
+// block. Every output address is written once.
 static __device__ void map_one_token(const int* s_ids, int K, int E, int B, int N,
                                      int32_t* __restrict__ tpid, int32_t* __restrict__ block_to_expert,
                                      int32_t* __restrict__ conditions,
                                      int32_t* __restrict__ expert_counts, int32_t* __restrict__ inv_pos,
                                      const MapWs& ws, const TileOut& to) {
-  const int lane = threadIdx.x & 63;
-  const int id = lane < K ? s_ids[lane] : -1;
-  const bool sel = id >= 0 && id < E;
-  const int m = (int)__popcll(__ballot(sel));
-  const int dropped = (int)__popcll(__ballot(lane < K && id >= E));
-  // one pass over the ids (uniform values): this lane's rank, the selected experts
-  // below each of its experts e = lane + 64 j, whether e is selected, and the expert of
-  // block `lane` (N <= T K <= 64 blocks)
-  int rank = 0, blk_e = E - 1, below[PM];
-  bool mine[PM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const int my = tid < K ? s_ids[tid] : -1;  // pair tid's expert
+  int m = 0, dropped = 0, below = 0, rank = 0;
+  bool mine = false;
+  for (int k0 = 0; k0 < K; k0 += 4) {
+    const int4 o4 = *(const int4*)(s_ids + k0);  // entries past K are not used
+    const int o[4] = {o4.x, o4.y, o4.z, o4.w};
 #pragma unroll
-  for (int j = 0; j < PM; ++j) {
-    below[j] = 0;
-    mine[j] = false;
-  }
-  for (int k = 0; k < K; ++k) {
-    const int o = __builtin_amdgcn_readlane(id, k);
-    if (o >= 0 && o < E) {  // uniform
-      rank += o < id ? 1 : 0;
-#pragma unroll
-      for (int j = 0; j < PM; ++j) {
-        below[j] += o < lane + 64 * j ? 1 : 0;
-        mine[j] = mine[j] || o == lane + 64 * j;
-      }
+    for (int u = 0; u < 4; ++u) {
+      const bool live = k0 + u < K;
+      const bool ok = live && o[u] >= 0 && o[u] < E;
+      m += ok ? 1 : 0;
+      dropped += (live && o[u] >= E) ? 1 : 0;
+      below += (ok && o[u] < tid) ? 1 : 0;
+      rank += (ok && o[u] < my) ? 1 : 0;
+      mine = mine || (ok && o[u] == tid);
     }
   }
-  // the expert of block `lane`: the selected expert whose rank is `lane`
-  for (int k = 0; k < K; ++k) {
-    const int o = __builtin_amdgcn_readlane(id, k), r = __builtin_amdgcn_readlane(rank, k);
-    if (o >= 0 && o < E && r == lane) blk_e = o;
+  if (tid < E) {
+    if (expert_counts != nullptr) expert_counts[tid] = mine ? 1 : 0;
+    ws.block_off[tid] = below;
   }
-#pragma unroll
-  for (int j = 0; j < PM; ++j) {
-    const int e = lane + 64 * j;
-    if (e < E) {
-      if (expert_counts != nullptr) expert_counts[e] = mine[j] ? 1 : 0;
-      ws.block_off[e] = below[j];
-    }
+  const bool sel = my >= 0 && my < E;  // false past K
+  const bool fits = sel && rank < N;    // always, with N from moe_num_blocks; else dropped
+  if (tid < K && inv_pos != nullptr) inv_pos[tid] = fits ? (to.compact ? rank : rank * B) : -1;
+  if (fits) {
+    block_to_expert[rank] = my;
+    if (conditions != nullptr) conditions[rank] = 1;
   }
-  if (lane < N) {
-    block_to_expert[lane] = lane < m ? blk_e : E - 1;
-    if (conditions != nullptr) conditions[lane] = lane < m ? 1 : 0;
+  if (tid >= m && tid < N) {
+    block_to_expert[tid] = E - 1;
+    if (conditions != nullptr) conditions[tid] = 0;
   }
+  const long NB = (long)N * B;
+  if (to.tiles != nullptr) {
+    if (sel && rank < to.max_tiles) to.tiles[rank] = make_int4(my, rank * B, 1, to.compact ? rank : rank * B);
+    const long row_sh = to.compact ? to.row_shared : NB;
+    if (tid < to.n_shared && m + tid < to.max_tiles)
+      to.tiles[m + tid] = make_int4(E + tid, (int)(NB + tid), 1, (int)(row_sh + tid));
+    if (tid == 0) to.num_tiles[0] = min(m + to.n_shared, to.max_tiles);
+  }
+  const int unfit = (int)__popcll(__ballot(sel && !fits));  // pairs are threads 0..K-1: wave 0
+  if (tid == 0) ws.status[0] = dropped + unfit;
   // slots, block by block: the first slot of block b < m holds token 0, the rest are empty
   const bool vec = ((uintptr_t)tpid & 15) == 0 && B % 4 == 0;  // uniform
-  for (int b = 0; b < N; ++b) {
+  for (int b = wave; b < N; b += nwaves) {
     int32_t* blk = tpid + (long)b * B;
     const int first = b < m ? 0 : -1;
     if (vec) {
@@ -480,16 +481,6 @@ static __device__ void map_one_token(const int* s_ids, int K, int E, int B, int 
       for (int i = lane; i < B; i += 64) blk[i] = i == 0 ? first : -1;
     }
   }
-  if (lane < K && inv_pos != nullptr) inv_pos[lane] = sel ? (to.compact ? rank : rank * B) : -1;
-  if (lane == 0) ws.status[0] = dropped;
-  if (to.tiles == nullptr) return;
-  if (sel && rank < to.max_tiles)
-    to.tiles[rank] = make_int4(id, rank * B, 1, to.compact ? rank : rank * B);
-  const long NB = (long)N * B;
-  const long row_sh = to.compact ? to.row_shared : NB;
-  for (int j = lane; j < to.n_shared; j += 64)
-    if (m + j < to.max_tiles) to.tiles[m + j] = make_int4(E + j, (int)(NB + j), 1, (int)(row_sh + j));
-  if (lane == 0) to.num_tiles[0] = min(m + to.n_shared, to.max_tiles);
 }
 
 }  // namespace moe

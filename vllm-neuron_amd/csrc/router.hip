@@ -641,7 +641,7 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
   __shared__ float s_act[4][PM * 64];
   __shared__ float s_key[4][PM * 64];
   // one workgroup (one token) ending in the mapping: its ids also go to LDS
-  __shared__ int s_ids[MAP ? 64 : 1];
+  __shared__ __attribute__((aligned(16))) int s_ids[MAP ? 64 : 4];
   const bool lds_ids = MAP && gridDim.x == 1 && T * K <= 64;  // workgroup-uniform
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int t0 = blockIdx.x * tpb, t = t0 + wave;
@@ -951,8 +951,8 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     // scope and takes a ticket; the last one acquires every workgroup's ids. One
     // fence per workgroup: a device-scope fence writes back (release) or
     // invalidates (acquire) the whole L2 of its XCD. mj.ws.status[1] was cleared
-    // by the logits launch. One token with row tiles: one wave writes the same
-    // outputs from the ids in LDS (map_one_token), with no barrier or scan.
+    // by the logits launch. One token with row tiles: the same outputs from the ids
+    // in LDS (map_one_token), with no barrier or scan.
     __shared__ uint32_t s_bm[PM * 64][8];
     __shared__ int s_blk[PM * 64], s_cnt[PM * 64], s_cex[PM * 64], s_tile[PM * 64];
     __shared__ int s_wave[16];
@@ -969,9 +969,8 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
       if (!s_last) return;  // whole workgroup
     }
     if (T == 1 && lds_ids && !mj.to.span) {  // workgroup-uniform: one token, row tiles
-      if (threadIdx.x < 64)
-        map_one_token<PM>(s_ids, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond, mj.counts, mj.inv,
-                          mj.ws, mj.to);
+      map_one_token(s_ids, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond, mj.counts, mj.inv, mj.ws,
+                    mj.to);
       return;
     }
     map_small_body(ids, lds_ids ? s_ids : nullptr, T, K, E, mj.B, mj.N, mj.tpid, mj.b2e, mj.cond,
