@@ -505,11 +505,6 @@ __global__ void router_logits_reduce(const float* __restrict__ part, const float
 constexpr int kTopkMaxE = 1024;
 constexpr int kTopkMaxP = kTopkMaxE / 64;
 
-struct KeyIdx {
-  float v;
-  int i;
-};
-
 __device__ __forceinline__ bool better(float v, int i, float v2, int i2) {
   return v > v2 || (v == v2 && i < i2);
 }
@@ -526,50 +521,30 @@ __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(dpp_i<CTRL, ROW_MASK>(__float_as_int(v)));
 }
 
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void argmax_step(float& v, int& i) {
-  const float v2 = dpp_f<CTRL, ROW_MASK>(v);
-  const int i2 = dpp_i<CTRL, ROW_MASK>(i);
-  if (better(v2, i2, v, i)) {
-    v = v2;
-    i = i2;
-  }
-}
-
-// Wave argmax under better() (larger value, then lower index). Candidates are
-// never NaN (a NaN key is never taken as a lane's candidate), so better() is a
-// total order and the result does not depend on the reduction tree: rows of 16
-// lanes by quad swaps and mirrors, then the rows into lane 63, read as scalars.
-__device__ __forceinline__ KeyIdx wave_argmax(float v, int i) {
-  argmax_step<0xB1, 0xF>(v, i);
-  argmax_step<0x4E, 0xF>(v, i);
-  argmax_step<0x141, 0xF>(v, i);
-  argmax_step<0x140, 0xF>(v, i);
-  argmax_step<0x142, 0xA>(v, i);
-  argmax_step<0x143, 0xC>(v, i);
-  return {__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)),
-          __builtin_amdgcn_readlane(i, 63)};
-}
-
-// Selection candidates as one unsigned 64-bit value each: the key's bits mapped
-// to an order-preserving u32 (negative keys inverted, the sign bit set on the
-// rest; -0 is taken as +0, which better() treats as equal) above the inverted
-// expert index, so a larger value is exactly better() (larger key, then lower
-// index) and one u64 compare replaces it. 0 is "no candidate": NaN keys, masked
-// experts and lanes past E.
-__device__ __forceinline__ uint64_t pack_key(float v, int e) {
+// Selection candidates as doubles: u * 1024 + (1023 - e), with u an order-preserving
+// u32 image of the key (negative keys inverted, the sign bit set on the rest; -0 taken
+// as +0, which better() treats as equal) and the expert e < 1024, is an integer below
+// 2^42, so exact, and a larger value is exactly better() (larger key, then lower
+// index): a reduction step is one v_max_f64 (a packed u64 took a 64-bit compare and
+// two selects). 0 is "no candidate": NaN keys (never packed), masked experts and lanes
+// past E (u >= 1 for every key that is not NaN).
+__device__ __forceinline__ double pack_key_d(float v, int e) {
   uint32_t u = (uint32_t)__float_as_int(v == 0.f ? 0.f : v);
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)e;
+  return (double)u * 1024.0 + (double)(1023 - e);
 }
-__device__ __forceinline__ float unpack_key(uint64_t p) {
-  const uint32_t o = (uint32_t)(p >> 32);
+__device__ __forceinline__ uint32_t packed_key_u(double p) { return (uint32_t)floor(p * (1.0 / 1024.0)); }
+__device__ __forceinline__ int unpack_id_d(double p) {
+  return 1023 - (int)(p - (double)packed_key_u(p) * 1024.0);
+}
+__device__ __forceinline__ float unpack_key_d(double p) {
+  const uint32_t o = packed_key_u(p);
   return __int_as_float((int)((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o));
 }
 
 // Per-lane bitonic sort of N (a power of two) packed candidates, descending.
 template <int N>
-__device__ __forceinline__ void sort_desc_u64(uint64_t (&a)[N]) {
+__device__ __forceinline__ void sort_desc_d(double (&a)[N]) {
 #pragma unroll
   for (int k = 2; k <= N; k <<= 1)
 #pragma unroll
@@ -578,34 +553,33 @@ __device__ __forceinline__ void sort_desc_u64(uint64_t (&a)[N]) {
       for (int i = 0; i < N; ++i) {
         const int l = i ^ j;
         if (l > i) {
-          const uint64_t x = a[i], y = a[l];
-          const bool sw = ((i & k) == 0) ? (x < y) : (x > y);
-          a[i] = sw ? y : x;
-          a[l] = sw ? x : y;
+          const double hi = fmax(a[i], a[l]), lo = fmin(a[i], a[l]);
+          a[i] = ((i & k) == 0) ? hi : lo;
+          a[l] = ((i & k) == 0) ? lo : hi;
         }
       }
 }
 
 template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ void max_step_u64(uint64_t& v) {
-  const uint32_t lo = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)(uint32_t)v);
-  const uint32_t hi = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)(uint32_t)(v >> 32));
-  const uint64_t o = ((uint64_t)hi << 32) | lo;
-  v = o > v ? o : v;
+__device__ __forceinline__ void max_step_d(double& v) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)dpp_i<CTRL, ROW_MASK>((int)(uint32_t)(b >> 32));
+  v = fmax(v, __longlong_as_double((long long)(((uint64_t)hi << 32) | lo)));
 }
 
-// Wave maximum of packed candidates (the same reduction tree as wave_argmax),
-// read from lane 63 as a scalar.
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-  max_step_u64<0xB1, 0xF>(v);
-  max_step_u64<0x4E, 0xF>(v);
-  max_step_u64<0x141, 0xF>(v);
-  max_step_u64<0x140, 0xF>(v);
-  max_step_u64<0x142, 0xA>(v);
-  max_step_u64<0x143, 0xC>(v);
-  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, 63);
-  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
-  return ((uint64_t)hi << 32) | lo;
+// Wave maximum of packed candidates (the same reduction tree), read from lane 63.
+__device__ __forceinline__ double wave_max_d(double v) {
+  max_step_d<0xB1, 0xF>(v);
+  max_step_d<0x4E, 0xF>(v);
+  max_step_d<0x141, 0xF>(v);
+  max_step_d<0x140, 0xF>(v);
+  max_step_d<0x142, 0xA>(v);
+  max_step_d<0x143, 0xC>(v);
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)b, 63);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), 63);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
 // Value of lane k (k wave-uniform): a scalar read, no LDS round trip.
@@ -855,15 +829,16 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
         gscore = NEG_INF;
         gidx += 64;
       }
-      uint64_t keep = 0;
-      for (int q = 0; q < topk_group; ++q) {
-        KeyIdx b = wave_argmax(gscore, gidx);
-        if (b.i < 128) keep |= 1ull << (b.i & 63);
-        if (lane == (b.i & 63)) {
-          gscore = NEG_INF;
-          gidx = 0x7fffffff;
-        }
+      // Group g (lane g < n_group) is kept when fewer than topk_group groups rank above
+      // it under better(): one scan of the n_group scores instead of topk_group rounds
+      // of a wave arg-max (the same set: better() is a total order on the groups).
+      int above = 0;
+      for (int q = 0; q < n_group; ++q) {
+        const float sq = lane_f32(gscore, q);
+        const int iq = __builtin_amdgcn_readlane(gidx, q);
+        above += better(sq, iq, gscore, gidx) ? 1 : 0;
       }
+      const uint64_t keep = __ballot(lane < n_group && above < topk_group);
 #pragma unroll
       for (int j = 0; j < PM; ++j) {
         int e = lane + 64 * j;
@@ -876,23 +851,23 @@ __global__ __launch_bounds__(MAP ? 1024 : 256) void router_topk_kernel(
     // compare per step), after which the winning lane (the one whose head it is:
     // indices are distinct) drops its head. A NaN key is never a candidate; with
     // no candidate left the round's maximum is 0 and its id is -1.
-    uint64_t pk[PM];
+    double pk[PM];
 #pragma unroll
     for (int j = 0; j < PM; ++j)
-      pk[j] = (valid[j] && key[j] == key[j]) ? pack_key(key[j], lane + 64 * j) : 0ull;
-    sort_desc_u64<PM>(pk);
+      pk[j] = (valid[j] && key[j] == key[j]) ? pack_key_d(key[j], lane + 64 * j) : 0.0;
+    sort_desc_d<PM>(pk);
     int my_id = -1;
     float my_key = 0.f;
     for (int k = 0; k < K; ++k) {
-      const uint64_t best = wave_max_u64(pk[0]);
+      const double best = wave_max_d(pk[0]);
       if (pk[0] == best) {  // the winner; lanes with nothing left shift zeros
 #pragma unroll
         for (int j = 0; j + 1 < PM; ++j) pk[j] = pk[j + 1];
-        pk[PM - 1] = 0ull;
+        pk[PM - 1] = 0.0;
       }
       if (lane == k) {
-        my_id = best != 0ull ? (int)~(uint32_t)best : -1;
-        my_key = best != 0ull ? unpack_key(best) : NEG_INF;
+        my_id = best != 0.0 ? unpack_id_d(best) : -1;
+        my_key = best != 0.0 ? unpack_key_d(best) : NEG_INF;
       }
     }
 
