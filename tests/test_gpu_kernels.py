@@ -129,6 +129,10 @@ ROUTER_CASES = [
     ("glm_160", 160, 8, 2, 1, 1, 1, True, 1e-20, 2.5, True),
     ("grouped_softmax", 64, 6, 2, 0, 8, 3, False, 0.0, 1.0, True),
     ("grouped_1expert_groups", 16, 3, 2, 1, 16, 5, True, 1e-20, 1.0, False),
+    # more selections than an 8-long merge list: K rounds of a wave maximum
+    ("sigmoid_act_topk_k16_rounds", 128, 16, 1, 1, 1, 1, True, 1e-20, 1.0, False),
+    # 1024 experts (16 per lane): merge lists of 16
+    ("softmax_topk_act_k12_e1024", 1024, 12, 0, 0, 1, 1, False, 0.0, 1.0, False),
 ]
 
 
