@@ -410,6 +410,30 @@ def test_layer_one_token_mapping(cuda, B, S, K):
         assert torch.equal(out, _op_path(cfg, w, x))
 
 
+@pytest.mark.parametrize("B", [256, 3])
+def test_layer_one_token_fewer_candidates_than_top_k(cuda, B):
+    """A NaN correction bias makes every expert but three a NaN key, which is never
+    selected: at one token the top-8 holds three experts and five -1 ids, so the
+    one-token mapping has three blocks, three tiles and the shared expert's, and five
+    pairs with no row. The layer equals the op-by-op path (the general mapping kernel
+    and tile builder) bit for bit, and its routing equals ops.router_topk's."""
+    cfg = MoEConfig(1024, 512, 32, 8, n_shared=1, scoring="sigmoid", grouped=True, n_group=1,
+                    topk_group=1, renorm=True, routed_scaling=2.5, block_size=B)
+    say("layer one token, fewer candidates", B)
+    w = synthetic.make_weights(cfg, 13, device=cuda, experts_device=cuda)
+    cb = torch.full((cfg.n_experts,), float("nan"), device=cuda)
+    cb[[3, 17, 29]] = torch.tensor([0.01, -0.02, 0.0], device=cuda)
+    w.corr_bias = cb
+    x = synthetic.hidden_states(1, cfg.hidden, 13).to(cuda)
+    out, ids, wts, lg = ops.layer_forward(x, w, cfg, return_routing=True)
+    ids2, wts2 = ops.router_topk(lg, cfg.top_k, ops.ORDER_GROUPED, cfg.scoring, cfg.n_group,
+                                 cfg.topk_group, w.corr_bias, cfg.renorm, 1e-20, cfg.routed_scaling)
+    assert torch.equal(ids, ids2) and torch.equal(wts, wts2)
+    got = ids.cpu().numpy()[0]
+    assert sorted(got[got >= 0].tolist()) == [3, 17, 29] and int((got == -1).sum()) == 5
+    assert torch.equal(out.view(torch.int16), _op_path(cfg, w, x).view(torch.int16))
+
+
 def test_layer_glm45_full_size_zipf(cuda):
     """GLM-4.5 layer (hidden 5120, intermediate 1536, 160 experts + 1 shared) at 4096
     tokens with Zipf(1.2) expert popularity and 10% of the experts empty: overfull
