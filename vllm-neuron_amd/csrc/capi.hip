@@ -252,9 +252,9 @@ static int layer_forward_impl(const char* _moe_fn, const void* x_bf16, const voi
                                    w2_shared_scale, nullptr, n_shared, (int)NB, w.btiles, w.bnum, mbt,
                                    w.y, stream));
   } else {
-    MOE_STEP(moe_expert_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, nullptr, w13_shared,
-                                w13_shared_scale, nullptr, n_shared, w.tpid, (int)NB, w.tiles,
-                                w.num_tiles, max_tiles, mt, w.hq, w.hs, stream));
+    MOE_STEP(layer_gate_up(w.xq, w.xs, T, H, I, E, w13, w13_scale, w13_shared, w13_shared_scale,
+                           n_shared, w.tpid, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.hq, w.hs,
+                           stream));
     MOE_STEP(moe_expert_down(w.hq, w.hs, T, H, I, E, w2, w2_scale, nullptr, w2_shared,
                              w2_shared_scale, nullptr, n_shared, (int)NB, w.tiles, w.num_tiles,
                              max_tiles, mt, w.y,

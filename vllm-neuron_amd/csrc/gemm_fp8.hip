@@ -53,6 +53,9 @@ struct GemmArgs {
   const float* cssh;
   int T, H, I, E, nsh;
   long NB;
+  // gate_up: every routed and shared slot of a tile holds token 0 (the layer at one
+  // token, whose own mapping wrote the tiles), so no token ids are loaded
+  int tok0;
 };
 
 __device__ __forceinline__ v4f mfma_fp8(const v8i& a, const v8i& b) {
@@ -183,27 +186,34 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
       wb = (is_sh ? p.wsh : p.w) + (size_t)ej * p.H * p.I;
       wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * (p.H / 128) * KB;
     }
-    if (tid < MT) {
-      long src = -1;
-      if (tid < nrows) {
-        const long slot = slot0 + tid;
-        if (KIND == 0) {
+    // Sources of the tile's rows: the token (gate_up) or the h row (down); -1 padding.
+    // Down rows and one-token gate_up rows need no load (direct), so then the first
+    // stages go out right after the tile descriptor, with the weight block scales,
+    // instead of one round trip later behind the token ids and a barrier.
+    const bool direct = KIND == 1 || p.tok0 != 0;  // workgroup-uniform
+    auto direct_src = [&](int r) -> long { return r < nrows ? (KIND == 0 ? 0L : row0 + r) : -1L; };
+    auto fill_tables = [&]() {
+      if (tid < MT) {
+        long src = -1;
+        if (direct) {
+          src = direct_src(tid);
+        } else if (tid < nrows) {
+          const long slot = slot0 + tid;
           src = is_sh ? slot - p.NB - (long)ej * p.T : (long)p.tpid[slot];
           if (src >= p.T) src = -1;  // token ids outside [0, T) are treated as padding
-        } else {
-          src = row0 + tid;
         }
+        sSrc[tid] = src;
       }
-      sSrc[tid] = src;
-    }
-    // weight block scales of the tile's two 128-row halves: gate / up blocks
-    // (gate_up) or the two output blocks (down)
-    for (int i = tid; i < (KIND == 0 ? 2 : NW / 2) * KB; i += 64 * NW) {
-      const int h = i / KB, kb = i - h * KB;
-      const int rb = (KIND == 0) ? (h == 0 ? nt : p.I / 128 + nt) : nt * (NW / 2) + h;
-      sWs[h][kb] = wsb[(size_t)rb * KB + kb];
-    }
-    __syncthreads();
+      // weight block scales of the tile's two 128-row halves: gate / up blocks
+      // (gate_up) or the two output blocks (down)
+      for (int i = tid; i < (KIND == 0 ? 2 : NW / 2) * KB; i += 64 * NW) {
+        const int h = i / KB, kb = i - h * KB;
+        const int rb = (KIND == 0) ? (h == 0 ? nt : p.I / 128 + nt) : nt * (NW / 2) + h;
+        sWs[h][kb] = wsb[(size_t)rb * KB + kb];
+      }
+      __syncthreads();
+    };
+    if (!direct) fill_tables();
 
     // Load sources. Weight load i of wave w: rows [8i, 8i + 8) of the wave's 64
     // (16-row column tile j = i / 2), lane l -> row 8 (i & 1) + l / 8 of the
@@ -230,7 +240,10 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
       const int q = wave * NA + a;
       const int r = q * 8 + (lane >> 3);
       long src = 0;
-      if (q < AQ && sSrc[r] >= 0) src = sSrc[r];
+      if (q < AQ) {
+        const long sr = direct ? direct_src(r) : sSrc[r];
+        if (sr >= 0) src = sr;
+      }
       aslot[a] = q < AQ ? q : AQ;
       aptr[a] = p.a + (size_t)src * Kdim + swz(r, lane & 7) * 16;
     }
@@ -238,7 +251,10 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
     long ssrc = 0;
     {
       const int r = wave * 64 + lane;
-      if (wave < NSQ && r < MT && sSrc[r] >= 0) ssrc = sSrc[r];
+      if (wave < NSQ && r < MT) {
+        const long sr = direct ? direct_src(r) : sSrc[r];
+        if (sr >= 0) ssrc = sr;
+      }
     }
     const float* asp = p.as + (size_t)ssrc * KB;
     const int sslot = wave < NSQ ? wave : NSQ;
@@ -306,6 +322,10 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_kernel(GemmArgs p) {
     issue(st0, 0);
     if (PD >= 3) issue(st1, min(1, KB - 1));
     if (PD >= 4) issue(st2, min(2, KB - 1));
+    // direct: the scale loads follow the stages, and the wait for them before their
+    // LDS stores (the compiler's, which counts only its own loads: vmcnt 0) covers the
+    // first stages as well, so the first step's wait stays exact
+    if (direct) fill_tables();
     for (int kb = 0; kb < KB; kb += PD) {
       if (PD == 2) {
         step(kb, st0, st1);
@@ -462,14 +482,15 @@ using namespace moe;
 #define MOE_CHECK_ALIGN16(ptr) \
   MOE_CHECK_ARG(((uintptr_t)(ptr)&15) == 0, "%s must be 16-byte aligned", #ptr)
 
-extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
-                                  const uint8_t* w13, const float* w13_scale,
-                                  const float* w13_channel_scale, const uint8_t* w13_shared,
-                                  const float* w13_shared_scale,
-                                  const float* w13_shared_channel_scale, int n_shared,
-                                  const int32_t* token_position_to_id, int NB,
-                                  const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
-                                  int mt, uint8_t* hq, float* hs, void* stream) {
+// moe_expert_gate_up; tok0: every slot of a tile holds token 0 (T = 1 and tiles from
+// the layer's own mapping), so the kernel loads no token ids.
+static int gate_up_entry(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
+                         const uint8_t* w13, const float* w13_scale, const float* w13_channel_scale,
+                         const uint8_t* w13_shared, const float* w13_shared_scale,
+                         const float* w13_shared_channel_scale, int n_shared,
+                         const int32_t* token_position_to_id, int NB, const int32_t* tiles,
+                         const int32_t* num_tiles, int max_tiles, int mt, uint8_t* hq, float* hs,
+                         void* stream, int tok0) {
   MOE_API_BEGIN("moe_expert_gate_up");
   MOE_CHECK_ARG(xq && xs && w13 && w13_scale && token_position_to_id && tiles && num_tiles && hq && hs,
                 "null pointer argument");
@@ -504,9 +525,32 @@ extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int
   a.E = E;
   a.nsh = n_shared;
   a.NB = NB;
+  a.tok0 = (tok0 != 0 && T == 1) ? 1 : 0;
   if (launch_gemm<0>(a, max_tiles, mt, (hipStream_t)stream) != MOE_OK)
     MOE_CHECK_ARG(false, "bad mt %d", mt);
   MOE_API_END();
+}
+
+extern "C" int moe_expert_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
+                                  const uint8_t* w13, const float* w13_scale,
+                                  const float* w13_channel_scale, const uint8_t* w13_shared,
+                                  const float* w13_shared_scale,
+                                  const float* w13_shared_channel_scale, int n_shared,
+                                  const int32_t* token_position_to_id, int NB,
+                                  const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                                  int mt, uint8_t* hq, float* hs, void* stream) {
+  return gate_up_entry(xq, xs, T, H, I, E, w13, w13_scale, w13_channel_scale, w13_shared,
+                       w13_shared_scale, w13_shared_channel_scale, n_shared, token_position_to_id, NB,
+                       tiles, num_tiles, max_tiles, mt, hq, hs, stream, 0);
+}
+
+int moe::layer_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E,
+                       const uint8_t* w13, const float* w13_scale, const uint8_t* w13_shared,
+                       const float* w13_shared_scale, int n_shared, const int32_t* tpid, int NB,
+                       const int32_t* tiles, const int32_t* num_tiles, int max_tiles, int mt,
+                       uint8_t* hq, float* hs, void* stream) {
+  return gate_up_entry(xq, xs, T, H, I, E, w13, w13_scale, nullptr, w13_shared, w13_shared_scale,
+                       nullptr, n_shared, tpid, NB, tiles, num_tiles, max_tiles, mt, hq, hs, stream, 1);
 }
 
 extern "C" int moe_expert_down(const uint8_t* hq, const float* hs, int T, int H, int I, int E,

@@ -112,6 +112,14 @@ int router_logits_topk(const void* x_bf16, const void* w_bf16, const float* bias
                        int topk_group, int renorm, float renorm_eps, float routed_scale,
                        int32_t* ids, float* weights, void* stream, RouterFuse* fuse = nullptr);
 
+// moe_expert_gate_up for the layer, whose tiles its own mapping wrote: at one token
+// every slot of a tile holds token 0, and the kernel loads no token ids.
+int layer_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E, const uint8_t* w13,
+                  const float* w13_scale, const uint8_t* w13_shared, const float* w13_shared_scale,
+                  int n_shared, const int32_t* tpid, int NB, const int32_t* tiles,
+                  const int32_t* num_tiles, int max_tiles, int mt, uint8_t* hq, float* hs,
+                  void* stream);
+
 // moe_blockwise_mapping plus an optional tile list (same checks and errors).
 int blockwise_mapping(const int32_t* ids, const float* affinities, const uint8_t* padding_mask,
                       int T, int K, int E, int B, int N, int32_t* token_position_to_id,
