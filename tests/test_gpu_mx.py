@@ -256,6 +256,23 @@ def test_gpt_oss_120b_layer(cuda, gpt_oss_weights, T, tokens):
     assert np.all(got[:, c["h_real"]:] == 0)  # padded hidden columns stay zero
 
 
+@pytest.mark.parametrize("seed,act,limited", [(1, "swish", True), (2, "swish", True), (3, "silu", False)])
+def test_gpt_oss_one_token_layer_equals_op_path(cuda, gpt_oss_weights, seed, act, limited):
+    """At one token the layer's MX GEMMs (K = 3072) keep each wave's weight fragments for
+    the whole K in registers, loaded in one memory round trip; the op-by-op path runs the
+    ring kernels through the public entry points. Same scaled MFMAs in the same K order
+    and the same epilogue, so the layer's output is the same bits, with and without the
+    clamps."""
+    c = GPT_OSS
+    w = gpt_oss_weights
+    say("gpt-oss one token vs op path", seed, act, limited)
+    gl, ul = ((None, LIMIT), (1 - LIMIT, 1 + LIMIT)) if limited else ((None, None), (None, None))
+    x = _padded_hidden(1, 500 + seed, cuda)
+    out, ids, wts, lg = ops.layer_forward_mx(x, w, c["K"], act, gl, ul, return_routing=True)
+    ref = ops.mx_experts(x, ids, wts, w, act, gl, ul)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 @pytest.mark.parametrize("T,with_res", [(1, True), (1, False), (4, True), (5, True)])
 def test_gpt_oss_norm_rides_in_router_launch(cuda, gpt_oss_weights, T, with_res):
     """Up to four tokens the GPT-OSS layer's RMSNorm (and residual add) runs inside the

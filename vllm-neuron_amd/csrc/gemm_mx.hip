@@ -57,6 +57,8 @@ struct MxArgs {
   long NB;
   int act;  // 0 SiLU, 1 Swish (g * sigmoid(1.702 g))
   float gate_lo, gate_hi, up_lo, up_hi;
+  // the layer at one token (tiles from its own mapping: one row each, token 0)
+  int one;
 };
 
 __device__ __forceinline__ v4f mfma_mx(const v8i& a, const v8i& b, const v4f& c, int sa, int sb,
@@ -641,11 +643,164 @@ __global__ void selftest_mfma_mx_kernel(const uint8_t* a, const uint8_t* sa, con
   for (int i = 0; i < 4; ++i) c[(4 * g + i) * 16 + r16] = d[i];
 }
 
+// ---------------------------------------------------------------------------
+// One-token MX GEMM for the layer (T = 1, MXFP4 weights, K = 128 KB): a work item is
+// one tile (one row) and 32 NW weight rows, one wave per 32 rows (gate_up: 16 gate rows
+// and the matching 16 up rows, so a pair of waves holds one 32-column MX block of h;
+// down: 32 output columns). Each wave owns two 16-row column tiles and loads all of
+// their MFMA fragments for the whole K into registers at once: 2 KB fragment loads and
+// KB / 2 scale loads per wave, all in flight (the counter holds 63), one memory round
+// trip where the ring kernel chains its stages. The token's row and its E8M0 bytes go
+// to LDS once. Every load is a plain load, so the compiler orders the waits and the
+// MFMAs start as the first fragments land. Same scaled MFMAs in the same K order and
+// the same epilogue arithmetic as expert_gemm_mx_kernel (the MX block maximum of h
+// combines the pair of waves that hold its 32 columns), so the outputs are the same
+// bits.
+// ---------------------------------------------------------------------------
+template <int KIND, int KB, int NW>
+__global__ __launch_bounds__(64 * NW) void expert_gemm_mx_one_kernel(MxArgs p) {
+  static_assert(KB % 4 == 0 && 2 * KB + KB / 2 <= 60, "fragment and scale loads in flight per wave");
+  static_assert(KIND == 1 || NW % 2 == 0, "gate_up: whole MX blocks of h per workgroup");
+  constexpr int K = 128 * KB;
+  constexpr int NA = (K / 16 + 64 * NW - 1) / (64 * NW);  // 16-byte pieces of the row per thread
+  __shared__ __attribute__((aligned(16))) uint8_t sA[K];       // the row's MXFP8 codes
+  __shared__ __attribute__((aligned(16))) uint8_t sAS[K / 32];  // its E8M0 bytes
+  __shared__ float sMax[NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r16 = lane & 15;
+  const int NT = (KIND == 0) ? p.I / (16 * NW) : p.H / (32 * NW);
+  const int tile = blockIdx.x / NT, nt = blockIdx.x - tile * NT;
+  if (tile >= p.num_tiles[0]) return;  // whole workgroup
+  const int4 td = p.tiles[tile];
+  const int e = td.x;
+  if (e < 0 || e >= p.E + p.nsh) return;  // whole workgroup: malformed tile
+  const bool is_sh = e >= p.E;
+  const int ej = is_sh ? e - p.E : e;
+  const long row0 = td.w;  // the tile's hq / y row
+  const int rows_w = (KIND == 0) ? 2 * p.I : p.H;
+  // weight rows of the wave's column tiles: gate_up, gate row c and up row I + c of
+  // h column c = 16 (NW nt + wave) + r16; down, output columns 32 (NW nt + wave) + 16 t + r16
+  const int col0 = (KIND == 0) ? 16 * (NW * nt + wave) : 32 * (NW * nt + wave);
+  int wr[2];
+  if (KIND == 0) {
+    wr[0] = col0 + r16;
+    wr[1] = p.I + wr[0];
+  } else {
+    wr[0] = col0 + r16;
+    wr[1] = wr[0] + 16;
+  }
+  const uint8_t* wb = (is_sh ? p.wsh : p.w) + (size_t)ej * rows_w * (K / 2);
+  const uint8_t* wsb = (is_sh ? p.wssh : p.ws) + (size_t)ej * rows_w * (K / 32);
+  const float* bb = is_sh ? p.bsh : p.bias;
+  // the token's row (gate_up: token 0 of x; down: the tile's h row) and its scales
+  const long a_row = (KIND == 0) ? 0 : row0;
+  const uint8_t* ap = p.a + (size_t)a_row * K;
+  const uint8_t* asp = p.as + (size_t)a_row * (K / 32);
+  int4 av[NA], asv = make_int4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int c = tid + i * 64 * NW;
+    av[i] = (c < K / 16) ? *(const int4*)(ap + c * 16) : make_int4(0, 0, 0, 0);
+  }
+  if (tid < K / 512) asv = *(const int4*)(asp + tid * 16);
+  // weight scales first (K blocks 4q .. 4q + 3 of the row in piece q), then the
+  // fragments in K order: the first MFMAs wait only for the first loads
+  int4 ws4[2][KB / 4];
+#pragma unroll
+  for (int q = 0; q < KB / 4; ++q)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) ws4[t][q] = *(const int4*)(wsb + (size_t)wr[t] * (K / 32) + q * 16);
+  int4 wf[KB][2];  // fp4 fragment: row wr[t], K values [128 kb + 32 g, +32)
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) wf[kb][t] = *(const int4*)(wb + (size_t)wr[t] * (K / 2) + kb * 64 + g * 16);
+  float bia[2] = {0.f, 0.f};
+  if (bb != nullptr) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) bia[t] = bb[(size_t)ej * rows_w + wr[t]];
+  }
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int c = tid + i * 64 * NW;
+    if (c < K / 16) *(int4*)(sA + c * 16) = av[i];
+  }
+  if (tid < K / 512) *(int4*)(sAS + tid * 16) = asv;
+  __syncthreads();
+
+  // A operand: row 0 of the MFMA is the token (lanes r16 == 0), the other rows zero
+  v4f acc[2] = {(v4f){0.f, 0.f, 0.f, 0.f}, (v4f){0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int4 lo = *(const int4*)(sA + kb * 128 + 16 * g);
+    const int4 hi = *(const int4*)(sA + kb * 128 + 64 + 16 * g);
+    const uint32_t sad = *(const uint32_t*)(sAS + kb * 4);
+    const bool tok = r16 == 0;
+    const v8i a = tok ? (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w} : (v8i){0, 0, 0, 0, 0, 0, 0, 0};
+    const int sa = tok ? (int)(sad >> (8 * g)) : 127;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int4 w4 = ws4[t][kb >> 2];
+      const int q = kb & 3;  // compile-time after unrolling
+      const uint32_t sw = (uint32_t)(q == 0 ? w4.x : q == 1 ? w4.y : q == 2 ? w4.z : w4.w);
+      const v8i b = (v8i){wf[kb][t].x, wf[kb][t].y, wf[kb][t].z, wf[kb][t].w, 0, 0, 0, 0};
+      acc[t] = mfma_mx(a, b, acc[t], sa, (int)(sw >> (8 * g)), std::integral_constant<int, kFmtFp4>{});
+    }
+  }
+
+  // The MFMA reads the operands of all 64 lanes whatever EXEC holds, and the compiler
+  // does not treat it as convergent: with the results used only by lanes 0..15 it
+  // would move the whole K loop into the branch below, where the operand set-up (the
+  // zeroed rows, the scale bytes) runs on those lanes alone and the other lanes feed
+  // the MFMAs stale registers. The empty asm takes the accumulators on every lane
+  // here, ahead of any branch.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(acc[t]));
+
+  // Epilogue: the token's outputs are register 0 of lanes 0..15 (row 0 of the tile,
+  // weight row r16 of each column tile).
+  if (KIND == 0) {
+    float h = 0.f;
+    if (g == 0) {
+      const float gt = fminf(fmaxf(acc[0][0] + bia[0], p.gate_lo), p.gate_hi);
+      const float up = fminf(fmaxf(acc[1][0] + bia[1], p.up_lo), p.up_hi);
+      h = mx_act(gt, p.act) * up;
+    }
+    // the MX block of h columns [32 b, +32) is waves 2 b and 2 b + 1 (mod NW)
+    const float m = group16_max_f32(fabsf(h));
+    if (lane == 0) sMax[wave] = m;
+    __syncthreads();
+    const int ex = mx_exponent(fmaxf(sMax[wave], sMax[wave ^ 1]));
+    if (g == 0) {
+      const uint32_t c2 = mx_e4m3x2(h, 0.f, mx_inv_scale(ex));
+      p.hq[(size_t)row0 * p.I + col0 + r16] = (uint8_t)c2;
+      if (r16 == 0 && (wave & 1) == 0) p.hs[(size_t)row0 * (p.I / 32) + col0 / 32] = (uint8_t)(ex + 127);
+    }
+  } else if (g == 0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      p.y[(size_t)row0 * p.H + wr[t]] = (uint16_t)bf16x2(acc[t][0] + bia[t], 0.f);
+  }
+}
+
 template <int KIND, int WFMT>
 static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
-  // one persistent workgroup per CU (the ring's LDS allows one), each running
-  // every G-th work item; 16-row tiles whose 2-wave half-width items still fit one
-  // per CU (one token) run those instead, twice as many workgroups
+  // The layer at one token with MXFP4 weights and K = 3072: the register kernel, one
+  // workgroup per work item. Gate_up items are two MX blocks of h (196 KB of weight
+  // rows), down items 64 output columns (98 KB): the time follows the bytes of the
+  // busiest CU, and smaller items (more than one per CU) measured no faster.
+  const int Kone = (KIND == 0) ? a.H : a.I;
+  constexpr int NW1 = (KIND == 0) ? 4 : 2;
+  if (a.one && a.T == 1 && WFMT == kFmtFp4 && mt == 16 && Kone == 128 * 24 && a.I % (16 * NW1) == 0 &&
+      a.H % (32 * NW1) == 0) {
+    const long items = (long)max_tiles * ((KIND == 0) ? a.I / (16 * NW1) : a.H / (32 * NW1));
+    hipLaunchKernelGGL((expert_gemm_mx_one_kernel<KIND, 24, NW1>), dim3((unsigned)items), dim3(64 * NW1),
+                       0, st, a);
+    return MOE_OK;
+  }
+  // otherwise the ring kernel: one persistent workgroup per CU (the ring's LDS allows
+  // one), each running every G-th work item; 16-row tiles whose 2-wave half-width
+  // items still fit one per CU (one token) run those instead, twice as many workgroups
   const int cus = device_cu_count();
   const int nt4 = (KIND == 0) ? a.I / 128 : a.H / 256;
   const bool half = mt == 16 && 2L * max_tiles * nt4 <= cus;
@@ -726,14 +881,14 @@ extern "C" int moe_act_quant_mx(const void* x_bf16, int rows, int cols, uint8_t*
   MOE_API_END();
 }
 
-extern "C" int moe_expert_gate_up_mx(const uint8_t* xq, const uint8_t* xs, int T, int H, int I, int E,
-                                     int wfmt, const uint8_t* w13, const uint8_t* w13_scale,
-                                     const float* b13, const uint8_t* w13_shared,
-                                     const uint8_t* w13_shared_scale, const float* b13_shared,
-                                     int n_shared, const int32_t* token_position_to_id, int NB,
-                                     const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
-                                     int mt, int act, float gate_lo, float gate_hi, float up_lo,
-                                     float up_hi, uint8_t* hq, uint8_t* hs, void* stream) {
+static int moe_expert_gate_up_mx_impl(const uint8_t* xq, const uint8_t* xs, int T, int H, int I, int E,
+                                      int wfmt, const uint8_t* w13, const uint8_t* w13_scale,
+                                      const float* b13, const uint8_t* w13_shared,
+                                      const uint8_t* w13_shared_scale, const float* b13_shared,
+                                      int n_shared, const int32_t* token_position_to_id, int NB,
+                                      const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                                      int mt, int act, float gate_lo, float gate_hi, float up_lo,
+                                      float up_hi, uint8_t* hq, uint8_t* hs, void* stream, int one) {
   MOE_API_BEGIN("moe_expert_gate_up_mx");
   MOE_CHECK_ARG(xq && xs && w13 && w13_scale && token_position_to_id && tiles && num_tiles && hq && hs,
                 "null pointer argument");
@@ -769,19 +924,48 @@ extern "C" int moe_expert_gate_up_mx(const uint8_t* xq, const uint8_t* xs, int T
   a.gate_hi = lim(gate_hi, INFINITY);
   a.up_lo = lim(up_lo, -INFINITY);
   a.up_hi = lim(up_hi, INFINITY);
+  a.one = one;
   rc = (wfmt == MOE_MX_FP4) ? launch_mx<0, kFmtFp4>(a, max_tiles, mt, (hipStream_t)stream)
                             : launch_mx<0, kFmtFp8>(a, max_tiles, mt, (hipStream_t)stream);
   MOE_CHECK_ARG(rc == MOE_OK, "bad mt %d", mt);
   MOE_API_END();
 }
 
-extern "C" int moe_expert_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E,
-                                  int wfmt, const uint8_t* w2, const uint8_t* w2_scale,
-                                  const float* b2, const uint8_t* w2_shared,
-                                  const uint8_t* w2_shared_scale, const float* b2_shared,
-                                  int n_shared, int NB, const int32_t* tiles,
-                                  const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
-                                  void* stream) {
+extern "C" int moe_expert_gate_up_mx(const uint8_t* xq, const uint8_t* xs, int T, int H, int I, int E,
+                                     int wfmt, const uint8_t* w13, const uint8_t* w13_scale,
+                                     const float* b13, const uint8_t* w13_shared,
+                                     const uint8_t* w13_shared_scale, const float* b13_shared,
+                                     int n_shared, const int32_t* token_position_to_id, int NB,
+                                     const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                                     int mt, int act, float gate_lo, float gate_hi, float up_lo,
+                                     float up_hi, uint8_t* hq, uint8_t* hs, void* stream) {
+  return moe_expert_gate_up_mx_impl(xq, xs, T, H, I, E, wfmt, w13, w13_scale, b13, w13_shared,
+                                    w13_shared_scale, b13_shared, n_shared, token_position_to_id,
+                                    NB, tiles, num_tiles, max_tiles, mt, act, gate_lo, gate_hi,
+                                    up_lo, up_hi, hq, hs, stream, 0);
+}
+
+int moe::layer_gate_up_mx(const uint8_t* xq, const uint8_t* xs, int T, int H, int I, int E,
+                          int wfmt, const uint8_t* w13, const uint8_t* w13_scale,
+                          const float* b13, const uint8_t* w13_shared,
+                          const uint8_t* w13_shared_scale, const float* b13_shared,
+                          int n_shared, const int32_t* token_position_to_id, int NB,
+                          const int32_t* tiles, const int32_t* num_tiles, int max_tiles,
+                          int mt, int act, float gate_lo, float gate_hi, float up_lo,
+                          float up_hi, uint8_t* hq, uint8_t* hs, void* stream) {
+  return moe_expert_gate_up_mx_impl(xq, xs, T, H, I, E, wfmt, w13, w13_scale, b13, w13_shared,
+                                    w13_shared_scale, b13_shared, n_shared, token_position_to_id,
+                                    NB, tiles, num_tiles, max_tiles, mt, act, gate_lo, gate_hi,
+                                    up_lo, up_hi, hq, hs, stream, T == 1);
+}
+
+static int moe_expert_down_mx_impl(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E,
+                                   int wfmt, const uint8_t* w2, const uint8_t* w2_scale,
+                                   const float* b2, const uint8_t* w2_shared,
+                                   const uint8_t* w2_shared_scale, const float* b2_shared,
+                                   int n_shared, int NB, const int32_t* tiles,
+                                   const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
+                                   void* stream, int one) {
   MOE_API_BEGIN("moe_expert_down_mx");
   MOE_CHECK_ARG(hq && hs && w2 && w2_scale && tiles && num_tiles && y_bf16, "null pointer argument");
   int rc = mx_common_checks(_moe_fn, T, H, I, E, NB, max_tiles, mt, wfmt, n_shared);
@@ -808,10 +992,35 @@ extern "C" int moe_expert_down_mx(const uint8_t* hq, const uint8_t* hs, int T, i
   a.E = E;
   a.nsh = n_shared;
   a.NB = NB;
+  a.one = one;
   rc = (wfmt == MOE_MX_FP4) ? launch_mx<1, kFmtFp4>(a, max_tiles, mt, (hipStream_t)stream)
                             : launch_mx<1, kFmtFp8>(a, max_tiles, mt, (hipStream_t)stream);
   MOE_CHECK_ARG(rc == MOE_OK, "bad mt %d", mt);
   MOE_API_END();
+}
+
+extern "C" int moe_expert_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E,
+                                  int wfmt, const uint8_t* w2, const uint8_t* w2_scale,
+                                  const float* b2, const uint8_t* w2_shared,
+                                  const uint8_t* w2_shared_scale, const float* b2_shared,
+                                  int n_shared, int NB, const int32_t* tiles,
+                                  const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
+                                  void* stream) {
+  return moe_expert_down_mx_impl(hq, hs, T, H, I, E, wfmt, w2, w2_scale, b2, w2_shared,
+                                 w2_shared_scale, b2_shared, n_shared, NB, tiles, num_tiles,
+                                 max_tiles, mt, y_bf16, stream, 0);
+}
+
+int moe::layer_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E,
+                       int wfmt, const uint8_t* w2, const uint8_t* w2_scale,
+                       const float* b2, const uint8_t* w2_shared,
+                       const uint8_t* w2_shared_scale, const float* b2_shared,
+                       int n_shared, int NB, const int32_t* tiles,
+                       const int32_t* num_tiles, int max_tiles, int mt, void* y_bf16,
+                       void* stream) {
+  return moe_expert_down_mx_impl(hq, hs, T, H, I, E, wfmt, w2, w2_scale, b2, w2_shared,
+                                 w2_shared_scale, b2_shared, n_shared, NB, tiles, num_tiles,
+                                 max_tiles, mt, y_bf16, stream, T == 1);
 }
 
 extern "C" int moe_selftest_mfma_mx(const uint8_t* a, const uint8_t* sa, const uint8_t* b,

@@ -120,6 +120,22 @@ int layer_gate_up(const uint8_t* xq, const float* xs, int T, int H, int I, int E
                   const int32_t* num_tiles, int max_tiles, int mt, uint8_t* hq, float* hs,
                   void* stream);
 
+// moe_expert_gate_up_mx / moe_expert_down_mx for the layer, whose tiles its own
+// mapping wrote: at one token (one row per tile, token 0) the MXFP4 GEMMs with K =
+// 3072 load each wave's fragments for the whole K into registers at once.
+int layer_gate_up_mx(const uint8_t* xq, const uint8_t* xs, int T, int H, int I, int E, int wfmt,
+                     const uint8_t* w13, const uint8_t* w13_scale, const float* b13,
+                     const uint8_t* w13_shared, const uint8_t* w13_shared_scale,
+                     const float* b13_shared, int n_shared, const int32_t* token_position_to_id,
+                     int NB, const int32_t* tiles, const int32_t* num_tiles, int max_tiles, int mt,
+                     int act, float gate_lo, float gate_hi, float up_lo, float up_hi, uint8_t* hq,
+                     uint8_t* hs, void* stream);
+int layer_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E, int wfmt,
+                  const uint8_t* w2, const uint8_t* w2_scale, const float* b2,
+                  const uint8_t* w2_shared, const uint8_t* w2_shared_scale, const float* b2_shared,
+                  int n_shared, int NB, const int32_t* tiles, const int32_t* num_tiles,
+                  int max_tiles, int mt, void* y_bf16, void* stream);
+
 // moe_blockwise_mapping plus an optional tile list (same checks and errors).
 int blockwise_mapping(const int32_t* ids, const float* affinities, const uint8_t* padding_mask,
                       int T, int K, int E, int B, int N, int32_t* token_position_to_id,
