@@ -259,9 +259,10 @@ def test_gpt_oss_120b_layer(cuda, gpt_oss_weights, T, tokens):
 @pytest.mark.parametrize("seed,act,limited", [(1, "swish", True), (2, "swish", True), (3, "silu", False)])
 def test_gpt_oss_one_token_layer_equals_op_path(cuda, gpt_oss_weights, seed, act, limited):
     """At one token the layer's MX GEMMs (K = 3072) keep each wave's weight fragments for
-    the whole K in registers, loaded in one memory round trip; the op-by-op path runs the
-    ring kernels through the public entry points. Same scaled MFMAs in the same K order
-    and the same epilogue, so the layer's output is the same bits, with and without the
+    the whole K in registers, loaded in one memory round trip, and down and the combine
+    run as one launch; the op-by-op path runs the ring kernels and moe_combine through
+    the public entry points. Same scaled MFMAs in the same K order, the same epilogues
+    and the same pair sum, so the layer's output is the same bits, with and without the
     clamps."""
     c = GPT_OSS
     w = gpt_oss_weights
@@ -271,6 +272,29 @@ def test_gpt_oss_one_token_layer_equals_op_path(cuda, gpt_oss_weights, seed, act
     out, ids, wts, lg = ops.layer_forward_mx(x, w, c["K"], act, gl, ul, return_routing=True)
     ref = ops.mx_experts(x, ids, wts, w, act, gl, ul)
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_gpt_oss_one_token_pairs_without_rows(cuda, gpt_oss_weights):
+    """A token with fewer finite router logits than top-k (a NaN router bias on all but
+    three experts) has pairs with no row (-1 ids): in the one-token down-and-combine
+    launch they add nothing, as in moe_combine, so the output equals the op path bit
+    for bit and stays finite."""
+    import dataclasses
+    c = GPT_OSS
+    w = gpt_oss_weights
+    say("gpt-oss one token, three candidates")
+    keep = [5, 77, 120]
+    bias = torch.full((c["E"],), float("nan"), device=cuda)
+    bias[keep] = w.router_bias[keep] if w.router_bias is not None else 0.0
+    w3 = dataclasses.replace(w, router_bias=bias)
+    gl, ul = (None, LIMIT), (1 - LIMIT, 1 + LIMIT)
+    x = _padded_hidden(1, 900, cuda)
+    out, ids, wts, lg = ops.layer_forward_mx(x, w3, c["K"], "swish", gl, ul, return_routing=True)
+    assert sorted(i for i in ids[0].tolist() if i >= 0) == keep
+    assert int((ids[0] < 0).sum()) == c["K"] - 3
+    ref = ops.mx_experts(x, ids, wts, w3, "swish", gl, ul)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert bool(torch.isfinite(out.float()).all())
 
 
 @pytest.mark.parametrize("T,with_res", [(1, True), (1, False), (4, True), (5, True)])

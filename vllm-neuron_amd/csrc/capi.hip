@@ -437,9 +437,14 @@ extern "C" int moe_layer_forward_mx(
   MOE_STEP(layer_gate_up_mx(w.xq, xs, T, H, I, E, wfmt, w13, w13_scale, b13, nullptr, nullptr,
                             nullptr, 0, w.tpid, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, act,
                             gate_lo, gate_hi, up_lo, up_hi, w.hq, hs, stream));
-  MOE_STEP(layer_down_mx(w.hq, hs, T, H, I, E, wfmt, w2, w2_scale, b2, nullptr, nullptr, nullptr,
-                         0, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y, stream));
-  MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)R, 0, out_bf16, stream));
+  bool fused = false;
+  MOE_STEP(layer_down_combine_mx(w.hq, hs, T, H, I, E, K, wfmt, w2, w2_scale, b2, ids, w.inv, wts,
+                                 out_bf16, stream, &fused));
+  if (!fused) {
+    MOE_STEP(layer_down_mx(w.hq, hs, T, H, I, E, wfmt, w2, w2_scale, b2, nullptr, nullptr, nullptr,
+                           0, (int)NB, w.tiles, w.num_tiles, max_tiles, mt, w.y, stream));
+    MOE_STEP(moe_combine(w.y, w.inv, wts, K, T, H, (int)R, 0, out_bf16, stream));
+  }
 #undef MOE_STEP
   return MOE_OK;
 }

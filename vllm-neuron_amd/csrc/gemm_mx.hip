@@ -783,6 +783,98 @@ __global__ __launch_bounds__(64 * NW) void expert_gemm_mx_one_kernel(MxArgs p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Down and combine in one launch for the layer at one token (MXFP4 w2, I = 128 KB,
+// no shared experts): out = bf16(sum over the token's live pairs k, in pair order, of
+// w_k * bf16(h_k W2[e_k]^T + b2[e_k])), the sum moe_combine takes over the y rows the
+// down GEMM writes. A workgroup owns 16 output columns and runs one wave per pair
+// (K <= 8): wave k loads pair k's h row (the row inv[k] of hq) and its E8M0 bytes into
+// LDS, and its expert's 16 weight rows for the whole K into registers (24 fragment
+// and 6 scale loads), as expert_gemm_mx_one_kernel does; the MFMAs and the y rounding
+// are the down kernel's, the pair sum (fused multiply-adds from zero, live pairs in
+// order) the combine kernel's, so the output is the same bits without the y rows or
+// the combine launch. Pairs with no row (inv < 0) add nothing, as in the combine.
+// ---------------------------------------------------------------------------
+constexpr int kDownCombineMaxK = 8;
+
+template <int KB>
+__global__ __launch_bounds__(64 * kDownCombineMaxK) void down_combine_mx_one_kernel(
+    const uint8_t* __restrict__ hq, const uint8_t* __restrict__ hs, const uint8_t* __restrict__ w2,
+    const uint8_t* __restrict__ w2s, const float* __restrict__ b2, const int32_t* __restrict__ ids,
+    const int32_t* __restrict__ inv, const float* __restrict__ wts, int H, int E, int K,
+    uint16_t* __restrict__ out) {
+  static_assert(KB % 4 == 0, "scale pieces of four K blocks");
+  constexpr int K_ = 128 * KB;
+  __shared__ __attribute__((aligned(16))) uint8_t sA[kDownCombineMaxK][K_];
+  __shared__ __attribute__((aligned(16))) uint8_t sAS[kDownCombineMaxK][K_ / 32];
+  __shared__ float sY[kDownCombineMaxK][16];
+  __shared__ float sW[kDownCombineMaxK];  // the pair's weight, 0 for a pair with no row
+  const int tid = threadIdx.x, lane = tid & 63, k = tid >> 6;  // wave k: pair k
+  const int g = lane >> 4, r16 = lane & 15;
+  const int col = blockIdx.x * 16 + r16;  // output column of lane r16
+  // the pair's compact row and expert, the same on every lane of the wave
+  const int row = __builtin_amdgcn_readfirstlane(inv[k]);
+  const int e = __builtin_amdgcn_readfirstlane(ids[k]);
+  const bool live = row >= 0 && e >= 0 && e < E;
+  int4 av[(K_ / 16 + 63) / 64], asv = make_int4(0, 0, 0, 0);
+  int4 ws4[KB / 4];
+  int4 wf[KB];
+  float bia = 0.f;
+  if (live) {
+    const uint8_t* ap = hq + (size_t)row * K_;
+#pragma unroll
+    for (int i = 0; i < (K_ / 16 + 63) / 64; ++i) {
+      const int c = lane + 64 * i;
+      av[i] = (c < K_ / 16) ? *(const int4*)(ap + c * 16) : make_int4(0, 0, 0, 0);
+    }
+    if (lane < K_ / 512) asv = *(const int4*)(hs + (size_t)row * (K_ / 32) + lane * 16);
+    const uint8_t* wsb = w2s + ((size_t)e * H + col) * (K_ / 32);
+#pragma unroll
+    for (int q = 0; q < KB / 4; ++q) ws4[q] = *(const int4*)(wsb + q * 16);
+    const uint8_t* wb = w2 + ((size_t)e * H + col) * (K_ / 2) + g * 16;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) wf[kb] = *(const int4*)(wb + kb * 64);
+    if (b2 != nullptr) bia = b2[(size_t)e * H + col];
+#pragma unroll
+    for (int i = 0; i < (K_ / 16 + 63) / 64; ++i) {
+      const int c = lane + 64 * i;
+      if (c < K_ / 16) *(int4*)(&sA[k][c * 16]) = av[i];
+    }
+    if (lane < K_ / 512) *(int4*)(&sAS[k][lane * 16]) = asv;
+  }
+  __syncthreads();
+  v4f acc = (v4f){0.f, 0.f, 0.f, 0.f};
+  float y = 0.f;  // bf16-rounded y of column col for pair k (0 without a row)
+  if (live) {
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int4 lo = *(const int4*)(&sA[k][kb * 128 + 16 * g]);
+      const int4 hi = *(const int4*)(&sA[k][kb * 128 + 64 + 16 * g]);
+      const uint32_t sad = *(const uint32_t*)(&sAS[k][kb * 4]);
+      const bool tok = r16 == 0;
+      const v8i a = tok ? (v8i){lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w} : (v8i){0, 0, 0, 0, 0, 0, 0, 0};
+      const int sa = tok ? (int)(sad >> (8 * g)) : 127;
+      const int4 w4 = ws4[kb >> 2];
+      const int q = kb & 3;
+      const uint32_t sw = (uint32_t)(q == 0 ? w4.x : q == 1 ? w4.y : q == 2 ? w4.z : w4.w);
+      const v8i b = (v8i){wf[kb].x, wf[kb].y, wf[kb].z, wf[kb].w, 0, 0, 0, 0};
+      acc = mfma_mx(a, b, acc, sa, (int)(sw >> (8 * g)), std::integral_constant<int, kFmtFp4>{});
+    }
+    // the MFMAs read every lane: keep them out of the lanes-0..15 branch below
+    asm volatile("" : "+v"(acc));
+    y = bf16_bits_to_f32((uint16_t)bf16x2(acc[0] + bia, 0.f));
+  }
+  if (g == 0) sY[k][r16] = y;
+  if (lane == 0) sW[k] = (row >= 0) ? wts[k] : 0.f;
+  __syncthreads();
+  if (k == 0 && g == 0) {
+    float o = 0.f;
+    for (int j = 0; j < K; ++j)
+      if (inv[j] >= 0) o = __builtin_fmaf(sW[j], sY[j][r16], o);  // the combine's live pairs, in order
+    out[col] = (uint16_t)bf16x2(o, 0.f);
+  }
+}
+
 template <int KIND, int WFMT>
 static int launch_mx(const MxArgs& a, int max_tiles, int mt, hipStream_t st) {
   // The layer at one token with MXFP4 weights and K = 3072: the register kernel, one
@@ -1009,6 +1101,25 @@ extern "C" int moe_expert_down_mx(const uint8_t* hq, const uint8_t* hs, int T, i
   return moe_expert_down_mx_impl(hq, hs, T, H, I, E, wfmt, w2, w2_scale, b2, w2_shared,
                                  w2_shared_scale, b2_shared, n_shared, NB, tiles, num_tiles,
                                  max_tiles, mt, y_bf16, stream, 0);
+}
+
+int moe::layer_down_combine_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E,
+                               int K, int wfmt, const uint8_t* w2, const uint8_t* w2_scale,
+                               const float* b2, const int32_t* ids, const int32_t* inv,
+                               const float* weights, void* out_bf16, void* stream, bool* done) {
+  MOE_API_BEGIN("moe_expert_down_mx");
+  *done = false;
+  if (T != 1 || wfmt != MOE_MX_FP4 || I != 128 * 24 || K < 1 || K > kDownCombineMaxK || H % 16 != 0 ||
+      ((uintptr_t)hq & 15) != 0 || ((uintptr_t)hs & 15) != 0 || ((uintptr_t)w2 & 15) != 0 ||
+      ((uintptr_t)w2_scale & 15) != 0)
+    return MOE_OK;  // not this form: the caller runs down and the combine
+  MOE_CHECK_ARG(hq && hs && w2 && w2_scale && ids && inv && weights && out_bf16 && E > 0,
+                "null pointer argument");
+  hipLaunchKernelGGL(down_combine_mx_one_kernel<24>, dim3((unsigned)(H / 16)), dim3(64 * K), 0,
+                     (hipStream_t)stream, hq, hs, w2, w2_scale, b2, ids, inv, weights, H, E, K,
+                     (uint16_t*)out_bf16);
+  *done = true;
+  MOE_API_END();
 }
 
 int moe::layer_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E,

@@ -136,6 +136,15 @@ int layer_down_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int
                   int n_shared, int NB, const int32_t* tiles, const int32_t* num_tiles,
                   int max_tiles, int mt, void* y_bf16, void* stream);
 
+// moe_expert_down_mx followed by moe_combine (no shared experts) in one launch for the
+// layer at one token with MXFP4 w2 and I = 3072 (K <= 8 pairs; ids, inv and weights of
+// the token's pairs, inv the compact rows of hq): the same output bits without the y
+// rows. *done says whether it ran; otherwise the caller runs both.
+int layer_down_combine_mx(const uint8_t* hq, const uint8_t* hs, int T, int H, int I, int E, int K,
+                          int wfmt, const uint8_t* w2, const uint8_t* w2_scale, const float* b2,
+                          const int32_t* ids, const int32_t* inv, const float* weights,
+                          void* out_bf16, void* stream, bool* done);
+
 // moe_blockwise_mapping plus an optional tile list (same checks and errors).
 int blockwise_mapping(const int32_t* ids, const float* affinities, const uint8_t* padding_mask,
                       int T, int K, int E, int B, int N, int32_t* token_position_to_id,
