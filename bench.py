@@ -165,16 +165,17 @@ def graph_ms(fn, reps, torch):
 
 
 def flushed_ms(fn, steps, torch):
-    """Device time per call of fn with the caches cold: before each call a 1 GiB fill
-    evicts the weights from L2 and the 256 MB MALL, then a short spin kernel lets the
-    host queue the call, which HIP events on the launch stream bracket. Median over
-    `steps` calls."""
-    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    """Device time per call of fn with the caches cold: before each call a read of
+    1 GiB evicts the weights from L2 and the 256 MB MALL (as the other layers' weights,
+    which a decode step reads in between, would; a read leaves no dirty lines whose
+    write-back would overlap the call), then a short spin kernel lets the host queue
+    the call, which HIP events on the launch stream bracket. Median over `steps` calls."""
+    buf = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
     fn()
     torch.cuda.synchronize()
     ev = []
     for i in range(steps):
-        buf.fill_(i & 0xFF)
+        buf.amax()
         torch.cuda._sleep(400_000)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
@@ -189,12 +190,20 @@ def flushed_ms(fn, steps, torch):
     return round(ts[len(ts) // 2], 4)
 
 
+def small_loop(T, steps):
+    """Calls per timed loop of an extra workload. Up to 64 tokens a call takes tens of
+    microseconds to about a millisecond, and the first launch after the synchronize
+    exposes the queue's whole latency: 100 calls or more, so that start is spread thin
+    (with 10 it added about a microsecond per one-token call)."""
+    return max(steps * 5, 100) if T <= 64 else max(steps // 2, 5)
+
+
 def workload_report(name, x, w, cfg, steps, torch, ops):
     """Whole-layer timing of one extra workload with its algorithmic roofline (and, up to
     64 tokens, the device time of the same call replayed from a HIP graph)."""
     T = x.shape[0]
     H, I, E = cfg.hidden, cfg.intermediate, cfg.n_experts
-    loop = max(steps // 2, 5)
+    loop = small_loop(T, steps)
     sec = time_layer(x, w, cfg, loop, 2, torch, ops, loops=3)
     gms = graph_ms(lambda: ops.layer_forward(x, w, cfg), max(steps, 20), torch) if T <= 64 else None
     fms = flushed_ms(lambda: ops.layer_forward(x, w, cfg), max(steps, 20), torch) if T <= 64 else None
@@ -271,7 +280,7 @@ def mx_report(name, layer, x, steps, torch):
     E, I, hr = w.n_experts, w.intermediate, layer.hidden_actual or H
     for _ in range(2):
         layer(x, None, True, None)
-    loop, runs = max(steps // 2, 5), []
+    loop, runs = small_loop(T, steps), []
     for _ in range(3):  # median of three timed loops
         torch.cuda.synchronize()
         t0 = time.perf_counter()

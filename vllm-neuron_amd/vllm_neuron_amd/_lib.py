@@ -120,5 +120,6 @@ def call(name, *args):
 
 
 def ptr(t):
-    """Device pointer of a tensor (or None for an absent optional argument)."""
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device pointer of a tensor (or None for an absent optional argument), as the
+    plain integer that the prototypes' c_void_p parameters take."""
+    return None if t is None else t.data_ptr()

@@ -19,7 +19,7 @@ BLOCK_TILES_HEADER = 16  # int32 header of a block-tile list (MOE_BLOCK_TILES_HE
 
 
 def _stream():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return torch.cuda.current_stream().cuda_stream
 
 
 def _need_cuda(*ts):
