@@ -648,9 +648,9 @@ __global__ void selftest_mfma_mx_kernel(const uint8_t* a, const uint8_t* sa, con
 // one tile (one row) and 32 NW weight rows, one wave per 32 rows (gate_up: 16 gate rows
 // and the matching 16 up rows, so a pair of waves holds one 32-column MX block of h;
 // down: 32 output columns). Each wave owns two 16-row column tiles and loads all of
-// their MFMA fragments for the whole K into registers at once: 2 KB fragment loads and
-// KB / 2 scale loads per wave, all in flight (the counter holds 63), one memory round
-// trip where the ring kernel chains its stages. The token's row and its E8M0 bytes go
+// their MFMA fragments for the whole K into registers at once: 2 x KB fragment loads
+// (16 bytes per lane each) and KB / 2 scale loads per wave, all in flight (the counter
+// holds 63), one memory round trip where the ring kernel chains its stages. The token's row and its E8M0 bytes go
 // to LDS once. Every load is a plain load, so the compiler orders the waits and the
 // MFMAs start as the first fragments land. Same scaled MFMAs in the same K order and
 // the same epilogue arithmetic as expert_gemm_mx_kernel (the MX block maximum of h
